@@ -1,0 +1,271 @@
+"""Pin the oracle's remaining functions against pure-Python brute force, closed forms and the
+reference's own known-answer cases (no transformers needed)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import metrics
+from oracle import attention, experts, mxfp4, packing, routing
+from oracle.numerics import bf16, bf16_bits_to_f32, f32_to_bf16_bits
+
+
+# ---- a1 packing -------------------------------------------------------------------------------
+
+def test_pack_ragged_brute_force():
+    rng = np.random.default_rng(0)
+    q = rng.integers(1, 9, size=13)
+    st = rng.integers(0, 500, size=13)
+    out = packing.pack_ragged(q, st, kv_base=np.arange(13) * 10_000, head_dim=64)
+    pos, sid, slot, cu = [], [], [], [0]
+    for b in range(13):
+        for i in range(q[b]):
+            pos.append(st[b] + i); sid.append(b); slot.append(b * 10_000 + (st[b] + i) * 64)
+        cu.append(cu[-1] + q[b])
+    assert out["positions"].tolist() == pos and out["seq_id"].tolist() == sid
+    assert out["kv_slot"].tolist() == slot and out["cu_seqlens"].tolist() == cu
+    assert out["kv_len"].tolist() == (st + q).tolist()
+
+
+def test_context_overflow_boundary():
+    """Boundary cases of the reference's KV bound (tests/test_kv_bound.py:17-24): writes
+    positions [start, start+q-1]; in bounds iff start + q <= capacity."""
+    packing.pack_ragged([8], [92], kv_cap=[100])                 # max index 99: exactly fits
+    packing.pack_ragged([100], [0], kv_cap=[100])
+    with pytest.raises(packing.ContextOverflow):
+        packing.pack_ragged([8], [93], kv_cap=[100])
+    with pytest.raises(packing.ContextOverflow):
+        packing.pack_ragged([1], [100], kv_cap=[100])
+
+
+@pytest.mark.parametrize("starts", [[0, 0, 0, 0], [17, 5, 900, 233], [2039, 1, 64, 2039]])
+def test_batched_mask_per_stream(starts):
+    """The per-stream mask cases of the reference's tests/test_graph_batch.py:38-55: row (b, qi)
+    allows col j iff j <= starts[b]+qi (and inside the window on sliding layers)."""
+    q = [9] * 4
+    for window in (0, 128):
+        m = packing.batched_mask(q, starts, 2048, window)
+        r = 0
+        for b in range(4):
+            for qi in range(9):
+                p = starts[b] + qi
+                for j in (0, max(0, p - 127) - 1, max(0, p - 127), p, p + 1, 2047):
+                    if 0 <= j < 2048:
+                        want = j <= p and (not window or p - j < window)
+                        assert m[r, j] == want
+                r += 1
+
+
+# ---- a2/a3/a4 routing --------------------------------------------------------------------------
+
+def _bf16_rand(rng, shape, std=1.0):
+    return bf16(torch.from_numpy(rng.standard_normal(shape).astype(np.float32) * std))
+
+
+def test_dot_fixed_matches_sequential_restatement():
+    rng = np.random.default_rng(1)
+    x = _bf16_rand(rng, (2, 192))
+    w = _bf16_rand(rng, (3, 192))
+    got = routing.dot_fixed(x, w)
+    for t in range(2):
+        for e in range(3):
+            lanes = []
+            for l in range(64):
+                acc = np.float32(0.0)
+                for j in range(3):
+                    acc = np.float32(acc + np.float32(x[t, l + 64 * j]) * np.float32(w[e, l + 64 * j]))
+                lanes.append(acc)
+            for off in (32, 16, 8, 4, 2, 1):
+                lanes = [np.float32(lanes[i] + lanes[i ^ off]) for i in range(64)]
+            assert np.float32(got[t, e]) == lanes[0]
+
+
+def test_gptoss_topk_ties_to_lower_id_and_softmax():
+    x = torch.zeros(3, 64)
+    x[:, 0] = 1.0
+    w = torch.zeros(8, 64)
+    b = torch.tensor([0.5, 2.0, 2.0, -1.0, 2.0, 0.5, 3.0, 0.5])      # ties at 2.0 and at 0.5
+    ids, wts, _ = routing.gptoss_route(x, w, b, k=4)
+    assert ids.tolist() == [[1, 2, 4, 6]] * 3                           # 6 first, then 1,2,4 (lowest ids)
+    v = np.array([2.0, 2.0, 2.0, 3.0])
+    e = np.exp(v - 3.0)
+    np.testing.assert_allclose(wts[0], e / e.sum(), rtol=1e-6)
+    b2 = torch.tensor([0.5, 2.0, 1.0, -1.0, 2.0, 0.5, 3.0, 0.5])
+    ids2, _, _ = routing.gptoss_route(x, w, b2, k=4)
+    assert ids2.tolist()[0] == [1, 2, 4, 6]
+    b3 = torch.tensor([0.5, 2.0, 0.0, -1.0, 2.0, 0.5, 3.0, 0.5])        # 0.5 tie among 0, 5, 7 -> 0
+    assert routing.gptoss_route(x, w, b3, k=4)[0].tolist()[0] == [0, 1, 4, 6]
+
+
+def test_gptoss_route_brute_force():
+    rng = np.random.default_rng(2)
+    x = _bf16_rand(rng, (40, 128))
+    w = _bf16_rand(rng, (16, 128), 0.1)
+    b = _bf16_rand(rng, (16,), 0.1)
+    ids, wts, logits = routing.gptoss_route(x, w, b, k=4)
+    L = logits.numpy()
+    for t in range(40):
+        order = sorted(range(16), key=lambda e: (-float(L[t, e]), e))[:4]
+        assert ids[t].tolist() == sorted(order)
+        vals = [float(L[t, e]) for e in sorted(order)]
+        m = max(vals)
+        ex = [math.exp(v - m) for v in vals]
+        np.testing.assert_allclose(wts[t], [v / sum(ex) for v in ex], rtol=1e-6)
+    # logits are the bf16 rounding of the fixed-order fp32 dot (+ bias)
+    ref = x.double() @ w.double().T + b.double()
+    assert torch.allclose(logits.double(), ref, rtol=1e-2, atol=1e-2)
+
+
+def test_permute_brute_force_and_invariants():
+    rng = np.random.default_rng(3)
+    T, k, E = 37, 4, 16
+    ids = np.sort(np.stack([rng.choice(E, k, replace=False) for _ in range(T)]), axis=1)
+    hist, off, perm, inv = routing.permute(ids, E)
+    flat = ids.reshape(-1)
+    want = [a for e in range(E) for a in range(T * k) if flat[a] == e]
+    assert perm.tolist() == want
+    assert hist.sum() == T * k and (np.diff(off) == hist).all() and off[0] == 0
+    assert (perm[inv] == np.arange(T * k)).all() and (inv[perm] == np.arange(T * k)).all()
+    for e in range(E):
+        assert (flat[perm[off[e]:off[e + 1]]] == e).all()
+
+
+def test_combine_fp64_brute_force():
+    rng = np.random.default_rng(4)
+    T, k, H = 5, 4, 32
+    y = rng.standard_normal((T * k, H)).astype(np.float32)
+    inv = rng.permutation(T * k).astype(np.int32)
+    w = rng.random((T, k)).astype(np.float32)
+    res = bf16(torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32)))
+    out = routing.combine(y, inv, w, residual=res).numpy()
+    ref = np.zeros((T, H))
+    for t in range(T):
+        for s in range(k):
+            ref[t] += float(w[t, s]) * y[inv[t * k + s]].astype(np.float64)
+    ref = bf16(res + bf16(torch.from_numpy(ref.astype(np.float32)))).numpy()
+    mar, cos = metrics(out, ref)
+    assert mar < 1e-2 and cos > 0.9999
+
+
+def test_sigmoid_det_accuracy():
+    x = np.linspace(-30, 30, 20001, dtype=np.float32)
+    got = routing.sigmoid_det(x).astype(np.float64)
+    ref = 1.0 / (1.0 + np.exp(-x.astype(np.float64)))
+    assert np.max(np.abs(got - ref) / ref) < 4e-7
+    e = routing.exp_det(np.linspace(-80, 80, 1001, dtype=np.float32)).astype(np.float64)
+    np.testing.assert_allclose(e, np.exp(np.linspace(-80, 80, 1001, dtype=np.float32).astype(np.float64)),
+                               rtol=4e-7)
+
+
+def test_grouped_sigmoid_brute_force():
+    rng = np.random.default_rng(5)
+    T, H, E, G, TG, K = 12, 64, 32, 8, 4, 8
+    x = _bf16_rand(rng, (T, H))
+    w = _bf16_rand(rng, (E, H), 0.2)
+    bias = (rng.standard_normal(E) * 0.1).astype(np.float32)
+    ids, wts, scores = routing.grouped_sigmoid_route(x, w, bias, G, TG, K, 2.5)
+    logits = routing.dot_fixed(x, w).numpy()
+    for t in range(T):
+        s = [float(routing.sigmoid_det(np.float32(logits[t, e]))) for e in range(E)]
+        c = [np.float32(np.float32(s[e]) + bias[e]) for e in range(E)]
+        gs = []
+        for g in range(G):
+            grp = sorted(c[g * 4:(g + 1) * 4], reverse=True)
+            gs.append(np.float32(grp[0] + grp[1]))
+        keep = sorted(range(G), key=lambda g: (-gs[g], g))[:TG]
+        cand = [e for e in range(E) if e // 4 in keep]
+        sel = sorted(sorted(cand, key=lambda e: (-c[e], e))[:K])
+        assert ids[t].tolist() == sel
+        ws = np.array([s[e] for e in sel])
+        np.testing.assert_allclose(wts[t], ws / (ws.sum() + 1e-20) * 2.5, rtol=1e-6)
+
+
+# ---- a5/a6 experts -----------------------------------------------------------------------------
+
+def test_swiglu_closed_form_boundaries():
+    g = torch.tensor([-10.0, 0.0, 7.0, 9.0, 2.0])
+    u = torch.tensor([-9.0, 3.0, -7.0, 8.0, -1.0])
+    out = experts.swiglu(g, u)
+    sig = lambda v: 1.0 / (1.0 + math.exp(-1.702 * v))
+    ref = [(-7 + 1) * (-10) * sig(-10), 0.0, (-7 + 1) * 7 * sig(7), (7 + 1) * 7 * sig(7), 0.0]
+    np.testing.assert_allclose(out.numpy(), ref, rtol=1e-6, atol=1e-7)
+
+
+def test_experts_mxfp4_fp64_brute_force():
+    rng = np.random.default_rng(6)
+    E, H, I, T, k = 3, 64, 64, 4, 2
+    mk = lambda n, kk: (rng.integers(0, 256, (E, n, kk // 32, 16), dtype=np.uint8),
+                        rng.integers(119, 124, (E, n, kk // 32), dtype=np.uint8))
+    b13, s13 = mk(2 * I, H)
+    b2, s2 = mk(H, I)
+    bias13 = rng.standard_normal((E, 2 * I)).astype(np.float32) * 0.1
+    bias2 = rng.standard_normal((E, H)).astype(np.float32) * 0.1
+    wts = experts.MxExpertWeights(b13, s13, bias13, b2, s2, bias2)
+    x = _bf16_rand(rng, (T, H))
+    ids = np.array([[0, 2], [1, 2], [0, 1], [2, 0]])
+    ids.sort(axis=1)
+    _, off, perm, inv = routing.permute(ids, E)
+    y = experts.experts_mxfp4(x, perm, off, k, wts).numpy()
+    for p in range(T * k):
+        t, e = perm[p] // k, ids.reshape(-1)[perm[p]]
+        W13 = mxfp4.dequant(b13[e], s13[e]).astype(np.float64)
+        W2 = mxfp4.dequant(b2[e], s2[e]).astype(np.float64)
+        gu = W13 @ x[t].double().numpy() + bias13[e]
+        gte, up = np.minimum(gu[0::2], 7.0), np.clip(gu[1::2], -7.0, 7.0)
+        h = (up + 1) * gte / (1 + np.exp(-1.702 * gte))
+        h = bf16(torch.from_numpy(h.astype(np.float32))).double().numpy()
+        ref = W2 @ h + bias2[e]
+        mar, cos = metrics(y[p], ref)
+        assert mar < 1e-5 and cos > 0.999999
+
+
+# ---- a7 fp8 ------------------------------------------------------------------------------------
+
+def test_round_scale_pow2_exact_at_powers_of_two():
+    """v4_kernels_cpu.py:34-39: scale = 2**ceil(log2(amax/448)), exact when amax = 448 * 2**k."""
+    for kk in range(-10, 10):
+        amax = np.float32(448.0 * 2.0 ** kk)
+        assert experts.round_scale_pow2(np.array([amax]), 1.0 / 448.0)[0] == np.float32(2.0 ** kk)
+        just_over = np.nextafter(amax, np.float32(np.inf))
+        assert experts.round_scale_pow2(np.array([just_over]), 1.0 / 448.0)[0] == np.float32(2.0 ** (kk + 1))
+
+
+def test_fp8_block_gemm_fp64():
+    rng = np.random.default_rng(7)
+    x = bf16(torch.from_numpy(rng.standard_normal((3, 256)).astype(np.float32))).numpy()
+    wq, ws = experts.fp8_block_quant_weight(rng.standard_normal((256, 256)).astype(np.float32) * 0.05)
+    aq, sa = experts.act_quant_128(x)
+    out = experts.fp8_block_gemm(aq, sa, wq, ws)
+    deq_a = aq * np.repeat(sa, 128, axis=1)
+    deq_w = wq * np.repeat(np.repeat(ws, 128, axis=0), 128, axis=1)
+    np.testing.assert_allclose(out, deq_a.astype(np.float64) @ deq_w.astype(np.float64).T, rtol=1e-9, atol=1e-9)
+    assert np.abs(aq).max() <= 448.0
+    mar, cos = metrics(out, x.astype(np.float64) @ deq_w.astype(np.float64).T)
+    assert cos > 0.999
+
+
+# ---- a8 attention ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("window", [0, 4])
+def test_ragged_attention_brute_force(window):
+    rng = np.random.default_rng(8)
+    Hq, Hkv, D = 4, 2, 8
+    q_lens, starts = [1, 3, 2], [5, 0, 9]
+    T = sum(q_lens)
+    q = bf16(torch.from_numpy(rng.standard_normal((T, Hq, D)).astype(np.float32)))
+    ks = [torch.from_numpy(rng.standard_normal((Hkv, 16, D)).astype(np.float32)) for _ in q_lens]
+    vs = [torch.from_numpy(rng.standard_normal((Hkv, 16, D)).astype(np.float32)) for _ in q_lens]
+    sinks = rng.standard_normal(Hq).astype(np.float32)
+    got = attention.ragged_attention(q, ks, vs, q_lens, starts, sinks, window).numpy()
+    ref = attention.brute_force_attention(q.numpy(), ks, vs, q_lens, starts, sinks, window)
+    mar, cos = metrics(got, ref)
+    assert mar < 1e-2 and cos > 0.99999
+
+
+def test_bf16_bit_helpers_roundtrip():
+    x = np.array([1.0, -2.5, 3.14159, 1e-20, 65504.0], dtype=np.float32)
+    bits = f32_to_bf16_bits(x)
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert (bits == ref).all()
+    assert (bf16_bits_to_f32(bits) == torch.from_numpy(x).to(torch.bfloat16).float().numpy()).all()

@@ -1,0 +1,193 @@
+"""Benchmark: one GPT-OSS-120B-shaped pipeline stage's continuous-batch forward step on one MI355X.
+
+Workload (default): 9 decoder layers (sliding window 128 on even layers, full attention on odd),
+64 query / 8 KV heads of dim 64 with learned sinks, 128-expert top-4 MXFP4 MoE (H = I = 2880);
+a ragged batch of 32 sequences -- 24 single-token decode rows and 8 four-token spec-verify rows
+(56 tokens) -- with per-sequence KV length uniform in [512, 8192]; KV and activations bf16
+N(0,1), weights random-init (synthetic data, seed 0).
+
+A step is one stage forward over that batch.  value = tokens / second over the timed steps.
+The roofline object covers the dominant kernel (the MXFP4 gate_up expert GEMM), timed with HIP
+events on the stream it runs on; its algorithmic bytes count every touched expert's weights and
+scales once plus activations in and out.  cpu_baseline runs the CPU oracle on one of the nine
+layers (same inputs) and scales to the stage.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+
+
+def c1_batch(seed=0):
+    rng = np.random.default_rng(seed)
+    q_lens = [1] * 24 + [4] * 8
+    starts = [int(v) for v in rng.integers(512, 8192 + 1, size=32)]
+    return q_lens, starts
+
+
+def gate_up_algorithmic_bytes(shape, hist, T, k):
+    """Touched experts' gate_up codes + scales + fp32 bias, once each, plus x in, h out, perm."""
+    H, I = shape.hidden, shape.intermediate
+    touched = int((hist > 0).sum())
+    per_expert = (2 * I) * H // 2 + (2 * I) * H // 32 + 4 * (2 * I)
+    return touched * per_expert + T * H * 2 + T * k * I * 2 + T * k * 4, touched
+
+
+def down_algorithmic_bytes(shape, hist, T, k):
+    H, I = shape.hidden, shape.intermediate
+    touched = int((hist > 0).sum())
+    per_expert = H * I // 2 + H * I // 32 + 4 * H
+    return touched * per_expert + T * k * I * 2 + T * k * H * 4, touched
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=9)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=50)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the stage is single-GPU by design: no collectives, no sharding)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from flyai_amd import ops
+    from flyai_amd.rope import YarnRotary
+    from flyai_amd.runtime import KVWorkspace, RaggedStage
+    from flyai_amd.weights import GptOssShape, synthetic_layer
+
+    dev = "cuda"
+    torch.cuda.set_device(0)
+    shape = GptOssShape()
+    q_lens, starts = c1_batch(0)
+    S, T = len(q_lens), sum(q_lens)
+    maxlen = 8192 + 64
+    print(f"[bench] building {args.layers}-layer stage ...", file=sys.stderr, flush=True)
+    layers = [synthetic_layer(shape, 1000 + i, dev, sliding=(i % 2 == 0), keep_hf=(i == 1 and not args.no_cpu))
+              for i in range(args.layers)]
+    rot = YarnRotary(maxlen, device=dev)
+    kv = KVWorkspace(args.layers, S, maxlen, shape.n_kv_heads, shape.head_dim, dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    for t in kv.k + kv.v:
+        t.copy_(torch.randn(t.shape, device=dev, generator=g).to(torch.bfloat16))
+    hidden0 = torch.randn(T, shape.hidden, device=dev, generator=g).to(torch.bfloat16)
+    stage = RaggedStage(shape, layers, rot, kv, max_tokens=64, max_seqs=S)
+    slots = list(range(S))
+    torch.cuda.synchronize()
+    print("[bench] warmup", file=sys.stderr, flush=True)
+    h = hidden0.clone()
+    for _ in range(args.warmup):
+        h.copy_(hidden0)
+        stage.forward(h, q_lens, starts, slots)
+    torch.cuda.synchronize()
+    print("[bench] timed steps", file=sys.stderr, flush=True)
+    hs = [hidden0.clone() for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        stage.forward(hs[i], q_lens, starts, slots)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = T * args.steps / elapsed
+
+    # ---- dominant kernel: MXFP4 gate_up of layer 1 (full-attention layer), HIP events ----------
+    lw = layers[1]
+    xn = stage.debug_buffer(0, torch.bfloat16, (T, shape.hidden)).clone()
+    ids, wts = ops.router_topk_softmax(xn, lw.router_w, lw.router_b, shape.top_k)
+    hist, off, perm, inv = ops.moe_permute(ids, shape.n_experts)
+    hmoe = ops.moe_gate_up(xn, perm, off, shape.top_k, lw.w13_packed, lw.b13, shape.n_experts, shape.intermediate)
+    torch.cuda.synchronize()
+    hist_np = hist.cpu().numpy()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    reps = args.kernel_reps
+    ev[0].record()
+    for _ in range(reps):
+        ops.moe_gate_up(xn, perm, off, shape.top_k, lw.w13_packed, lw.b13, shape.n_experts, shape.intermediate)
+    ev[1].record()
+    for _ in range(reps):
+        ops.moe_down(hmoe, off, lw.w2_packed, lw.b2, shape.n_experts, shape.hidden)
+    ev[2].record()
+    torch.cuda.synchronize()
+    gu_us = ev[0].elapsed_time(ev[1]) * 1e3 / reps
+    dn_us = ev[1].elapsed_time(ev[2]) * 1e3 / reps
+    gu_bytes, touched = gate_up_algorithmic_bytes(shape, hist_np, T, shape.top_k)
+    dn_bytes, _ = down_algorithmic_bytes(shape, hist_np, T, shape.top_k)
+    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+    dn_gbs = dn_bytes / (dn_us * 1e-6) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "moe_gate_up_c1_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(layers[1], kv, 1, hidden0, q_lens, starts, slots, shape, maxlen, args.layers)
+
+    line = {
+        "metric": "stage tokens/sec at ragged batch 32; MoE layer us; % HBM/MFMA roofline",
+        "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4-e2m1/bf16 (fp32 accumulate)",
+        "data": "synthetic (seeded random-init weights, N(0,1) KV and activations)",
+        "config": {"workload": "gpt-oss-120b-shaped 9-layer MXFP4 stage, ragged batch of 32 sequences "
+                               "(24 decode + 8 four-token verify = 56 tokens), KV 512-8192",
+                   "layers": args.layers, "tokens": T, "sequences": S, "experts": shape.n_experts,
+                   "top_k": shape.top_k, "hidden": shape.hidden, "parallelism": "single GPU"},
+        "moe_layer_us": round(gu_us + dn_us, 2),
+        "roofline": {"bound": "hbm", "kernel": "moe_mxfp4_kernel<gate_up>", "achieved": round(gu_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "algorithmic_bytes": gu_bytes, "avg_us": round(gu_us, 2),
+                     "experts_touched": touched},
+        "kernels": {"moe_down": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),
+                                 "frac": round(dn_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": dn_bytes}},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+def cpu_baseline(lw, kv, layer_idx, hidden0, q_lens, starts, slots, shape, maxlen, n_layers):
+    """The CPU oracle on one decoder layer of the same batch; stage tokens/s = T / (n_layers * t)."""
+    import torch
+    from oracle import experts as oexperts
+    from oracle import layer as olayer
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    f = lambda t: t.detach().float().cpu()
+    moe = oexperts.MxExpertWeights(lw.w13_blocks.cpu().numpy(), lw.w13_scales.cpu().numpy(),
+                                   lw.b13.cpu().numpy(), lw.w2_blocks.cpu().numpy(),
+                                   lw.w2_scales.cpu().numpy(), lw.b2.cpu().numpy())
+    p = olayer.LayerParams(f(lw.ln1), f(lw.ln2), f(lw.wqkv), f(lw.bqkv), f(lw.wo), f(lw.bo), f(lw.sinks),
+                           f(lw.router_w), f(lw.router_b), moe, lw.sliding)
+    ks = [f(kv.k_view(layer_idx, s)).clone() for s in slots]
+    vs = [f(kv.v_view(layer_idx, s)).transpose(1, 2).contiguous() for s in slots]
+    cos, sin = olayer.rope_table(maxlen)
+    h = f(hidden0)
+    print("[bench] cpu oracle: one layer", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    olayer.decoder_layer(h, p, (ks, vs), q_lens, starts, cos, sin)
+    dt = time.perf_counter() - t0
+    T = sum(q_lens)
+    return {"value": round(T / (dt * n_layers), 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle (torch fp32 + numpy) on 1 of {n_layers} layers (a full-attention layer) "
+                      f"of the same 56-token batch: {dt:.2f} s; stage rate = 56 / ({n_layers} x layer time)"}
+
+
+if __name__ == "__main__":
+    main()

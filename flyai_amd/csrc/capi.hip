@@ -1,0 +1,331 @@
+// C ABI: error reporting and the stage step driver (per-layer kernel sequence on one stream).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+#include <string>
+
+#include "common.h"
+
+namespace flyai {
+
+static thread_local char g_last_error[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(FLYAI_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return FLYAI_OK;
+}
+
+// launchers defined in the kernel files
+int launch_router(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int, int, int32_t*,
+                  float*, float*, hipStream_t);
+int launch_permute(const int32_t*, int, int, int, int32_t*, int32_t*, int32_t*, int32_t*, hipStream_t);
+int launch_combine(const float*, const int32_t*, const float*, int, int, int, const uint16_t*,
+                   uint16_t*, hipStream_t);
+int launch_moe_gate_up(const uint16_t*, const int32_t*, const int32_t*, int, const uint8_t*,
+                       const float*, int, int, int, uint16_t*, hipStream_t);
+int launch_moe_down(const uint16_t*, const int32_t*, const uint8_t*, const float*, int, int, int,
+                    float*, hipStream_t);
+int launch_rmsnorm(const uint16_t*, const float*, int, int, float, uint16_t*, hipStream_t);
+int launch_linear(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int, uint16_t*,
+                  uint16_t*, hipStream_t);
+int launch_rope_kv(const uint16_t*, const int32_t*, const int32_t*, const uint16_t*,
+                   const uint16_t*, int, int, int, int, int, const int64_t*, const int32_t*, uint16_t*,
+                   uint16_t*, uint16_t*, hipStream_t);
+int launch_attn(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
+                const float*, int, int, const flyai_attn_item*, int, const flyai_attn_group*, int,
+                float*, uint16_t*, hipStream_t);
+int attn_plan(const int32_t*, const int32_t*, int, int, int, int, flyai_attn_item*, int,
+              flyai_attn_group*, int, int*, int*);
+
+}  // namespace flyai
+
+using namespace flyai;
+
+namespace {
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct Carve {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t o = off;
+    off = align256(off + bytes);
+    return o;
+  }
+};
+
+}  // namespace
+
+struct flyai_stage {
+  flyai_stage_config cfg;
+  int qkv_width, max_groups, P;
+  flyai_layer_desc* layers = nullptr;
+  const uint16_t* cos_tab = nullptr;
+  const uint16_t* sin_tab = nullptr;
+  // device workspace offsets
+  size_t o_qlens, o_starts, o_cap, o_base, o_cu, o_pos, o_sid, o_kvlen, o_slot, o_status;
+  size_t o_xn, o_qkv, o_qrot, o_attn, o_items[2], o_groups[2], o_parts;
+  size_t o_ids, o_w, o_hist, o_off, o_perm, o_inv, o_hmoe, o_y;
+  size_t dev_bytes = 0;
+  // host staging offsets (within one half)
+  size_t h_qlens, h_starts, h_cap, h_base, h_items[2], h_groups[2];
+  size_t host_half = 0;
+  char* dev = nullptr;
+  char* host = nullptr;
+  hipEvent_t staged[2] = {nullptr, nullptr};
+  int half = 0;
+  bool events_ready = false;
+};
+
+static void layout(flyai_stage* st) {
+  const flyai_stage_config& c = st->cfg;
+  const size_t S = c.max_seqs, T = c.max_tokens, P = (size_t)T * c.top_k;
+  Carve d;
+  st->o_qlens = d.take(S * 4);
+  st->o_starts = d.take(S * 4);
+  st->o_cap = d.take(S * 4);
+  st->o_base = d.take(S * 8);
+  st->o_cu = d.take((S + 1) * 4);
+  st->o_pos = d.take(T * 4);
+  st->o_sid = d.take(T * 4);
+  st->o_kvlen = d.take(S * 4);
+  st->o_slot = d.take(T * 8);
+  st->o_status = d.take(4);
+  st->o_xn = d.take(T * c.hidden * 2);
+  st->o_qkv = d.take(T * st->qkv_width * 2);
+  st->o_qrot = d.take(T * c.n_q_heads * c.head_dim * 2);
+  st->o_attn = d.take(T * c.n_q_heads * c.head_dim * 2);
+  for (int i = 0; i < 2; ++i) {
+    st->o_items[i] = d.take((size_t)c.max_attn_items * sizeof(flyai_attn_item));
+    st->o_groups[i] = d.take((size_t)st->max_groups * sizeof(flyai_attn_group));
+  }
+  st->o_parts = d.take(flyai_attn_partials_bytes(c.max_attn_items));
+  st->o_ids = d.take(P * 4);
+  st->o_w = d.take(P * 4);
+  st->o_hist = d.take((size_t)c.n_experts * 4);
+  st->o_off = d.take(((size_t)c.n_experts + 1) * 4);
+  st->o_perm = d.take(P * 4);
+  st->o_inv = d.take(P * 4);
+  st->o_hmoe = d.take(P * c.intermediate * 2);
+  st->o_y = d.take(P * c.hidden * 4);
+  st->dev_bytes = d.off;
+  Carve h;
+  st->h_qlens = h.take(S * 4);
+  st->h_starts = h.take(S * 4);
+  st->h_cap = h.take(S * 4);
+  st->h_base = h.take(S * 8);
+  for (int i = 0; i < 2; ++i) {
+    st->h_items[i] = h.take((size_t)c.max_attn_items * sizeof(flyai_attn_item));
+    st->h_groups[i] = h.take((size_t)st->max_groups * sizeof(flyai_attn_group));
+  }
+  st->host_half = h.off;
+}
+
+extern "C" const char* flyai_last_error(void) { return g_last_error; }
+extern "C" int flyai_abi_version(void) { return FLYAI_ABI_VERSION; }
+
+extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** out) {
+  FLYAI_REQUIRE(cfg && out, "stage_create: null pointer");
+  const flyai_stage_config& c = *cfg;
+  FLYAI_REQUIRE(c.n_layers > 0 && c.hidden > 0 && c.hidden % 64 == 0, "stage: hidden must be a multiple of 64");
+  FLYAI_REQUIRE(c.head_dim == 64 && c.n_kv_heads > 0 && c.n_q_heads == 8 * c.n_kv_heads,
+                "stage: attention kernel needs head_dim 64 and 8 query heads per kv head");
+  FLYAI_REQUIRE(c.n_experts > 0 && c.n_experts <= 256 && c.top_k >= 1 && c.top_k <= 8,
+                "stage: need 1 <= n_experts <= 256, 1 <= top_k <= 8");
+  FLYAI_REQUIRE(c.intermediate > 0 && c.intermediate % 32 == 0 && c.hidden % 32 == 0,
+                "stage: MXFP4 needs hidden and intermediate multiples of 32");
+  FLYAI_REQUIRE(c.max_tokens > 0 && (int64_t)c.max_tokens * c.top_k <= 65536, "stage: max_tokens*top_k <= 65536");
+  FLYAI_REQUIRE(c.max_seqs > 0 && c.max_seqs <= 8192, "stage: max_seqs in [1, 8192]");
+  FLYAI_REQUIRE(c.max_attn_items > 0 && c.rope_positions > 0, "stage: bad capacities");
+  FLYAI_REQUIRE(c.attn_split_keys >= 64 && c.attn_split_keys % 64 == 0, "stage: attn_split_keys % 64");
+  flyai_stage* st = new (std::nothrow) flyai_stage();
+  if (!st) return set_error(FLYAI_EINVAL, "stage_create: out of host memory");
+  st->cfg = c;
+  st->qkv_width = (c.n_q_heads + 2 * c.n_kv_heads) * c.head_dim;
+  st->max_groups = (c.max_seqs + (c.max_tokens + 3) / 4) * c.n_kv_heads;
+  st->layers = new (std::nothrow) flyai_layer_desc[c.n_layers];
+  if (!st->layers) { delete st; return set_error(FLYAI_EINVAL, "stage_create: out of host memory"); }
+  memset(st->layers, 0, sizeof(flyai_layer_desc) * c.n_layers);
+  layout(st);
+  *out = st;
+  return FLYAI_OK;
+}
+
+extern "C" void flyai_stage_destroy(flyai_stage* st) {
+  if (!st) return;
+  for (int i = 0; i < 2; ++i)
+    if (st->staged[i]) hipEventDestroy(st->staged[i]);
+  delete[] st->layers;
+  delete st;
+}
+
+extern "C" int flyai_stage_set_layer(flyai_stage* st, int32_t layer, const flyai_layer_desc* d) {
+  FLYAI_REQUIRE(st && d, "set_layer: null pointer");
+  FLYAI_REQUIRE(layer >= 0 && layer < st->cfg.n_layers, "set_layer: layer %d out of range", layer);
+  FLYAI_REQUIRE(d->ln1 && d->ln2 && d->wqkv && d->wo && d->sinks && d->router_w && d->router_b &&
+                    d->w13_packed && d->b13 && d->w2_packed && d->b2 && d->k_pool && d->v_pool,
+                "set_layer: null weight pointer");
+  st->layers[layer] = *d;
+  return FLYAI_OK;
+}
+
+extern "C" int flyai_stage_set_rope(flyai_stage* st, const uint16_t* cos_tab, const uint16_t* sin_tab) {
+  FLYAI_REQUIRE(st && cos_tab && sin_tab, "set_rope: null pointer");
+  st->cos_tab = cos_tab;
+  st->sin_tab = sin_tab;
+  return FLYAI_OK;
+}
+
+extern "C" size_t flyai_stage_workspace_bytes(const flyai_stage* st) { return st ? st->dev_bytes : 0; }
+extern "C" size_t flyai_stage_host_staging_bytes(const flyai_stage* st) {
+  return st ? 2 * st->host_half : 0;
+}
+
+extern "C" int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t dev_bytes,
+                                         void* host_pinned, size_t host_bytes) {
+  FLYAI_REQUIRE(st && dev_ws && host_pinned, "set_workspace: null pointer");
+  FLYAI_REQUIRE(dev_bytes >= st->dev_bytes && host_bytes >= 2 * st->host_half,
+                "set_workspace: need %zu device and %zu pinned host bytes", st->dev_bytes,
+                2 * st->host_half);
+  FLYAI_REQUIRE(((uintptr_t)dev_ws & 255) == 0, "set_workspace: device workspace must be 256-byte aligned");
+  st->dev = static_cast<char*>(dev_ws);
+  st->host = static_cast<char*>(host_pinned);
+  if (!st->events_ready) {
+    for (int i = 0; i < 2; ++i) {
+      const hipError_t e = hipEventCreateWithFlags(&st->staged[i], hipEventDisableTiming);
+      if (e != hipSuccess) return set_error(FLYAI_EHIP, "hipEventCreate: %s", hipGetErrorString(e));
+    }
+    st->events_ready = true;
+  }
+  return FLYAI_OK;
+}
+
+extern "C" void* flyai_stage_debug_buffer(flyai_stage* st, int32_t which) {
+  if (!st || !st->dev) return nullptr;
+  const size_t offs[] = {st->o_xn, st->o_qkv, st->o_qrot, st->o_attn, st->o_ids, st->o_w,
+                         st->o_off, st->o_perm, st->o_inv, st->o_hmoe, st->o_y, st->o_pos,
+                         st->o_sid, st->o_cu};
+  if (which < 0 || which >= (int)(sizeof(offs) / sizeof(offs[0]))) return nullptr;
+  return st->dev + offs[which];
+}
+
+#define RUN(x)              \
+  do {                      \
+    const int rc__ = (x);   \
+    if (rc__) return rc__;  \
+  } while (0)
+
+static int copy_h2d(char* dst, const char* src, size_t bytes, hipStream_t s) {
+  if (bytes == 0) return FLYAI_OK;
+  const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return set_error(FLYAI_EHIP, "hipMemcpyAsync: %s", hipGetErrorString(e));
+  return FLYAI_OK;
+}
+
+extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const int32_t* starts,
+                                   const int64_t* kv_base, const int32_t* kv_cap, int32_t S,
+                                   uint16_t* hidden, flyai_stream_t stream) {
+  FLYAI_REQUIRE(st && q_lens && starts && kv_base && kv_cap && hidden, "forward: null pointer");
+  FLYAI_REQUIRE(st->dev && st->host, "forward: workspace not set");
+  FLYAI_REQUIRE(st->cos_tab && st->sin_tab, "forward: rope tables not set");
+  const flyai_stage_config& c = st->cfg;
+  FLYAI_REQUIRE(S >= 1 && S <= c.max_seqs, "forward: n_seqs %d out of [1, %d]", S, c.max_seqs);
+  int64_t T = 0;
+  for (int b = 0; b < S; ++b) {
+    FLYAI_REQUIRE(q_lens[b] >= 1 && starts[b] >= 0, "forward: sequence %d has q_len %d start %d", b,
+                  q_lens[b], starts[b]);
+    FLYAI_REQUIRE(kv_cap[b] > 0 && kv_cap[b] % 64 == 0 && kv_base[b] >= 0 && kv_base[b] % 8 == 0,
+                  "forward: sequence %d needs kv_cap %% 64 == 0 and kv_base %% 8 == 0", b);
+    const int64_t need = (int64_t)starts[b] + q_lens[b];
+    if (need > kv_cap[b])
+      return set_error(FLYAI_ERANGE, "sequence %d needs %lld positions > KV capacity %d", b,
+                       (long long)need, kv_cap[b]);
+    if (need > c.rope_positions)
+      return set_error(FLYAI_ERANGE, "sequence %d needs %lld positions > rope table %d", b,
+                       (long long)need, c.rope_positions);
+    T += q_lens[b];
+  }
+  if (T > c.max_tokens)
+    return set_error(FLYAI_ERANGE, "batch has %lld tokens > max_tokens %d", (long long)T, c.max_tokens);
+  for (int l = 0; l < c.n_layers; ++l)
+    FLYAI_REQUIRE(st->layers[l].wqkv, "forward: layer %d not bound", l);
+  hipStream_t s = as_stream(stream);
+
+  // stage host inputs: wait until the GPU consumed this half's previous contents
+  const int h = st->half;
+  st->half ^= 1;
+  const hipError_t ew = hipEventSynchronize(st->staged[h]);
+  if (ew != hipSuccess) return set_error(FLYAI_EHIP, "hipEventSynchronize: %s", hipGetErrorString(ew));
+  char* hb = st->host + h * st->host_half;
+  memcpy(hb + st->h_qlens, q_lens, S * 4);
+  memcpy(hb + st->h_starts, starts, S * 4);
+  memcpy(hb + st->h_cap, kv_cap, S * 4);
+  memcpy(hb + st->h_base, kv_base, S * 8);
+  int n_items[2], n_groups[2];
+  for (int p = 0; p < 2; ++p) {
+    RUN(attn_plan(q_lens, starts, S, c.n_kv_heads, p == 0 ? 0 : c.window, c.attn_split_keys,
+                  reinterpret_cast<flyai_attn_item*>(hb + st->h_items[p]), c.max_attn_items,
+                  reinterpret_cast<flyai_attn_group*>(hb + st->h_groups[p]), st->max_groups,
+                  &n_items[p], &n_groups[p]));
+  }
+  char* d = st->dev;
+  RUN(copy_h2d(d + st->o_qlens, hb + st->h_qlens, S * 4, s));
+  RUN(copy_h2d(d + st->o_starts, hb + st->h_starts, S * 4, s));
+  RUN(copy_h2d(d + st->o_cap, hb + st->h_cap, S * 4, s));
+  RUN(copy_h2d(d + st->o_base, hb + st->h_base, S * 8, s));
+  for (int p = 0; p < 2; ++p) {
+    RUN(copy_h2d(d + st->o_items[p], hb + st->h_items[p], n_items[p] * sizeof(flyai_attn_item), s));
+    RUN(copy_h2d(d + st->o_groups[p], hb + st->h_groups[p], n_groups[p] * sizeof(flyai_attn_group), s));
+  }
+  const hipError_t er = hipEventRecord(st->staged[h], s);
+  if (er != hipSuccess) return set_error(FLYAI_EHIP, "hipEventRecord: %s", hipGetErrorString(er));
+
+  auto I32 = [&](size_t o) { return reinterpret_cast<int32_t*>(d + o); };
+  auto F32 = [&](size_t o) { return reinterpret_cast<float*>(d + o); };
+  auto B16 = [&](size_t o) { return reinterpret_cast<uint16_t*>(d + o); };
+  const int64_t* base_d = reinterpret_cast<const int64_t*>(d + st->o_base);
+
+  RUN(flyai_pack_ragged(I32(st->o_qlens), I32(st->o_starts), base_d, I32(st->o_cap), S, c.head_dim,
+                        c.max_tokens, I32(st->o_cu), I32(st->o_pos), I32(st->o_sid),
+                        I32(st->o_kvlen), reinterpret_cast<int64_t*>(d + st->o_slot),
+                        I32(st->o_status), stream));
+  const int Tn = (int)T;
+  const int H = c.hidden, E = c.n_experts, k = c.top_k, I = c.intermediate;
+  for (int l = 0; l < c.n_layers; ++l) {
+    const flyai_layer_desc& L = st->layers[l];
+    const int p = L.sliding ? 1 : 0;
+    RUN(launch_rmsnorm(hidden, L.ln1, Tn, H, c.rms_eps, B16(st->o_xn), s));
+    RUN(launch_linear(B16(st->o_xn), L.wqkv, L.bqkv, Tn, st->qkv_width, H, B16(st->o_qkv), nullptr, s));
+    RUN(launch_rope_kv(B16(st->o_qkv), I32(st->o_pos), I32(st->o_sid), st->cos_tab, st->sin_tab,
+                       c.rope_positions, Tn,
+                       c.n_q_heads, c.n_kv_heads, c.head_dim, base_d, I32(st->o_cap), B16(st->o_qrot),
+                       L.k_pool, L.v_pool, s));
+    RUN(launch_attn(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, I32(st->o_cap), L.sinks,
+                    L.sliding ? c.window : 0, c.n_q_heads,
+                    reinterpret_cast<const flyai_attn_item*>(d + st->o_items[p]), n_items[p],
+                    reinterpret_cast<const flyai_attn_group*>(d + st->o_groups[p]), n_groups[p],
+                    F32(st->o_parts), B16(st->o_attn), s));
+    RUN(launch_linear(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim, nullptr, hidden, s));
+    RUN(launch_rmsnorm(hidden, L.ln2, Tn, H, c.rms_eps, B16(st->o_xn), s));
+    RUN(launch_router(B16(st->o_xn), L.router_w, L.router_b, Tn, H, E, k, I32(st->o_ids),
+                      F32(st->o_w), nullptr, s));
+    RUN(launch_permute(I32(st->o_ids), Tn, k, E, I32(st->o_hist), I32(st->o_off), I32(st->o_perm),
+                       I32(st->o_inv), s));
+    RUN(launch_moe_gate_up(B16(st->o_xn), I32(st->o_perm), I32(st->o_off), k, L.w13_packed, L.b13,
+                           E, H, I, B16(st->o_hmoe), s));
+    RUN(launch_moe_down(B16(st->o_hmoe), I32(st->o_off), L.w2_packed, L.b2, E, H, I, F32(st->o_y), s));
+    RUN(launch_combine(F32(st->o_y), I32(st->o_inv), F32(st->o_w), Tn, k, H, hidden, hidden, s));
+  }
+  return FLYAI_OK;
+}

@@ -1,0 +1,96 @@
+// Ragged batch packing (decode, spec-verify and chunked-prefill rows -> one flat token axis).
+#include "common.h"
+
+namespace flyai {
+
+constexpr int kPackThreads = 1024;
+constexpr int kPackMaxSeqs = 8192;
+
+// One workgroup: block-wide exclusive scan of q_lens into cu_seqlens (LDS), then every thread
+// walks tokens with a binary search over the scanned offsets.
+__global__ __launch_bounds__(kPackThreads) void pack_ragged_kernel(
+    const int32_t* __restrict__ q_lens, const int32_t* __restrict__ starts,
+    const int64_t* __restrict__ kv_base, const int32_t* __restrict__ kv_cap, int S, int head_dim,
+    int max_tokens, int32_t* __restrict__ cu_out, int32_t* __restrict__ positions,
+    int32_t* __restrict__ seq_id, int32_t* __restrict__ kv_len, int64_t* __restrict__ kv_slot,
+    int32_t* __restrict__ status) {
+  __shared__ int32_t cu[kPackMaxSeqs + 1];
+  __shared__ int32_t wave_tot[kPackThreads / 64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) *status = 0;
+  // each thread owns a contiguous run of sequences
+  const int per = (S + kPackThreads - 1) / kPackThreads;
+  const int s0 = min(S, tid * per), s1 = min(S, s0 + per);
+  int local = 0;
+  for (int s = s0; s < s1; ++s) local += q_lens[s];
+  // inclusive wave scan
+  int incl = local;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    int v = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += v;
+  }
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int w = 0; w < kPackThreads / 64; ++w) {
+      int t = wave_tot[w];
+      wave_tot[w] = run;
+      run += t;
+    }
+  }
+  __syncthreads();
+  int run = wave_tot[wave] + incl - local;
+  for (int s = s0; s < s1; ++s) {
+    cu[s] = run;
+    cu_out[s] = run;
+    int len = starts[s] + q_lens[s];
+    kv_len[s] = len;
+    if (len > kv_cap[s]) atomicOr(status, 1);
+    run += q_lens[s];
+  }
+  if (s1 == S && s0 < s1) {
+    cu[S] = run;
+    cu_out[S] = run;
+  }
+  if (S == 0 && tid == 0) { cu[0] = 0; cu_out[0] = 0; }
+  __syncthreads();
+  const int T = cu[S];
+  if (T > max_tokens && tid == 0) atomicOr(status, 2);
+  const int Tw = min(T, max_tokens);
+  for (int t = tid; t < Tw; t += kPackThreads) {
+    int lo = 0, hi = S - 1;  // last s with cu[s] <= t
+    while (lo < hi) {
+      int mid = (lo + hi + 1) >> 1;
+      if (cu[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    const int b = lo;
+    const int pos = starts[b] + (t - cu[b]);
+    positions[t] = pos;
+    seq_id[t] = b;
+    kv_slot[t] = (pos < kv_cap[b]) ? kv_base[b] + (int64_t)pos * head_dim : (int64_t)-1;
+  }
+}
+
+}  // namespace flyai
+
+using namespace flyai;
+
+extern "C" int flyai_pack_ragged(const int32_t* q_lens, const int32_t* starts,
+                                 const int64_t* kv_base, const int32_t* kv_cap, int32_t n_seqs,
+                                 int32_t head_dim, int32_t max_tokens, int32_t* cu_seqlens,
+                                 int32_t* positions, int32_t* seq_id, int32_t* kv_len,
+                                 int64_t* kv_slot, int32_t* status_dev, flyai_stream_t stream) {
+  FLYAI_REQUIRE(n_seqs >= 1 && n_seqs <= kPackMaxSeqs, "pack: n_seqs %d out of [1, %d]", n_seqs,
+                kPackMaxSeqs);
+  FLYAI_REQUIRE(head_dim > 0 && max_tokens >= 0, "pack: bad head_dim/max_tokens");
+  FLYAI_REQUIRE(q_lens && starts && kv_base && kv_cap && cu_seqlens && positions && seq_id &&
+                    kv_len && kv_slot && status_dev,
+                "pack: null pointer");
+  hipLaunchKernelGGL(pack_ragged_kernel, dim3(1), dim3(kPackThreads), 0, as_stream(stream),
+                     q_lens, starts, kv_base, kv_cap, n_seqs, head_dim, max_tokens, cu_seqlens,
+                     positions, seq_id, kv_len, kv_slot, status_dev);
+  return check_launch("pack_ragged");
+}

@@ -1,0 +1,214 @@
+"""Torch-tensor wrappers around the C ABI (one call = one HIP launch sequence on the current stream).
+
+PyTorch provides device memory and the stream; every computation happens in libflyai_stage.so.
+Each wrapper checks dtype / device / contiguity / shape on the host before the launch."""
+import ctypes as C
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return C.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _need(t, dtype, shape=None, name="tensor"):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be on the GPU")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)}, got {tuple(t.shape)}")
+    return t
+
+
+def pack_ragged(q_lens, starts, kv_base, kv_cap, head_dim, max_tokens):
+    """Device int32 q_lens/starts/kv_cap [S], int64 kv_base [S] -> dict of packed index tensors."""
+    S = q_lens.numel()
+    for n, t, dt in (("q_lens", q_lens, torch.int32), ("starts", starts, torch.int32),
+                     ("kv_cap", kv_cap, torch.int32), ("kv_base", kv_base, torch.int64)):
+        _need(t, dt, (S,), n)
+    dev = q_lens.device
+    out = dict(cu_seqlens=torch.empty(S + 1, dtype=torch.int32, device=dev),
+               positions=torch.empty(max_tokens, dtype=torch.int32, device=dev),
+               seq_id=torch.empty(max_tokens, dtype=torch.int32, device=dev),
+               kv_len=torch.empty(S, dtype=torch.int32, device=dev),
+               kv_slot=torch.empty(max_tokens, dtype=torch.int64, device=dev),
+               status=torch.empty(1, dtype=torch.int32, device=dev))
+    check(lib().flyai_pack_ragged(_ptr(q_lens), _ptr(starts), _ptr(kv_base), _ptr(kv_cap), S, head_dim,
+                                  max_tokens, _ptr(out["cu_seqlens"]), _ptr(out["positions"]),
+                                  _ptr(out["seq_id"]), _ptr(out["kv_len"]), _ptr(out["kv_slot"]),
+                                  _ptr(out["status"]), _stream()))
+    return out
+
+
+def router_topk_softmax(x, w, b, k, want_logits=False):
+    T, H = x.shape
+    E = w.shape[0]
+    _need(x, torch.bfloat16, (T, H), "x")
+    _need(w, torch.bfloat16, (E, H), "router weight")
+    _need(b, torch.bfloat16, (E,), "router bias")
+    ids = torch.empty(T, k, dtype=torch.int32, device=x.device)
+    wts = torch.empty(T, k, dtype=torch.float32, device=x.device)
+    logits = torch.empty(T, E, dtype=torch.float32, device=x.device) if want_logits else None
+    check(lib().flyai_router_topk_softmax(_ptr(x), _ptr(w), _ptr(b), T, H, E, k, _ptr(ids), _ptr(wts),
+                                          _ptr(logits), _stream()))
+    return (ids, wts, logits) if want_logits else (ids, wts)
+
+
+def moe_permute(ids, n_experts):
+    T, k = ids.shape
+    _need(ids, torch.int32, (T, k), "topk_ids")
+    dev = ids.device
+    hist = torch.empty(n_experts, dtype=torch.int32, device=dev)
+    offsets = torch.empty(n_experts + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(T * k, dtype=torch.int32, device=dev)
+    inv = torch.empty(T * k, dtype=torch.int32, device=dev)
+    check(lib().flyai_moe_permute(_ptr(ids), T, k, n_experts, _ptr(hist), _ptr(offsets), _ptr(perm),
+                                  _ptr(inv), _stream()))
+    return hist, offsets, perm, inv
+
+
+def moe_combine(y_perm, inv, topk_w, residual=None, out=None):
+    T, k = topk_w.shape
+    H = y_perm.shape[1]
+    _need(y_perm, torch.float32, (T * k, H), "y_perm")
+    _need(inv, torch.int32, (T * k,), "inv")
+    _need(topk_w, torch.float32, (T, k), "topk_w")
+    if residual is not None:
+        _need(residual, torch.bfloat16, (T, H), "residual")
+    if out is None:
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=y_perm.device)
+    _need(out, torch.bfloat16, (T, H), "out")
+    check(lib().flyai_moe_combine(_ptr(y_perm), _ptr(inv), _ptr(topk_w), T, k, H, _ptr(residual),
+                                  _ptr(out), _stream()))
+    return out
+
+
+def mxfp4_packed_bytes(E, N, K):
+    return int(lib().flyai_mxfp4_packed_bytes(E, N, K))
+
+
+def mxfp4_repack(blocks, scales):
+    """HF layout blocks u8 [E, N, K/32, 16] + scales u8 [E, N, K/32] -> packed u8 buffer."""
+    E, N, G, _ = blocks.shape
+    _need(blocks, torch.uint8, (E, N, G, 16), "blocks")
+    _need(scales, torch.uint8, (E, N, G), "scales")
+    packed = torch.empty(mxfp4_packed_bytes(E, N, G * 32), dtype=torch.uint8, device=blocks.device)
+    check(lib().flyai_mxfp4_repack(_ptr(blocks), _ptr(scales), E, N, G * 32, _ptr(packed), _stream()))
+    return packed
+
+
+def moe_gate_up(x, perm, offsets, k, w13_packed, b13, n_experts, inter):
+    T, H = x.shape
+    _need(x, torch.bfloat16, (T, H), "x")
+    _need(perm, torch.int32, (T * k,), "perm")
+    _need(offsets, torch.int32, (n_experts + 1,), "offsets")
+    _need(b13, torch.float32, (n_experts, 2 * inter), "b13")
+    _need(w13_packed, torch.uint8, (mxfp4_packed_bytes(n_experts, 2 * inter, H),), "w13_packed")
+    h = torch.empty(T * k, inter, dtype=torch.bfloat16, device=x.device)
+    check(lib().flyai_moe_gate_up_mxfp4(_ptr(x), _ptr(perm), _ptr(offsets), k, _ptr(w13_packed),
+                                        _ptr(b13), n_experts, H, inter, _ptr(h), _stream()))
+    return h
+
+
+def moe_down(h, offsets, w2_packed, b2, n_experts, hidden):
+    P, inter = h.shape
+    _need(h, torch.bfloat16, (P, inter), "h")
+    _need(offsets, torch.int32, (n_experts + 1,), "offsets")
+    _need(b2, torch.float32, (n_experts, hidden), "b2")
+    _need(w2_packed, torch.uint8, (mxfp4_packed_bytes(n_experts, hidden, inter),), "w2_packed")
+    y = torch.empty(P, hidden, dtype=torch.float32, device=h.device)
+    check(lib().flyai_moe_down_mxfp4(_ptr(h), _ptr(offsets), _ptr(w2_packed), _ptr(b2), n_experts,
+                                     hidden, inter, _ptr(y), _stream()))
+    return y
+
+
+def rmsnorm(x, w, eps=1e-5):
+    T, H = x.shape
+    _need(x, torch.bfloat16, (T, H), "x")
+    _need(w, torch.float32, (H,), "weight")
+    y = torch.empty_like(x)
+    check(lib().flyai_rmsnorm(_ptr(x), _ptr(w), T, H, eps, _ptr(y), _stream()))
+    return y
+
+
+def linear(x, w, b=None, residual=None):
+    """y = bf16(x W^T + b); with residual, residual <- bf16(residual + y) (returned)."""
+    M, K = x.shape
+    N = w.shape[0]
+    _need(x, torch.bfloat16, (M, K), "x")
+    _need(w, torch.bfloat16, (N, K), "weight")
+    if b is not None:
+        _need(b, torch.bfloat16, (N,), "bias")
+    y = None
+    if residual is not None:
+        _need(residual, torch.bfloat16, (M, N), "residual")
+    else:
+        y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    check(lib().flyai_linear_bf16(_ptr(x), _ptr(w), _ptr(b), M, N, K, _ptr(y), _ptr(residual), _stream()))
+    return residual if residual is not None else y
+
+
+def rope_kv_append(qkv, positions, seq_id, cos_tab, sin_tab, n_q_heads, n_kv_heads, head_dim,
+                   kv_base, kv_cap, k_pool, v_pool):
+    T = qkv.shape[0]
+    _need(qkv, torch.bfloat16, (T, (n_q_heads + 2 * n_kv_heads) * head_dim), "qkv")
+    _need(positions, torch.int32, None, "positions")
+    _need(seq_id, torch.int32, None, "seq_id")
+    _need(cos_tab, torch.bfloat16, None, "cos")
+    _need(sin_tab, torch.bfloat16, cos_tab.shape, "sin")
+    _need(kv_base, torch.int64, None, "kv_base")
+    _need(kv_cap, torch.int32, kv_base.shape, "kv_cap")
+    _need(k_pool, torch.bfloat16, None, "k_pool")
+    _need(v_pool, torch.bfloat16, k_pool.shape, "v_pool")
+    if positions.numel() < T or seq_id.numel() < T:
+        raise ValueError("positions/seq_id shorter than the token count")
+    q = torch.empty(T, n_q_heads, head_dim, dtype=torch.bfloat16, device=qkv.device)
+    check(lib().flyai_rope_kv_append(_ptr(qkv), _ptr(positions), _ptr(seq_id), _ptr(cos_tab),
+                                     _ptr(sin_tab), cos_tab.shape[0], T, n_q_heads, n_kv_heads, head_dim, _ptr(kv_base),
+                                     _ptr(kv_cap), _ptr(q), _ptr(k_pool), _ptr(v_pool), _stream()))
+    return q
+
+
+def attn_plan(q_lens, starts, n_kv_heads, window, split_keys, max_items=1 << 20):
+    """Host planner -> (items tensor int32 [n, 8], groups tensor int32 [g, 8]) on the CPU."""
+    S = len(q_lens)
+    ql = (C.c_int32 * S)(*[int(v) for v in q_lens])
+    st = (C.c_int32 * S)(*[int(v) for v in starts])
+    max_groups = (S + sum((int(v) + 3) // 4 for v in q_lens)) * n_kv_heads
+    items = (_lib.AttnItem * max_items)()
+    groups = (_lib.AttnGroup * max_groups)()
+    ni, ng = C.c_int32(0), C.c_int32(0)
+    check(lib().flyai_attn_plan(ql, st, S, n_kv_heads, window, split_keys, items, max_items, groups,
+                                max_groups, C.byref(ni), C.byref(ng)))
+    it = torch.frombuffer(bytearray(items), dtype=torch.int32).view(max_items, 8)[:ni.value].clone()
+    gr = torch.frombuffer(bytearray(groups), dtype=torch.int32).view(max_groups, 8)[:ng.value].clone()
+    return it, gr
+
+
+def attn_ragged(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, items, groups, n_kv_heads):
+    """q bf16 [T, Hq, 64]; items/groups from attn_plan (moved to the GPU here)."""
+    T, Hq, D = q.shape
+    _need(q, torch.bfloat16, (T, Hq, D), "q")
+    _need(sinks, torch.float32, (Hq,), "sinks")
+    dev = q.device
+    items_d = items.to(dev).contiguous()
+    groups_d = groups.to(dev).contiguous()
+    parts = torch.empty(max(1, int(lib().flyai_attn_partials_bytes(items.shape[0])) // 4),
+                        dtype=torch.float32, device=dev)
+    out = torch.empty_like(q)
+    check(lib().flyai_attn_ragged(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(kv_base), _ptr(kv_cap),
+                                  _ptr(sinks), window, Hq, n_kv_heads, D, _ptr(items_d), items.shape[0],
+                                  _ptr(groups_d), groups.shape[0], _ptr(parts), _ptr(out), _stream()))
+    return out

@@ -1,0 +1,241 @@
+"""Stage runtimes over libflyai_stage: a ragged continuous-batch step, plus classes that keep the
+call surface of the reference's stage runtimes so they drop in for that path.
+
+* ``RaggedStage.forward(hidden, q_lens, starts, slots)`` -- one step over a flat token batch that
+  mixes decode rows (q=1), spec-verify rows (q=K+1) and chunked-prefill rows (q=chunk).
+* ``FastVerifyStage`` -- ``FastVerify`` (phase0/fastverify.py:80-309): ``reset``, ``prefill(h, start)``,
+  ``decode(h, start)``, ``tree_decode``, ``tree_gather``; raises ``ContextOverflow`` before any write.
+* ``BatchedFastVerifyStage`` -- ``BatchedFastVerify`` (phase0/batchverify.py:64-190): ``reset``,
+  ``load_prefix(b, src)``, ``decode(h[B, kp1, H], starts[B], use_graph=True)``.
+
+The KV workspace is one slab per sequence slot in per-layer pools: K [Hkv][cap][D] and V transposed
+[Hkv][D][cap] (the attention kernel streams both with 16-byte loads).  It replaces StaticKV /
+BatchedStaticKV ([B, Hkv, maxlen, D] per layer, fastverify.py:52-77, batchverify.py:29-48)."""
+import ctypes as C
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._lib import ContextOverflow, check, lib
+from .weights import GptOssShape
+
+
+def _round_up(v, m):
+    return (v + m - 1) // m * m
+
+
+class KVWorkspace:
+    """Per-layer K/V pools holding ``n_slots`` sequence slabs of ``cap`` positions each."""
+
+    def __init__(self, n_layers, n_slots, maxlen, n_kv_heads=8, head_dim=64, device="cuda"):
+        self.n_layers, self.n_slots = n_layers, n_slots
+        self.cap = _round_up(max(maxlen, 64), 64)
+        self.maxlen = maxlen
+        self.n_kv_heads, self.head_dim = n_kv_heads, head_dim
+        self.slab = n_kv_heads * self.cap * head_dim
+        n = n_slots * self.slab
+        self.k = [torch.zeros(n, dtype=torch.bfloat16, device=device) for _ in range(n_layers)]
+        self.v = [torch.zeros(n, dtype=torch.bfloat16, device=device) for _ in range(n_layers)]
+
+    def base(self, slot):
+        return slot * self.slab
+
+    def zero(self):
+        for t in self.k + self.v:
+            t.zero_()
+
+    def k_view(self, layer, slot):
+        """[Hkv, cap, D] view of one slot's keys."""
+        return self.k[layer][self.base(slot):self.base(slot) + self.slab].view(
+            self.n_kv_heads, self.cap, self.head_dim)
+
+    def v_view(self, layer, slot):
+        """[Hkv, D, cap] view of one slot's (transposed) values."""
+        return self.v[layer][self.base(slot):self.base(slot) + self.slab].view(
+            self.n_kv_heads, self.head_dim, self.cap)
+
+    def copy_slot(self, dst, src_ws, src_slot=0):
+        for l in range(self.n_layers):
+            self.k_view(l, dst).copy_(src_ws.k_view(l, src_slot))
+            self.v_view(l, dst).copy_(src_ws.v_view(l, src_slot))
+
+
+class RaggedStage:
+    """One pipeline stage of GPT-OSS decoder layers on libflyai_stage."""
+
+    def __init__(self, shape: GptOssShape, layers, rotary, kv: KVWorkspace, max_tokens, max_seqs,
+                 max_attn_items=None, split_keys=512, device="cuda"):
+        self.shape, self.layers, self.rotary, self.kv = shape, layers, rotary, kv
+        self.device = torch.device(device)
+        self.max_tokens, self.max_seqs = max_tokens, max_seqs
+        if max_attn_items is None:
+            groups = (max_seqs + (max_tokens + 3) // 4) * shape.n_kv_heads
+            max_attn_items = groups * max(1, -(-kv.cap // split_keys))
+        cfg = _lib.StageConfig(
+            n_layers=len(layers), hidden=shape.hidden, n_q_heads=shape.n_q_heads,
+            n_kv_heads=shape.n_kv_heads, head_dim=shape.head_dim, n_experts=shape.n_experts,
+            top_k=shape.top_k, intermediate=shape.intermediate, window=shape.window,
+            max_tokens=max_tokens, max_seqs=max_seqs, max_attn_items=max_attn_items,
+            rope_positions=rotary.n_positions, attn_split_keys=split_keys, rms_eps=shape.rms_eps)
+        handle = C.c_void_p()
+        check(lib().flyai_stage_create(C.byref(cfg), C.byref(handle)))
+        self._h = handle
+        self._keep = []
+        for i, lw in enumerate(layers):
+            d = _lib.LayerDesc(
+                ln1=lw.ln1.data_ptr(), ln2=lw.ln2.data_ptr(), wqkv=lw.wqkv.data_ptr(),
+                bqkv=lw.bqkv.data_ptr(), wo=lw.wo.data_ptr(), bo=lw.bo.data_ptr(),
+                sinks=lw.sinks.data_ptr(), router_w=lw.router_w.data_ptr(),
+                router_b=lw.router_b.data_ptr(), w13_packed=lw.w13_packed.data_ptr(),
+                b13=lw.b13.data_ptr(), w2_packed=lw.w2_packed.data_ptr(), b2=lw.b2.data_ptr(),
+                k_pool=kv.k[i].data_ptr(), v_pool=kv.v[i].data_ptr(), sliding=int(lw.sliding), pad=0)
+            check(lib().flyai_stage_set_layer(self._h, i, C.byref(d)))
+        check(lib().flyai_stage_set_rope(self._h, C.c_void_p(rotary.cos.data_ptr()),
+                                         C.c_void_p(rotary.sin.data_ptr())))
+        dev_bytes = int(lib().flyai_stage_workspace_bytes(self._h))
+        host_bytes = int(lib().flyai_stage_host_staging_bytes(self._h))
+        self.workspace = torch.empty(dev_bytes + 256, dtype=torch.uint8, device=self.device)
+        off = (-self.workspace.data_ptr()) % 256
+        self._ws_ptr = self.workspace.data_ptr() + off
+        self.staging = torch.empty(host_bytes, dtype=torch.uint8, pin_memory=True)
+        check(lib().flyai_stage_set_workspace(self._h, C.c_void_p(self._ws_ptr), dev_bytes,
+                                              C.c_void_p(self.staging.data_ptr()), host_bytes))
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            try:
+                torch.cuda.synchronize(self.device)
+            except Exception:
+                pass
+            lib().flyai_stage_destroy(h)
+            self._h = None
+
+    def forward(self, hidden, q_lens, starts, slots):
+        """hidden bf16 [T, H] (packed token order, updated in place and returned); q_lens/starts/slots
+        per sequence (host ints).  Raises ContextOverflow before any write."""
+        S = len(q_lens)
+        if not (len(starts) == S == len(slots)):
+            raise ValueError("q_lens, starts and slots must have one entry per sequence")
+        T = int(sum(int(q) for q in q_lens))
+        if hidden.dtype != torch.bfloat16 or not hidden.is_contiguous() or tuple(hidden.shape) != (T, self.shape.hidden):
+            raise ValueError(f"hidden must be contiguous bf16 [{T}, {self.shape.hidden}]")
+        for s in slots:
+            if not 0 <= int(s) < self.kv.n_slots:
+                raise ValueError(f"slot {s} out of range")
+        ql = np.ascontiguousarray(q_lens, dtype=np.int32)
+        st = np.ascontiguousarray(starts, dtype=np.int32)
+        base = np.ascontiguousarray([self.kv.base(int(s)) for s in slots], dtype=np.int64)
+        cap = np.full(S, self.kv.cap, dtype=np.int32)
+        need = st.astype(np.int64) + ql
+        if np.any(need > self.kv.maxlen):
+            b = int(np.argmax(need > self.kv.maxlen))
+            raise ContextOverflow(_lib.FLYAI_ERANGE, f"sequence {b} needs {int(need[b])} positions > max_ctx {self.kv.maxlen}")
+        check(lib().flyai_stage_forward(
+            self._h, ql.ctypes.data_as(C.c_void_p), st.ctypes.data_as(C.c_void_p),
+            base.ctypes.data_as(C.c_void_p), cap.ctypes.data_as(C.c_void_p), S,
+            C.c_void_p(hidden.data_ptr()), C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)))
+        return hidden
+
+    def debug_buffer(self, which, dtype, shape):
+        """A view of an internal buffer of the last step (tests only); see flyai_stage.h."""
+        ptr = lib().flyai_stage_debug_buffer(self._h, which)
+        off = ptr - self.workspace.data_ptr()
+        n = int(np.prod(shape)) * torch.tensor([], dtype=dtype).element_size()
+        return self.workspace[off:off + n].view(dtype).view(*shape)
+
+
+def _parts_shape(parts):
+    return parts.get("shape") or GptOssShape()
+
+
+class FastVerifyStage:
+    """Drop-in for ``FastVerify(parts, maxlen, dev)`` (phase0/fastverify.py:80-309), B = 1.
+
+    ``parts`` keys read: ``layers`` (LayerWeights), ``rotary`` (YarnRotary), ``shape`` (GptOssShape);
+    ``sliding``/``window`` are carried by the layers and the shape.  ``decode`` returns a buffer the
+    runtime owns and reuses on the next call (as the graph output is in the reference)."""
+
+    DECODE_BUCKETS = (2048, 4096, 8192, 16384, 32768, 65536, 131072)
+
+    def __init__(self, parts, maxlen=2048, dev="cuda", max_tokens=4096):
+        self.parts, self.maxlen, self.dev = parts, maxlen, dev
+        self.shape = _parts_shape(parts)
+        self.layers = parts["layers"]
+        self.n_layers = len(self.layers)
+        self.hidden = self.shape.hidden
+        self.cache = KVWorkspace(self.n_layers, 1, maxlen, self.shape.n_kv_heads, self.shape.head_dim, dev)
+        self.stage = RaggedStage(self.shape, self.layers, parts["rotary"], self.cache, max_tokens, 1, device=dev)
+        self.out = None
+
+    def reset(self):
+        self.cache.zero()
+
+    def _run(self, h, start):
+        n = h.shape[1]
+        if start + n > self.maxlen:
+            raise ContextOverflow(_lib.FLYAI_ERANGE, f"needs {start + n} positions > max_ctx {self.maxlen} (raise --max-ctx)")
+        flat = h.reshape(n, self.hidden).to(torch.bfloat16).contiguous().clone()
+        self.stage.forward(flat, [n], [start], [0])
+        return flat.view(1, n, self.hidden)
+
+    def prefill(self, h, start):
+        return self._run(h, start)
+
+    def decode(self, h, start):
+        self.out = self._run(h, start)
+        return self.out
+
+    def tree_decode(self, h, start, par, dep):
+        raise NotImplementedError("tree verify needs ancestor masks; the ragged kernel is causal-only")
+
+    def tree_gather(self, start, keep):
+        """Compact the accepted path's KV (scratch slots start+keep[i]) to start+i, every layer
+        (fastverify.py:301-309)."""
+        src = torch.tensor([start + k for k in keep], device=self.dev)
+        dst = torch.arange(start, start + len(keep), device=self.dev)
+        for l in range(self.n_layers):
+            kk, vv = self.cache.k_view(l, 0), self.cache.v_view(l, 0)
+            kk.index_copy_(1, dst, kk.index_select(1, src))
+            vv.index_copy_(2, dst, vv.index_select(2, src))
+
+
+class BatchedFastVerifyStage:
+    """Drop-in for ``BatchedFastVerify(parts, B, maxlen, dev)`` (phase0/batchverify.py:64-190).
+
+    Every stream is one ragged sequence of kp1 tokens at its own start; per-stream KV slabs and the
+    per-row order-fixed MoE make each stream's output independent of its batch mates."""
+
+    DECODE_BUCKETS = FastVerifyStage.DECODE_BUCKETS
+
+    def __init__(self, parts, B, maxlen=2048, dev="cuda", lossless=False, max_tokens=None):
+        self.parts, self.B, self.maxlen, self.dev = parts, B, maxlen, dev
+        self.shape = _parts_shape(parts)
+        self.layers = parts["layers"]
+        self.n_layers = len(self.layers)
+        self.hidden = self.shape.hidden
+        self.cache = KVWorkspace(self.n_layers, B, maxlen, self.shape.n_kv_heads, self.shape.head_dim, dev)
+        self.stage = RaggedStage(self.shape, self.layers, parts["rotary"], self.cache,
+                                 max_tokens or 64 * B, B, device=dev)
+        self.out = None
+
+    def reset(self):
+        self.cache.zero()
+
+    def load_prefix(self, b, src_cache):
+        """Copy a solo runtime's committed KV (its KVWorkspace, slot 0) into stream b."""
+        self.cache.copy_slot(b, src_cache, 0)
+
+    def decode(self, h, starts, use_graph=True):
+        B, kp1, H = h.shape
+        if B != self.B:
+            raise ValueError(f"expected {self.B} streams, got {B}")
+        st = [int(v) for v in (starts.tolist() if torch.is_tensor(starts) else starts)]
+        need = max(st) + kp1
+        if need > self.maxlen:
+            raise ContextOverflow(_lib.FLYAI_ERANGE, f"batched decode needs {need} positions > max_ctx {self.maxlen}")
+        flat = h.reshape(B * kp1, H).to(torch.bfloat16).contiguous().clone()
+        self.stage.forward(flat, [kp1] * B, st, list(range(B)))
+        self.out = flat.view(B, kp1, H)
+        return self.out

@@ -1,0 +1,234 @@
+/*
+ * flyai_stage.h -- C ABI of the MI355X (gfx950) stage-step library libflyai_stage.so.
+ *
+ * One pipeline stage's continuous-batch forward step for a GPT-OSS-120B-shaped MXFP4 MoE model:
+ * ragged packing, router top-k + histogram + permute + combine, MXFP4 expert GEMMs, ragged GQA
+ * attention with sinks and a sliding window, and the layer glue around them.
+ *
+ * Conventions
+ *   - Every pointer named *_dev / every tensor argument is DEVICE memory unless the name ends in
+ *     _host.  bf16 tensors are passed as uint16_t bit patterns, row-major, densely packed.
+ *   - Every launch takes an explicit stream (a hipStream_t, passed as void*; NULL = null stream).
+ *   - Return value: 0 on success, a negative FLYAI_E* code on error; flyai_last_error() gives a
+ *     message.  Shapes are validated on the host before any launch; nothing aborts the process.
+ *   - The library allocates no device memory: scratch comes from caller-provided workspaces whose
+ *     sizes the *_bytes functions report.  A stage handle is not thread-safe (one per worker thread,
+ *     matching the reference's one ContinuousRingWorker thread per ring,
+ *     shard/continuous_batch.py:98-156).
+ */
+#ifndef FLYAI_STAGE_H
+#define FLYAI_STAGE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* flyai_stream_t;
+
+#define FLYAI_OK 0
+#define FLYAI_EINVAL -1   /* bad shape / argument */
+#define FLYAI_ERANGE -2   /* context or capacity overflow (reference: ContextOverflow,
+                             phase0/fastverify.py:23-26), raised before any write */
+#define FLYAI_EHIP -3     /* a HIP runtime call failed */
+
+#define FLYAI_ABI_VERSION 1
+
+/* Last error message of the calling thread ("" when none). */
+const char* flyai_last_error(void);
+int flyai_abi_version(void);
+
+/* ---- a1: ragged packing ----------------------------------------------------------------------
+ * Replaces the per-stream position/mask construction of BatchedFastVerify._set
+ * (phase0/batchverify.py:149-158, :51-61) and FastVerify._set (phase0/fastverify.py:170-183) with a
+ * flat token axis.  Inputs per sequence b (device): q_lens[b] >= 1, starts[b] (committed length =
+ * position of its first query token), kv_base[b] (element offset of the sequence's K/V slab in a
+ * pool), kv_cap[b] (slab capacity in positions).  Outputs: cu_seqlens[S+1], positions[T],
+ * seq_id[T], kv_len[S] = starts+q_lens, kv_slot[T] = kv_base + position*head_dim.
+ * *status_dev gets bit 0 set if any kv_len > kv_cap (those tokens get kv_slot = -1) and bit 1 if
+ * T > max_tokens (nothing past max_tokens is written). */
+int flyai_pack_ragged(const int32_t* q_lens, const int32_t* starts, const int64_t* kv_base,
+                      const int32_t* kv_cap, int32_t n_seqs, int32_t head_dim, int32_t max_tokens,
+                      int32_t* cu_seqlens, int32_t* positions, int32_t* seq_id, int32_t* kv_len,
+                      int64_t* kv_slot, int32_t* status_dev, flyai_stream_t stream);
+
+/* ---- a2: router --------------------------------------------------------------------------------
+ * GPT-OSS top-k softmax router; replaces GptOssTopKRouter.forward
+ * (transformers/models/gpt_oss/modeling_gpt_oss.py:126-130) and the native path's bf16 router
+ * Linear + hub `routing` (transformers/integrations/mxfp4.py:484-487, torch restatement
+ * routing_torch_dist :435-444).  x bf16 [T,H], w bf16 [E,H], b bf16 [E].  Logits are the bf16
+ * rounding of an fp32 dot product in a fixed order (64 lane partials k = l + 64j, xor butterfly)
+ * plus bias; top-k by (value desc, id asc); softmax over the k selected values in fp32; each row's
+ * ids sorted ascending with their weights.  H % 64 == 0, H <= 7168, E <= 256, k <= 8.
+ * logits_out (fp32 [T,E], may be NULL) receives the bf16-valued logits. */
+int flyai_router_topk_softmax(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t T,
+                              int32_t H, int32_t E, int32_t k, int32_t* topk_ids, float* topk_w,
+                              float* logits_out, flyai_stream_t stream);
+
+/* ---- a3: expert histogram + stable permute -----------------------------------------------------
+ * Replaces routing_torch_dist's histc / stable argsort / inverse argsort
+ * (transformers/integrations/mxfp4.py:449-457) and the one_hot/where expert loop of
+ * GptOssExperts.forward (modeling_gpt_oss.py:93-107).  topk_ids int32 [T*k] in [0,E).
+ * hist[E], offsets[E+1] (exclusive scan), perm[T*k] (experts ascending, flat index ascending
+ * within an expert), inv[T*k] (inverse).  T*k <= 65536, E <= 256. */
+int flyai_moe_permute(const int32_t* topk_ids, int32_t T, int32_t k, int32_t E, int32_t* hist,
+                      int32_t* offsets, int32_t* perm, int32_t* inv, flyai_stream_t stream);
+
+/* ---- a4: unpermute / combine -------------------------------------------------------------------
+ * Replaces the weighted index_add_ of GptOssExperts.forward (modeling_gpt_oss.py:108-113) / the
+ * gammas scatter of matmul_ogs (transformers/integrations/mxfp4.py:394-403) and the residual add
+ * (modeling_gpt_oss.py:375).  out[t] = bf16(sum_s topk_w[t,s] * y_perm[inv[t*k+s]]) in fp32, slot
+ * order; when residual is non-NULL, out[t] = bf16(residual[t] + that) (residual may equal out). */
+int flyai_moe_combine(const float* y_perm, const int32_t* inv, const float* topk_w, int32_t T,
+                      int32_t k, int32_t H, const uint16_t* residual, uint16_t* out,
+                      flyai_stream_t stream);
+
+/* ---- a5: MXFP4 weight format -------------------------------------------------------------------
+ * The HF/GPT-OSS checkpoint layout (Mxfp4GptOssExperts, transformers/integrations/mxfp4.py:349-365;
+ * checked by phase0/mxfp4_guard.py:223-276): blocks u8 [E, N, K/32, 16] (E2M1 pairs, low nibble =
+ * even element), scales u8 [E, N, K/32] (E8M0).  The expert kernels read a one-time re-packed
+ * tile layout with identical values: flyai_mxfp4_repack converts on the device (N % 16 == 0,
+ * K % 32 == 0).  flyai_mxfp4_packed_bytes gives the packed size for all E experts. */
+size_t flyai_mxfp4_packed_bytes(int32_t E, int32_t N, int32_t K);
+int flyai_mxfp4_repack(const uint8_t* blocks, const uint8_t* scales, int32_t E, int32_t N,
+                       int32_t K, uint8_t* packed, flyai_stream_t stream);
+
+/* ---- a6: MXFP4 expert FFN (GPT-OSS SwiGLU) -------------------------------------------------------
+ * Replaces Mxfp4GptOssExperts.forward's two matmul_ogs calls (transformers/integrations/
+ * mxfp4.py:372-403) and GptOssExperts.forward/_apply_gate (modeling_gpt_oss.py:82-88, :108-111).
+ * gate_up: for permuted row p of expert e (offsets[e] <= p < offsets[e+1]), token t = perm[p]/k:
+ *   gu = x[t] . W13[e]^T + b13[e] (fp32), rows 2j/2j+1 = gate/up of unit j,
+ *   h[p, j] = bf16((clamp(up,-7,7)+1) * min(gate,7) * sigmoid(1.702*min(gate,7))).
+ * down: y_perm[p] = h[p] . W2[e]^T + b2[e] (fp32).
+ * x bf16 [T,H]; w13_packed/w2_packed from flyai_mxfp4_repack; b13 fp32 [E,2I]; b2 fp32 [E,H];
+ * h bf16 [T*k, I]; y_perm fp32 [T*k, H].  Groups of any row count are handled: MFMA on
+ * dequantised tiles for every group (16 rows per MFMA tile). */
+int flyai_moe_gate_up_mxfp4(const uint16_t* x, const int32_t* perm, const int32_t* offsets,
+                            int32_t k, const uint8_t* w13_packed, const float* b13, int32_t E,
+                            int32_t H, int32_t I, uint16_t* h, flyai_stream_t stream);
+int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, const uint8_t* w2_packed,
+                         const float* b2, int32_t E, int32_t H, int32_t I, float* y_perm,
+                         flyai_stream_t stream);
+
+/* ---- a9: layer glue ------------------------------------------------------------------------------
+ * RMSNorm: GptOssRMSNorm.forward (modeling_gpt_oss.py:57-62): y = bf16(w * (x * rsqrt(mean(x^2)+eps)))
+ * with fp32 weight.  Linear: q/k/v/o projections (modeling_gpt_oss.py:280-291): y = bf16(x W^T + b),
+ * W bf16 [N,K]; with residual non-NULL the result is bf16(residual + y) written to residual
+ * (the residual add of modeling_gpt_oss.py:369).  RoPE + KV append: GPT-OSS half-split rotary
+ * (modeling_gpt_oss.py:215-232) with per-op bf16 rounding, then the K/V write at each token's
+ * position (StaticKV.update, phase0/fastverify.py:71-77; BatchedStaticKV.update,
+ * phase0/batchverify.py:42-48).  KV pool layout per sequence slab (element offset kv_base[b]):
+ * K [Hkv][kv_cap[b]][D], V transposed [Hkv][D][kv_cap[b]].  cos_tab/sin_tab bf16
+ * [rope_positions][D/2]; a token whose position is outside the table or its slab is skipped. */
+int flyai_rmsnorm(const uint16_t* x, const float* w, int32_t T, int32_t H, float eps, uint16_t* y,
+                  flyai_stream_t stream);
+int flyai_linear_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t M, int32_t N,
+                      int32_t K, uint16_t* y, uint16_t* residual, flyai_stream_t stream);
+int flyai_rope_kv_append(const uint16_t* qkv, const int32_t* positions, const int32_t* seq_id,
+                         const uint16_t* cos_tab, const uint16_t* sin_tab, int32_t rope_positions,
+                         int32_t T, int32_t Hq, int32_t Hkv, int32_t D, const int64_t* kv_base,
+                         const int32_t* kv_cap, uint16_t* q_out, uint16_t* k_pool,
+                         uint16_t* v_pool, flyai_stream_t stream);
+
+/* ---- a8: ragged GQA attention with sinks and sliding window -------------------------------------
+ * Replaces eager_attention_forward (modeling_gpt_oss.py:235-263) over the additive masks of
+ * phase0/pipeline.py:38-48 / phase0/batchverify.py:51-61 and the bucketed StaticKV reads
+ * (phase0/fastverify.py:52-77).  Query token i of sequence b (position p = starts[b]+i) attends
+ * keys j in [lo, p], lo = 0 or max(0, p-window+1); logits scaled by D^-0.5; the per-head sink
+ * logit joins the softmax denominator only.  q bf16 [T,Hq,D] (rotated); out bf16 [T,Hq,D].
+ * Work is split over (sequence, kv head, group of <= 4 query tokens, key split); the host-side
+ * plan (flyai_attn_plan) is uploaded into `plan_dev` by the caller.  D == 64, Hq/Hkv == 8.
+ * Partials scratch: flyai_attn_partials_bytes(n_items). */
+typedef struct {
+  int32_t seq;      /* sequence index b */
+  int32_t kv_head;  /* g */
+  int32_t tok;      /* flat token index of the item's first query token */
+  int32_t ntok;     /* query tokens in the item (1..4) */
+  int32_t pos0;     /* position of the first query token */
+  int32_t key_lo;   /* key range [key_lo, key_hi) of this split */
+  int32_t key_hi;
+  int32_t group;    /* query group index (items of one group are consecutive) */
+} flyai_attn_item;
+
+typedef struct {
+  int32_t first_item; /* index of the group's first split item */
+  int32_t n_splits;
+  int32_t tok;        /* flat token index of the first query token */
+  int32_t ntok;
+  int32_t kv_head;
+  int32_t pad[3];
+} flyai_attn_group;
+
+int flyai_attn_plan(const int32_t* q_lens_host, const int32_t* starts_host, int32_t n_seqs,
+                    int32_t Hkv, int32_t window, int32_t split_keys, flyai_attn_item* items_host,
+                    int32_t max_items, flyai_attn_group* groups_host, int32_t max_groups,
+                    int32_t* n_items, int32_t* n_groups);
+size_t flyai_attn_partials_bytes(int32_t n_items);
+int flyai_attn_ragged(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                      const int64_t* kv_base, const int32_t* kv_cap, const float* sinks,
+                      int32_t window, int32_t Hq, int32_t Hkv, int32_t D,
+                      const flyai_attn_item* items_dev, int32_t n_items,
+                      const flyai_attn_group* groups_dev, int32_t n_groups, float* partials,
+                      uint16_t* out, flyai_stream_t stream);
+
+/* ---- a10: stage step driver ----------------------------------------------------------------------
+ * The per-layer loop of FastVerify._layers / BatchedFastVerify._layers (phase0/fastverify.py:116-122,
+ * phase0/batchverify.py:132-138) over GptOssDecoderLayer.forward (modeling_gpt_oss.py:347-376), for
+ * a ragged batch of decode / verify / prefill-chunk rows.  Weights and KV pools are caller-owned
+ * device memory bound once per layer; the step itself only launches kernels on `stream`. */
+typedef struct {
+  int32_t n_layers, hidden, n_q_heads, n_kv_heads, head_dim;
+  int32_t n_experts, top_k, intermediate, window;
+  int32_t max_tokens, max_seqs, max_attn_items, rope_positions, attn_split_keys;
+  float rms_eps;
+} flyai_stage_config;
+
+typedef struct {
+  const float* ln1;           /* fp32 [H] */
+  const float* ln2;           /* fp32 [H] */
+  const uint16_t* wqkv;       /* bf16 [(Hq+2Hkv)*D, H]: q_proj, k_proj, v_proj stacked */
+  const uint16_t* bqkv;       /* bf16 [(Hq+2Hkv)*D] */
+  const uint16_t* wo;         /* bf16 [H, Hq*D] */
+  const uint16_t* bo;         /* bf16 [H] */
+  const float* sinks;         /* fp32 [Hq] (bf16-valued) */
+  const uint16_t* router_w;   /* bf16 [E, H] */
+  const uint16_t* router_b;   /* bf16 [E] */
+  const uint8_t* w13_packed;  /* flyai_mxfp4_repack of gate_up blocks/scales */
+  const float* b13;           /* fp32 [E, 2I] */
+  const uint8_t* w2_packed;   /* flyai_mxfp4_repack of down blocks/scales */
+  const float* b2;            /* fp32 [E, H] */
+  uint16_t* k_pool;           /* this layer's K pool */
+  uint16_t* v_pool;           /* this layer's V pool (transposed slabs) */
+  int32_t sliding;            /* 1: sliding-window layer */
+  int32_t pad;
+} flyai_layer_desc;
+
+typedef struct flyai_stage flyai_stage;
+
+int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** out);
+void flyai_stage_destroy(flyai_stage* st);
+int flyai_stage_set_layer(flyai_stage* st, int32_t layer, const flyai_layer_desc* desc);
+int flyai_stage_set_rope(flyai_stage* st, const uint16_t* cos_tab, const uint16_t* sin_tab);
+size_t flyai_stage_workspace_bytes(const flyai_stage* st);
+size_t flyai_stage_host_staging_bytes(const flyai_stage* st);
+/* device workspace (>= workspace_bytes) and pinned host staging (>= host_staging_bytes) */
+int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t dev_bytes, void* host_pinned,
+                              size_t host_bytes);
+/* One step.  Batch description on the host (validated here; ContextOverflow -> FLYAI_ERANGE before
+ * any launch): per sequence q_lens, starts, kv_base (element offset of its slab in every layer's
+ * pools), kv_cap.  hidden: device bf16 [T, H] in packed token order, updated in place. */
+int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens_host, const int32_t* starts_host,
+                        const int64_t* kv_base_host, const int32_t* kv_cap_host, int32_t n_seqs,
+                        uint16_t* hidden, flyai_stream_t stream);
+/* Device pointer of an internal buffer of the last step (for tests): 0 xn, 1 qkv, 2 q_rot,
+ * 3 attn_out, 4 topk_ids, 5 topk_w, 6 offsets, 7 perm, 8 inv, 9 h_moe, 10 y_perm, 11 positions,
+ * 12 seq_id, 13 cu_seqlens. */
+void* flyai_stage_debug_buffer(flyai_stage* st, int32_t which);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLYAI_STAGE_H */

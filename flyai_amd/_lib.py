@@ -53,17 +53,19 @@ _PROTOS = {
     "flyai_pack_ragged": (C.c_int, [P, P, P, P, I32, I32, I32, P, P, P, P, P, P, P]),
     "flyai_router_topk_softmax": (C.c_int, [P, P, P, I32, I32, I32, I32, P, P, P, P]),
     "flyai_moe_permute": (C.c_int, [P, I32, I32, I32, P, P, P, P, P]),
+    "flyai_moe_route_permute": (C.c_int, [P, P, P, I32, I32, I32, I32, P, P, P, P, P, P, P, P]),
     "flyai_moe_combine": (C.c_int, [P, P, P, I32, I32, I32, P, P, P]),
     "flyai_mxfp4_packed_bytes": (SZ, [I32, I32, I32]),
     "flyai_mxfp4_repack": (C.c_int, [P, P, I32, I32, I32, P, P]),
     "flyai_moe_gate_up_mxfp4": (C.c_int, [P, P, P, I32, P, P, I32, I32, I32, P, P]),
     "flyai_moe_down_mxfp4": (C.c_int, [P, P, P, P, I32, I32, I32, P, P]),
     "flyai_rmsnorm": (C.c_int, [P, P, I32, I32, F32, P, P]),
-    "flyai_linear_bf16": (C.c_int, [P, P, P, I32, I32, I32, P, P, P]),
+    "flyai_linear_workspace_bytes": (SZ, [I32, I32, I32]),
+    "flyai_linear_bf16": (C.c_int, [P, P, P, I32, I32, I32, P, P, P, P]),
     "flyai_rope_kv_append": (C.c_int, [P, P, P, P, P, I32, I32, I32, I32, I32, P, P, P, P, P, P]),
-    "flyai_attn_plan": (C.c_int, [P, P, I32, I32, I32, I32, P, I32, P, I32, P, P]),
+    "flyai_attn_plan": (C.c_int, [P, P, I32, I32, I32, I32, P, I32, P, I32, P, P, P]),
     "flyai_attn_partials_bytes": (SZ, [I32]),
-    "flyai_attn_ragged": (C.c_int, [P, P, P, P, P, P, I32, I32, I32, I32, P, I32, P, I32, P, P, P]),
+    "flyai_attn_ragged": (C.c_int, [P, P, P, P, P, P, I32, I32, I32, I32, P, I32, I32, P, I32, P, P, P]),
     "flyai_stage_create": (C.c_int, [P, P]),
     "flyai_stage_destroy": (None, [P]),
     "flyai_stage_set_layer": (C.c_int, [P, I32, P]),

@@ -4,15 +4,19 @@
 // KV slab of sequence b at element offset kv_base[b] (caller-owned pools, kv_cap[b] % 64 == 0):
 //   K  [Hkv][cap][64]   (row per key)
 //   Vt [Hkv][64][cap]   (V transposed: row per head dim)
-// Work item = (sequence, kv head, <= 4 query tokens, key split).  Its 32 query rows (4 tokens x 8
-// heads of the GQA group) are processed by one wave with 16x16x32 bf16 MFMAs:
+// Work item = (sequence, kv head, <= 4 query tokens, key split).  Its query rows (tokens x the 8
+// heads of the GQA group, in tiles of 16) are processed by one wave with 16x16x32 bf16 MFMAs:
 //   S^T[16 keys][16 qrows] = K_tile . Q^T       (K as A operand, Q^T as B, head dim reduced)
 //   O^T[16 dims][16 qrows] += Vt_tile . P^T     (Vt as A operand, P^T as B, keys reduced)
-// The key order inside a 64-key block is permuted so that the S^T accumulator registers of a lane
-// are exactly the P^T operand the second MFMA needs (no shuffles): S^T tile kt, row m holds key
-// 16*(m/4) + 4*kt + m%4, so lane (qrow n, group g) holds keys 16g .. 16g+15 across the 4 tiles,
-// which is the contiguous 32-byte run of the Vt row it loads.
-// Each item writes (m, l, O[64]) per query row; a merge kernel folds the splits and the sink.
+// Operand orders are permuted (any order consistent between the two operands of a product is
+// valid) so that every 16-byte load instruction of the wave reads 64-byte contiguous runs:
+//   head dims: lane group g supplies dims 8g..8g+7 (step 0) and 32+8g..32+8g+7 (step 1);
+//   keys of a 64-key block: S^T tile kt, row m is key 32*(kt/2) + 8*(m/4) + 4*(kt%2) + m%4, so the
+//   C-layout registers of lane (qrow n, group g) hold keys 8g..8g+7 (tiles 0,1) and 32+8g..+7
+//   (tiles 2,3) -- exactly the P^T operand of the two PV steps and the two 16-byte Vt loads.
+// K of the next block is loaded while the current block computes.  Each item writes (m, l, O[64])
+// per query row; a merge kernel folds the splits and the sink.
+#include <limits.h>
 #include <math.h>
 #include <vector>
 
@@ -34,12 +38,40 @@ __device__ __forceinline__ uint4 mask_keys(uint4 v, int key0, int lo, int hi) {
   return make_uint4(w[0], w[1], w[2], w[3]);
 }
 
-__global__ __launch_bounds__(64) void attn_partial_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
-    const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
-    const int32_t* __restrict__ kv_cap, int window, int Hq,
-    const flyai_attn_item* __restrict__ items, float* __restrict__ partials) {
-  const flyai_attn_item it = items[blockIdx.x];
+__device__ __forceinline__ int tile_key(int kt, int m) {
+  return 32 * (kt >> 1) + 8 * (m >> 2) + 4 * (kt & 1) + (m & 3);
+}
+
+// Every 64-key block starts at a multiple of 64 below key_hi <= cap (cap % 64 == 0), so all 64 keys
+// are inside the slab: the loads below are unconditional (no branch between loads).
+__device__ __forceinline__ void load_k_tile(uint4 (&k)[4][2], const uint16_t* __restrict__ K, int kb,
+                                            int n, int g) {
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    const uint16_t* kp = K + (size_t)(kb + tile_key(kt, n)) * 64 + 8 * g;
+    k[kt][0] = *reinterpret_cast<const uint4*>(kp);
+    k[kt][1] = *reinterpret_cast<const uint4*>(kp + 32);
+  }
+}
+
+__device__ __forceinline__ void load_v_tile(uint4 (&v)[4][2], const uint16_t* __restrict__ Vt, int cap,
+                                            int kb, int n, int g) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+      v[dt][h] = *reinterpret_cast<const uint4*>(Vt + (size_t)(16 * dt + n) * cap + kb + 32 * h + 8 * g);
+}
+
+// QT query-row tiles of 16 (QT = 1: up to 2 tokens; QT = 2: up to 4 tokens).
+template <int QT>
+__device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_idx,
+                                          const uint16_t* __restrict__ q,
+                                          const uint16_t* __restrict__ k_pool,
+                                          const uint16_t* __restrict__ v_pool,
+                                          const int64_t* __restrict__ kv_base,
+                                          const int32_t* __restrict__ kv_cap, int window, int Hq,
+                                          float* __restrict__ partials) {
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
   const int cap = kv_cap[it.seq];
@@ -48,90 +80,79 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
   const uint16_t* Vt = v_pool + base;
   const float scale = 0.125f;  // 64 ** -0.5
 
-  // Q^T operand: qrow rq = 16*qt + n -> token rq/8, head kv_head*8 + rq%8; dims 16g .. 16g+15
-  bf16x8_t qf[2][2];
-  int qpos[2];
-  bool qval[2];
+  // Q^T operand: qrow rq = 16*qt + n -> token rq/8, head kv_head*8 + rq%8
+  bf16x8_t qf[QT][2];
+  int qpos[QT];
+  bool qval[QT];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     const int rq = 16 * qt + n;
     const int ti = rq >> 3;
     qval[qt] = ti < it.ntok;
     qpos[qt] = it.pos0 + ti;
     uint4 a = make_uint4(0, 0, 0, 0), b2 = make_uint4(0, 0, 0, 0);
     if (qval[qt]) {
-      const uint4* qp = reinterpret_cast<const uint4*>(
-          q + ((size_t)(it.tok + ti) * Hq + it.kv_head * 8 + (rq & 7)) * 64 + 16 * g);
-      a = qp[0];
-      b2 = qp[1];
+      const uint16_t* qp = q + ((size_t)(it.tok + ti) * Hq + it.kv_head * 8 + (rq & 7)) * 64 + 8 * g;
+      a = *reinterpret_cast<const uint4*>(qp);
+      b2 = *reinterpret_cast<const uint4*>(qp + 32);
     }
     qf[qt][0] = as_bf16x8(a);
     qf[qt][1] = as_bf16x8(b2);
   }
-  float m_run[2] = {-1e30f, -1e30f}, l_run[2] = {0.f, 0.f};
-  f32x4_t O[2][4];
+  float m_run[QT], l_run[QT];
+  f32x4_t O[QT][4];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -1e30f;
+    l_run[qt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) O[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const bool two_tiles = it.ntok > 2;
+  }
 
-  for (int kb = it.key_lo & ~63; kb < it.key_hi; kb += 64) {
-    // K tiles (A operand): lane row n of tile kt is key kb + 16*(n/4) + 4*kt + n%4
-    uint4 ka[4][2];
+  const int kb_first = it.key_lo & ~63;
+  // Blocks fully inside every valid query row's key range need no score mask (wave-uniform test).
+  const int pos_last = it.pos0 + it.ntok - 1;
+  const int int_lo = max(it.key_lo, window > 0 ? pos_last - window + 1 : 0);
+  const int int_hi = min(it.key_hi - 1, it.pos0);
+  uint4 kc[4][2], kn[4][2], vv[4][2];
+  load_k_tile(kc, K, kb_first, n, g);
+  for (int kb = kb_first; kb < it.key_hi; kb += 64) {
+    load_v_tile(vv, Vt, cap, kb, n, g);
+    const bool more = kb + 64 < it.key_hi;
+    if (more) load_k_tile(kn, K, kb + 64, n, g);
+    const bool interior = kb >= int_lo && kb + 63 <= int_hi;
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const int key = kb + 16 * (n >> 2) + 4 * kt + (n & 3);
-      if (key < it.key_hi) {
-        const uint4* kp = reinterpret_cast<const uint4*>(K + (size_t)key * 64 + 16 * g);
-        ka[kt][0] = kp[0];
-        ka[kt][1] = kp[1];
-      } else {
-        ka[kt][0] = make_uint4(0, 0, 0, 0);
-        ka[kt][1] = make_uint4(0, 0, 0, 0);
-      }
-    }
-    // Vt tiles (A operand of the PV product): lane row n = dim 16*dt + n, keys kb + 16g .. +15
-    uint4 va[4][2];
-    const int vkey0 = kb + 16 * g;
-    const bool vfull = vkey0 >= it.key_lo && vkey0 + 16 <= it.key_hi;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      if (vkey0 < it.key_hi) {
-        const uint4* vp = reinterpret_cast<const uint4*>(Vt + (size_t)(16 * dt + n) * cap + vkey0);
-        va[dt][0] = vp[0];
-        va[dt][1] = vp[1];
-        if (!vfull) {
-          va[dt][0] = mask_keys(va[dt][0], vkey0, it.key_lo, it.key_hi);
-          va[dt][1] = mask_keys(va[dt][1], vkey0 + 8, it.key_lo, it.key_hi);
-        }
-      } else {
-        va[dt][0] = make_uint4(0, 0, 0, 0);
-        va[dt][1] = make_uint4(0, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
-      if (qt == 1 && !two_tiles) break;
+    for (int qt = 0; qt < QT; ++qt) {
       f32x4_t s[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-        s[kt] = mfma16x16x32(as_bf16x8(ka[kt][0]), qf[qt][0], f32x4_t{0.f, 0.f, 0.f, 0.f});
-        s[kt] = mfma16x16x32(as_bf16x8(ka[kt][1]), qf[qt][1], s[kt]);
+        s[kt] = mfma16x16x32(as_bf16x8(kc[kt][0]), qf[qt][0], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        s[kt] = mfma16x16x32(as_bf16x8(kc[kt][1]), qf[qt][1], s[kt]);
       }
-      // lane holds S^T[key kb + 16g + 4kt + v][qrow n]
-      const int p = qpos[qt];
-      const int lo = window > 0 ? max(0, p - window + 1) : 0;
+      // lane holds S^T[key kb + tile_key(kt, 4g + v)][qrow n]
       float bmax = -INFINITY;
+      if (interior && qval[qt]) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int key = kb + 16 * g + 4 * kt + v;
-          const bool ok = qval[qt] && key >= lo && key <= p && key >= it.key_lo && key < it.key_hi;
-          s[kt][v] = ok ? s[kt][v] * scale : -INFINITY;
-          bmax = fmaxf(bmax, s[kt][v]);
-        }
+          for (int v = 0; v < 4; ++v) {
+            s[kt][v] *= scale;
+            bmax = fmaxf(bmax, s[kt][v]);
+          }
+      } else {
+        const int p = qpos[qt];
+        const int lo = max(it.key_lo, window > 0 ? p - window + 1 : 0);
+        const int hi = min(p, it.key_hi - 1);
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int key = kb + tile_key(kt, 4 * g + v);
+            const bool ok = qval[qt] && key >= lo && key <= hi;
+            s[kt][v] = ok ? s[kt][v] * scale : -INFINITY;
+            bmax = fmaxf(bmax, s[kt][v]);
+          }
+      }
       bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
       bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
       const float m_new = fmaxf(m_run[qt], bmax);
@@ -149,23 +170,38 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
           pt[kt >> 1][(kt & 1) * 4 + v] = __builtin_bit_cast(__bf16, pb);
         }
       l_run[qt] = l_run[qt] * alpha + lsum;
+      if (qt == 0 && kb + 64 > it.key_hi) {
+        // keys at or past key_hi may be unwritten (even non-finite): zero their values, P is 0 there
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt)
+            vv[dt][h] = mask_keys(vv[dt][h], kb + 32 * h + 8 * g, INT_MIN, it.key_hi);
+      }
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
         O[qt][dt] *= alpha;
-        O[qt][dt] = mfma16x16x32(as_bf16x8(va[dt][0]), pt[0], O[qt][dt]);
-        O[qt][dt] = mfma16x16x32(as_bf16x8(va[dt][1]), pt[1], O[qt][dt]);
+        O[qt][dt] = mfma16x16x32(as_bf16x8(vv[dt][0]), pt[0], O[qt][dt]);
+        O[qt][dt] = mfma16x16x32(as_bf16x8(vv[dt][1]), pt[1], O[qt][dt]);
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+        kc[kt][0] = kn[kt][0];
+        kc[kt][1] = kn[kt][1];
       }
     }
   }
   // partial record per query row: [m, l, O[64]]; O^T layout: lane holds dims 16dt + 4g + v of qrow n
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     float l = l_run[qt];
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     const int rq = 16 * qt + n;
     if (!qval[qt]) continue;
-    float* rec = partials + ((size_t)blockIdx.x * kAttnRows + rq) * kPartFloats;
+    float* rec = partials + ((size_t)item_idx * kAttnRows + rq) * kPartFloats;
     if (g == 0) {
       rec[0] = m_run[qt];
       rec[1] = l;
@@ -175,6 +211,19 @@ __global__ __launch_bounds__(64) void attn_partial_kernel(
 #pragma unroll
       for (int v = 0; v < 4; ++v) rec[2 + 16 * dt + 4 * g + v] = O[qt][dt][v];
   }
+}
+
+// One launch for every item; the body is chosen per item (uniform across the wave).
+__global__ __launch_bounds__(64, 2) void attn_partial_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
+    const int32_t* __restrict__ kv_cap, int window, int Hq,
+    const flyai_attn_item* __restrict__ items, float* __restrict__ partials) {
+  const flyai_attn_item it = items[blockIdx.x];
+  if (it.ntok <= 2)
+    attn_item<1>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials);
+  else
+    attn_item<2>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials);
 }
 
 // Merge: per query row, M = max(sink, max_s m_s), L = e^(sink-M) + sum_s l_s e^(m_s-M),
@@ -212,11 +261,13 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
 
 int launch_attn(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
                 const int64_t* kv_base, const int32_t* kv_cap, const float* sinks, int window,
-                int Hq, const flyai_attn_item* items, int n_items, const flyai_attn_group* groups,
-                int n_groups, float* partials, uint16_t* out, hipStream_t s) {
+                int Hq, const flyai_attn_item* items, int n_items, int n_small,
+                const flyai_attn_group* groups, int n_groups, float* partials, uint16_t* out,
+                hipStream_t s) {
   if (n_items == 0) return FLYAI_OK;
-  hipLaunchKernelGGL(attn_partial_kernel, dim3(n_items), dim3(64), 0, s, q, k_pool, v_pool,
-                     kv_base, kv_cap, window, Hq, items, partials);
+  (void)n_small;  // the plan's two ranges share one launch
+  hipLaunchKernelGGL(attn_partial_kernel, dim3(n_items), dim3(64), 0, s, q, k_pool, v_pool, kv_base,
+                     kv_cap, window, Hq, items, partials);
   int rc = check_launch("attn_partial");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_merge_kernel, dim3(n_groups), dim3(256), 0, s, partials, groups, sinks,
@@ -224,47 +275,54 @@ int launch_attn(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_poo
   return check_launch("attn_merge");
 }
 
+// Groups of <= 2 query tokens (one 16-row tile) are emitted first, then the larger ones, so the two
+// kernel variants each take one contiguous item range; a group's splits stay consecutive.
 int attn_plan(const int32_t* q_lens, const int32_t* starts, int S, int Hkv, int window,
               int split_keys, flyai_attn_item* items, int max_items, flyai_attn_group* groups,
-              int max_groups, int* n_items, int* n_groups) {
-  int ni = 0, ng = 0, tok = 0;
-  for (int b = 0; b < S; ++b) {
-    const int ql = q_lens[b], st = starts[b];
-    for (int i0 = 0; i0 < ql; i0 += 4) {
-      const int nt = ql - i0 < 4 ? ql - i0 : 4;
-      const int p_first = st + i0, p_last = st + i0 + nt - 1;
-      const int key_hi = p_last + 1;
-      const int key_lo = window > 0 ? (p_first - window + 1 > 0 ? p_first - window + 1 : 0) : 0;
-      const int kb0 = key_lo & ~63;
-      const int nsplit = (key_hi - kb0 + split_keys - 1) / split_keys;
-      for (int g = 0; g < Hkv; ++g) {
-        if (ng >= max_groups || ni + nsplit > max_items)
-          return set_error(FLYAI_ERANGE, "attention plan exceeds capacity (%d items, %d groups)",
-                           max_items, max_groups);
-        flyai_attn_group& gr = groups[ng];
-        gr.first_item = ni;
-        gr.n_splits = nsplit;
-        gr.tok = tok + i0;
-        gr.ntok = nt;
-        gr.kv_head = g;
-        gr.pad[0] = gr.pad[1] = gr.pad[2] = 0;
-        for (int sp = 0; sp < nsplit; ++sp) {
-          flyai_attn_item& it = items[ni++];
-          it.seq = b;
-          it.kv_head = g;
-          it.tok = tok + i0;
-          it.ntok = nt;
-          it.pos0 = p_first;
-          const int lo = kb0 + sp * split_keys;
-          it.key_lo = lo > key_lo ? lo : key_lo;
-          const int hi = kb0 + (sp + 1) * split_keys;
-          it.key_hi = hi < key_hi ? hi : key_hi;
-          it.group = ng;
+              int max_groups, int* n_items, int* n_groups, int* n_small) {
+  int ni = 0, ng = 0;
+  for (int pass = 0; pass < 2; ++pass) {
+    if (pass == 1) *n_small = ni;
+    int tok = 0;
+    for (int b = 0; b < S; ++b) {
+      const int ql = q_lens[b], st = starts[b];
+      for (int i0 = 0; i0 < ql; i0 += 4) {
+        const int nt = ql - i0 < 4 ? ql - i0 : 4;
+        if ((nt <= 2) != (pass == 0)) continue;
+        const int p_first = st + i0, p_last = st + i0 + nt - 1;
+        const int key_hi = p_last + 1;
+        const int key_lo = window > 0 ? (p_first - window + 1 > 0 ? p_first - window + 1 : 0) : 0;
+        const int kb0 = key_lo & ~63;
+        const int nsplit = (key_hi - kb0 + split_keys - 1) / split_keys;
+        for (int g = 0; g < Hkv; ++g) {
+          if (ng >= max_groups || ni + nsplit > max_items)
+            return set_error(FLYAI_ERANGE, "attention plan exceeds capacity (%d items, %d groups)",
+                             max_items, max_groups);
+          flyai_attn_group& gr = groups[ng];
+          gr.first_item = ni;
+          gr.n_splits = nsplit;
+          gr.tok = tok + i0;
+          gr.ntok = nt;
+          gr.kv_head = g;
+          gr.pad[0] = gr.pad[1] = gr.pad[2] = 0;
+          for (int sp = 0; sp < nsplit; ++sp) {
+            flyai_attn_item& it = items[ni++];
+            it.seq = b;
+            it.kv_head = g;
+            it.tok = tok + i0;
+            it.ntok = nt;
+            it.pos0 = p_first;
+            const int lo = kb0 + sp * split_keys;
+            it.key_lo = lo > key_lo ? lo : key_lo;
+            const int hi = kb0 + (sp + 1) * split_keys;
+            it.key_hi = hi < key_hi ? hi : key_hi;
+            it.group = ng;
+          }
+          ++ng;
         }
-        ++ng;
       }
+      tok += ql;
     }
-    tok += ql;
   }
   *n_items = ni;
   *n_groups = ng;
@@ -279,15 +337,16 @@ extern "C" int flyai_attn_plan(const int32_t* q_lens_host, const int32_t* starts
                                int32_t n_seqs, int32_t Hkv, int32_t window, int32_t split_keys,
                                flyai_attn_item* items_host, int32_t max_items,
                                flyai_attn_group* groups_host, int32_t max_groups, int32_t* n_items,
-                               int32_t* n_groups) {
+                               int32_t* n_groups, int32_t* n_items_small) {
   FLYAI_REQUIRE(n_seqs >= 0 && Hkv > 0 && window >= 0 && split_keys >= 64 && split_keys % 64 == 0,
                 "attn_plan: split_keys must be a positive multiple of 64");
-  FLYAI_REQUIRE(q_lens_host && starts_host && items_host && groups_host && n_items && n_groups,
+  FLYAI_REQUIRE(q_lens_host && starts_host && items_host && groups_host && n_items && n_groups &&
+                    n_items_small,
                 "attn_plan: null pointer");
   for (int b = 0; b < n_seqs; ++b)
     FLYAI_REQUIRE(q_lens_host[b] >= 1 && starts_host[b] >= 0, "attn_plan: bad q_len/start at %d", b);
   return attn_plan(q_lens_host, starts_host, n_seqs, Hkv, window, split_keys, items_host, max_items,
-                   groups_host, max_groups, n_items, n_groups);
+                   groups_host, max_groups, n_items, n_groups, n_items_small);
 }
 
 extern "C" size_t flyai_attn_partials_bytes(int32_t n_items) {
@@ -298,13 +357,16 @@ extern "C" int flyai_attn_ragged(const uint16_t* q, const uint16_t* k_pool, cons
                                  const int64_t* kv_base, const int32_t* kv_cap, const float* sinks,
                                  int32_t window, int32_t Hq, int32_t Hkv, int32_t D,
                                  const flyai_attn_item* items_dev, int32_t n_items,
-                                 const flyai_attn_group* groups_dev, int32_t n_groups,
-                                 float* partials, uint16_t* out, flyai_stream_t stream) {
+                                 int32_t n_items_small, const flyai_attn_group* groups_dev,
+                                 int32_t n_groups, float* partials, uint16_t* out,
+                                 flyai_stream_t stream) {
   FLYAI_REQUIRE(D == 64 && Hkv > 0 && Hq == 8 * Hkv, "attn: needs head_dim 64 and 8 query heads per kv head");
-  FLYAI_REQUIRE(n_items >= 0 && n_groups >= 0 && window >= 0, "attn: bad counts");
+  FLYAI_REQUIRE(n_items >= 0 && n_groups >= 0 && window >= 0 && n_items_small >= 0 &&
+                    n_items_small <= n_items,
+                "attn: bad counts");
   FLYAI_REQUIRE(q && k_pool && v_pool && kv_base && kv_cap && sinks && out &&
                     (n_items == 0 || (items_dev && groups_dev && partials)),
                 "attn: null pointer");
   return launch_attn(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, items_dev, n_items,
-                     groups_dev, n_groups, partials, out, as_stream(stream));
+                     n_items_small, groups_dev, n_groups, partials, out, as_stream(stream));
 }

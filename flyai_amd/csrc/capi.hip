@@ -5,6 +5,7 @@
 
 #include <new>
 #include <string>
+#include <vector>
 
 #include "common.h"
 
@@ -30,23 +31,26 @@ int check_launch(const char* what) {
 int launch_router(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int, int, int32_t*,
                   float*, float*, hipStream_t);
 int launch_permute(const int32_t*, int, int, int, int32_t*, int32_t*, int32_t*, int32_t*, hipStream_t);
+int launch_route_permute(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int, int, int32_t*,
+                         float*, float*, int32_t*, int32_t*, int32_t*, int32_t*, hipStream_t);
 int launch_combine(const float*, const int32_t*, const float*, int, int, int, const uint16_t*,
-                   uint16_t*, hipStream_t);
+                   uint16_t*, const float*, float, uint16_t*, hipStream_t);
 int launch_moe_gate_up(const uint16_t*, const int32_t*, const int32_t*, int, const uint8_t*,
                        const float*, int, int, int, uint16_t*, hipStream_t);
 int launch_moe_down(const uint16_t*, const int32_t*, const uint8_t*, const float*, int, int, int,
                     float*, hipStream_t);
 int launch_rmsnorm(const uint16_t*, const float*, int, int, float, uint16_t*, hipStream_t);
-int launch_linear(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int, uint16_t*,
-                  uint16_t*, hipStream_t);
-int launch_rope_kv(const uint16_t*, const int32_t*, const int32_t*, const uint16_t*,
-                   const uint16_t*, int, int, int, int, int, const int64_t*, const int32_t*, uint16_t*,
-                   uint16_t*, uint16_t*, hipStream_t);
+int launch_linear_residual_rmsnorm(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int,
+                                   uint16_t*, const float*, float, uint16_t*, float*, hipStream_t);
+int launch_qkv_rope_kv(const uint16_t*, const uint16_t*, const uint16_t*, float*, const int32_t*,
+                       const int32_t*, const uint16_t*, const uint16_t*, int, int, int, int, int, int,
+                       const int64_t*, const int32_t*, uint16_t*, uint16_t*, uint16_t*, hipStream_t);
+size_t linear_partials_bytes(int M, int N, int K);
 int launch_attn(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
-                const float*, int, int, const flyai_attn_item*, int, const flyai_attn_group*, int,
+                const float*, int, int, const flyai_attn_item*, int, int, const flyai_attn_group*, int,
                 float*, uint16_t*, hipStream_t);
 int attn_plan(const int32_t*, const int32_t*, int, int, int, int, flyai_attn_item*, int,
-              flyai_attn_group*, int, int*, int*);
+              flyai_attn_group*, int, int*, int*, int*);
 
 }  // namespace flyai
 
@@ -73,14 +77,14 @@ struct flyai_stage {
   flyai_layer_desc* layers = nullptr;
   const uint16_t* cos_tab = nullptr;
   const uint16_t* sin_tab = nullptr;
-  // device workspace offsets
-  size_t o_qlens, o_starts, o_cap, o_base, o_cu, o_pos, o_sid, o_kvlen, o_slot, o_status;
-  size_t o_xn, o_qkv, o_qrot, o_attn, o_items[2], o_groups[2], o_parts;
-  size_t o_ids, o_w, o_hist, o_off, o_perm, o_inv, o_hmoe, o_y;
+  // device workspace offsets; o_blob holds the per-step batch blob copied from the host
+  size_t o_blob, blob_max, o_cu, o_pos, o_sid, o_kvlen, o_slot, o_status;
+  size_t o_xn, o_gemm, o_qrot, o_attn, o_parts;
+  size_t o_ids, o_w, o_logits, o_hist, o_off, o_perm, o_inv, o_hmoe, o_y;
   size_t dev_bytes = 0;
-  // host staging offsets (within one half)
-  size_t h_qlens, h_starts, h_cap, h_base, h_items[2], h_groups[2];
-  size_t host_half = 0;
+  size_t host_half = 0;  // bytes of one pinned staging half (== blob_max)
+  std::vector<flyai_attn_item> plan_items[2];
+  std::vector<flyai_attn_group> plan_groups[2];
   char* dev = nullptr;
   char* host = nullptr;
   hipEvent_t staged[2] = {nullptr, nullptr};
@@ -88,14 +92,18 @@ struct flyai_stage {
   bool events_ready = false;
 };
 
+static size_t blob_bytes(int S, int n_items0, int n_items1, int n_groups0, int n_groups1) {
+  return align256((size_t)S * 4) * 3 + align256((size_t)S * 8) +
+         align256((size_t)n_items0 * sizeof(flyai_attn_item)) + align256((size_t)n_items1 * sizeof(flyai_attn_item)) +
+         align256((size_t)n_groups0 * sizeof(flyai_attn_group)) + align256((size_t)n_groups1 * sizeof(flyai_attn_group));
+}
+
 static void layout(flyai_stage* st) {
   const flyai_stage_config& c = st->cfg;
   const size_t S = c.max_seqs, T = c.max_tokens, P = (size_t)T * c.top_k;
+  st->blob_max = blob_bytes(c.max_seqs, c.max_attn_items, c.max_attn_items, st->max_groups, st->max_groups);
   Carve d;
-  st->o_qlens = d.take(S * 4);
-  st->o_starts = d.take(S * 4);
-  st->o_cap = d.take(S * 4);
-  st->o_base = d.take(S * 8);
+  st->o_blob = d.take(st->blob_max);
   st->o_cu = d.take((S + 1) * 4);
   st->o_pos = d.take(T * 4);
   st->o_sid = d.take(T * 4);
@@ -103,16 +111,17 @@ static void layout(flyai_stage* st) {
   st->o_slot = d.take(T * 8);
   st->o_status = d.take(4);
   st->o_xn = d.take(T * c.hidden * 2);
-  st->o_qkv = d.take(T * st->qkv_width * 2);
+  {
+    const size_t a = linear_partials_bytes(c.max_tokens, st->qkv_width, c.hidden);
+    const size_t b = linear_partials_bytes(c.max_tokens, c.hidden, c.n_q_heads * c.head_dim);
+    st->o_gemm = d.take(a > b ? a : b);
+  }
   st->o_qrot = d.take(T * c.n_q_heads * c.head_dim * 2);
   st->o_attn = d.take(T * c.n_q_heads * c.head_dim * 2);
-  for (int i = 0; i < 2; ++i) {
-    st->o_items[i] = d.take((size_t)c.max_attn_items * sizeof(flyai_attn_item));
-    st->o_groups[i] = d.take((size_t)st->max_groups * sizeof(flyai_attn_group));
-  }
   st->o_parts = d.take(flyai_attn_partials_bytes(c.max_attn_items));
   st->o_ids = d.take(P * 4);
   st->o_w = d.take(P * 4);
+  st->o_logits = d.take(T * (size_t)c.n_experts * 4);
   st->o_hist = d.take((size_t)c.n_experts * 4);
   st->o_off = d.take(((size_t)c.n_experts + 1) * 4);
   st->o_perm = d.take(P * 4);
@@ -120,16 +129,7 @@ static void layout(flyai_stage* st) {
   st->o_hmoe = d.take(P * c.intermediate * 2);
   st->o_y = d.take(P * c.hidden * 4);
   st->dev_bytes = d.off;
-  Carve h;
-  st->h_qlens = h.take(S * 4);
-  st->h_starts = h.take(S * 4);
-  st->h_cap = h.take(S * 4);
-  st->h_base = h.take(S * 8);
-  for (int i = 0; i < 2; ++i) {
-    st->h_items[i] = h.take((size_t)c.max_attn_items * sizeof(flyai_attn_item));
-    st->h_groups[i] = h.take((size_t)st->max_groups * sizeof(flyai_attn_group));
-  }
-  st->host_half = h.off;
+  st->host_half = st->blob_max;
 }
 
 extern "C" const char* flyai_last_error(void) { return g_last_error; }
@@ -141,8 +141,9 @@ extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** o
   FLYAI_REQUIRE(c.n_layers > 0 && c.hidden > 0 && c.hidden % 64 == 0, "stage: hidden must be a multiple of 64");
   FLYAI_REQUIRE(c.head_dim == 64 && c.n_kv_heads > 0 && c.n_q_heads == 8 * c.n_kv_heads,
                 "stage: attention kernel needs head_dim 64 and 8 query heads per kv head");
-  FLYAI_REQUIRE(c.n_experts > 0 && c.n_experts <= 256 && c.top_k >= 1 && c.top_k <= 8,
-                "stage: need 1 <= n_experts <= 256, 1 <= top_k <= 8");
+  FLYAI_REQUIRE(c.n_experts >= 4 && c.n_experts <= 256 && c.n_experts % 4 == 0 &&
+                    (c.top_k == 2 || c.top_k == 4 || c.top_k == 8),
+                "stage: need n_experts %% 4 == 0 in [4, 256] and top_k in {2, 4, 8}");
   FLYAI_REQUIRE(c.intermediate > 0 && c.intermediate % 32 == 0 && c.hidden % 32 == 0,
                 "stage: MXFP4 needs hidden and intermediate multiples of 32");
   FLYAI_REQUIRE(c.max_tokens > 0 && (int64_t)c.max_tokens * c.top_k <= 65536, "stage: max_tokens*top_k <= 65536");
@@ -157,6 +158,16 @@ extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** o
   st->layers = new (std::nothrow) flyai_layer_desc[c.n_layers];
   if (!st->layers) { delete st; return set_error(FLYAI_EINVAL, "stage_create: out of host memory"); }
   memset(st->layers, 0, sizeof(flyai_layer_desc) * c.n_layers);
+  try {
+    for (int i = 0; i < 2; ++i) {
+      st->plan_items[i].resize(c.max_attn_items);
+      st->plan_groups[i].resize(st->max_groups);
+    }
+  } catch (...) {
+    delete[] st->layers;
+    delete st;
+    return set_error(FLYAI_EINVAL, "stage_create: out of host memory for the attention plan");
+  }
   layout(st);
   *out = st;
   return FLYAI_OK;
@@ -213,7 +224,7 @@ extern "C" int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t d
 
 extern "C" void* flyai_stage_debug_buffer(flyai_stage* st, int32_t which) {
   if (!st || !st->dev) return nullptr;
-  const size_t offs[] = {st->o_xn, st->o_qkv, st->o_qrot, st->o_attn, st->o_ids, st->o_w,
+  const size_t offs[] = {st->o_xn, st->o_gemm, st->o_qrot, st->o_attn, st->o_ids, st->o_w,
                          st->o_off, st->o_perm, st->o_inv, st->o_hmoe, st->o_y, st->o_pos,
                          st->o_sid, st->o_cu};
   if (which < 0 || which >= (int)(sizeof(offs) / sizeof(offs[0]))) return nullptr;
@@ -262,70 +273,81 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
     FLYAI_REQUIRE(st->layers[l].wqkv, "forward: layer %d not bound", l);
   hipStream_t s = as_stream(stream);
 
-  // stage host inputs: wait until the GPU consumed this half's previous contents
-  const int h = st->half;
-  st->half ^= 1;
-  const hipError_t ew = hipEventSynchronize(st->staged[h]);
-  if (ew != hipSuccess) return set_error(FLYAI_EHIP, "hipEventSynchronize: %s", hipGetErrorString(ew));
-  char* hb = st->host + h * st->host_half;
-  memcpy(hb + st->h_qlens, q_lens, S * 4);
-  memcpy(hb + st->h_starts, starts, S * 4);
-  memcpy(hb + st->h_cap, kv_cap, S * 4);
-  memcpy(hb + st->h_base, kv_base, S * 8);
-  int n_items[2], n_groups[2];
+  int n_items[2], n_groups[2], n_small[2];
   for (int p = 0; p < 2; ++p) {
     RUN(attn_plan(q_lens, starts, S, c.n_kv_heads, p == 0 ? 0 : c.window, c.attn_split_keys,
-                  reinterpret_cast<flyai_attn_item*>(hb + st->h_items[p]), c.max_attn_items,
-                  reinterpret_cast<flyai_attn_group*>(hb + st->h_groups[p]), st->max_groups,
-                  &n_items[p], &n_groups[p]));
+                  st->plan_items[p].data(), c.max_attn_items, st->plan_groups[p].data(), st->max_groups,
+                  &n_items[p], &n_groups[p], &n_small[p]));
+  }
+  // one compact blob per step: q_lens | starts | kv_cap | kv_base | items x2 | groups x2
+  size_t off_q, off_st, off_cap, off_base, off_items[2], off_groups[2];
+  {
+    Carve b;
+    off_q = b.take((size_t)S * 4);
+    off_st = b.take((size_t)S * 4);
+    off_cap = b.take((size_t)S * 4);
+    off_base = b.take((size_t)S * 8);
+    for (int p = 0; p < 2; ++p) off_items[p] = b.take((size_t)n_items[p] * sizeof(flyai_attn_item));
+    for (int p = 0; p < 2; ++p) off_groups[p] = b.take((size_t)n_groups[p] * sizeof(flyai_attn_group));
+    if (b.off > st->blob_max) return set_error(FLYAI_ERANGE, "batch blob exceeds its reservation");
+    // wait until the GPU consumed this staging half's previous contents, then fill it
+    const int h = st->half;
+    st->half ^= 1;
+    const hipError_t ew = hipEventSynchronize(st->staged[h]);
+    if (ew != hipSuccess) return set_error(FLYAI_EHIP, "hipEventSynchronize: %s", hipGetErrorString(ew));
+    char* hb = st->host + h * st->host_half;
+    memcpy(hb + off_q, q_lens, S * 4);
+    memcpy(hb + off_st, starts, S * 4);
+    memcpy(hb + off_cap, kv_cap, S * 4);
+    memcpy(hb + off_base, kv_base, S * 8);
+    for (int p = 0; p < 2; ++p) {
+      memcpy(hb + off_items[p], st->plan_items[p].data(), n_items[p] * sizeof(flyai_attn_item));
+      memcpy(hb + off_groups[p], st->plan_groups[p].data(), n_groups[p] * sizeof(flyai_attn_group));
+    }
+    RUN(copy_h2d(st->dev + st->o_blob, hb, b.off, s));
+    const hipError_t er = hipEventRecord(st->staged[h], s);
+    if (er != hipSuccess) return set_error(FLYAI_EHIP, "hipEventRecord: %s", hipGetErrorString(er));
   }
   char* d = st->dev;
-  RUN(copy_h2d(d + st->o_qlens, hb + st->h_qlens, S * 4, s));
-  RUN(copy_h2d(d + st->o_starts, hb + st->h_starts, S * 4, s));
-  RUN(copy_h2d(d + st->o_cap, hb + st->h_cap, S * 4, s));
-  RUN(copy_h2d(d + st->o_base, hb + st->h_base, S * 8, s));
-  for (int p = 0; p < 2; ++p) {
-    RUN(copy_h2d(d + st->o_items[p], hb + st->h_items[p], n_items[p] * sizeof(flyai_attn_item), s));
-    RUN(copy_h2d(d + st->o_groups[p], hb + st->h_groups[p], n_groups[p] * sizeof(flyai_attn_group), s));
-  }
-  const hipError_t er = hipEventRecord(st->staged[h], s);
-  if (er != hipSuccess) return set_error(FLYAI_EHIP, "hipEventRecord: %s", hipGetErrorString(er));
-
+  char* blob = d + st->o_blob;
   auto I32 = [&](size_t o) { return reinterpret_cast<int32_t*>(d + o); };
   auto F32 = [&](size_t o) { return reinterpret_cast<float*>(d + o); };
   auto B16 = [&](size_t o) { return reinterpret_cast<uint16_t*>(d + o); };
-  const int64_t* base_d = reinterpret_cast<const int64_t*>(d + st->o_base);
+  const int64_t* base_d = reinterpret_cast<const int64_t*>(blob + off_base);
+  const int32_t* cap_d = reinterpret_cast<const int32_t*>(blob + off_cap);
 
-  RUN(flyai_pack_ragged(I32(st->o_qlens), I32(st->o_starts), base_d, I32(st->o_cap), S, c.head_dim,
+  RUN(flyai_pack_ragged(reinterpret_cast<const int32_t*>(blob + off_q),
+                        reinterpret_cast<const int32_t*>(blob + off_st), base_d, cap_d, S, c.head_dim,
                         c.max_tokens, I32(st->o_cu), I32(st->o_pos), I32(st->o_sid),
                         I32(st->o_kvlen), reinterpret_cast<int64_t*>(d + st->o_slot),
                         I32(st->o_status), stream));
   const int Tn = (int)T;
   const int H = c.hidden, E = c.n_experts, k = c.top_k, I = c.intermediate;
+  RUN(launch_rmsnorm(hidden, st->layers[0].ln1, Tn, H, c.rms_eps, B16(st->o_xn), s));
   for (int l = 0; l < c.n_layers; ++l) {
     const flyai_layer_desc& L = st->layers[l];
     const int p = L.sliding ? 1 : 0;
-    RUN(launch_rmsnorm(hidden, L.ln1, Tn, H, c.rms_eps, B16(st->o_xn), s));
-    RUN(launch_linear(B16(st->o_xn), L.wqkv, L.bqkv, Tn, st->qkv_width, H, B16(st->o_qkv), nullptr, s));
-    RUN(launch_rope_kv(B16(st->o_qkv), I32(st->o_pos), I32(st->o_sid), st->cos_tab, st->sin_tab,
-                       c.rope_positions, Tn,
-                       c.n_q_heads, c.n_kv_heads, c.head_dim, base_d, I32(st->o_cap), B16(st->o_qrot),
-                       L.k_pool, L.v_pool, s));
-    RUN(launch_attn(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, I32(st->o_cap), L.sinks,
+    // xn holds this layer's input RMSNorm (written by the previous layer's combine)
+    RUN(launch_qkv_rope_kv(B16(st->o_xn), L.wqkv, L.bqkv, F32(st->o_gemm), I32(st->o_pos),
+                           I32(st->o_sid), st->cos_tab, st->sin_tab, c.rope_positions, Tn, H,
+                           c.n_q_heads, c.n_kv_heads, c.head_dim, base_d, cap_d, B16(st->o_qrot),
+                           L.k_pool, L.v_pool, s));
+    RUN(launch_attn(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks,
                     L.sliding ? c.window : 0, c.n_q_heads,
-                    reinterpret_cast<const flyai_attn_item*>(d + st->o_items[p]), n_items[p],
-                    reinterpret_cast<const flyai_attn_group*>(d + st->o_groups[p]), n_groups[p],
+                    reinterpret_cast<const flyai_attn_item*>(blob + off_items[p]), n_items[p], n_small[p],
+                    reinterpret_cast<const flyai_attn_group*>(blob + off_groups[p]), n_groups[p],
                     F32(st->o_parts), B16(st->o_attn), s));
-    RUN(launch_linear(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim, nullptr, hidden, s));
-    RUN(launch_rmsnorm(hidden, L.ln2, Tn, H, c.rms_eps, B16(st->o_xn), s));
-    RUN(launch_router(B16(st->o_xn), L.router_w, L.router_b, Tn, H, E, k, I32(st->o_ids),
-                      F32(st->o_w), nullptr, s));
-    RUN(launch_permute(I32(st->o_ids), Tn, k, E, I32(st->o_hist), I32(st->o_off), I32(st->o_perm),
-                       I32(st->o_inv), s));
+    RUN(launch_linear_residual_rmsnorm(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
+                                       hidden, L.ln2, c.rms_eps, B16(st->o_xn), F32(st->o_gemm), s));
+    RUN(launch_route_permute(B16(st->o_xn), L.router_w, L.router_b, Tn, H, E, k, I32(st->o_ids),
+                             F32(st->o_w), F32(st->o_logits), I32(st->o_hist), I32(st->o_off),
+                             I32(st->o_perm), I32(st->o_inv), s));
     RUN(launch_moe_gate_up(B16(st->o_xn), I32(st->o_perm), I32(st->o_off), k, L.w13_packed, L.b13,
                            E, H, I, B16(st->o_hmoe), s));
     RUN(launch_moe_down(B16(st->o_hmoe), I32(st->o_off), L.w2_packed, L.b2, E, H, I, F32(st->o_y), s));
-    RUN(launch_combine(F32(st->o_y), I32(st->o_inv), F32(st->o_w), Tn, k, H, hidden, hidden, s));
+    const float* next_ln1 = (l + 1 < c.n_layers) ? st->layers[l + 1].ln1 : nullptr;
+    RUN(launch_combine(F32(st->o_y), I32(st->o_inv), F32(st->o_w), Tn, k, H, hidden, hidden, next_ln1,
+                       c.rms_eps, B16(st->o_xn), s));
   }
   return FLYAI_OK;
 }

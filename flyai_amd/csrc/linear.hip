@@ -4,24 +4,33 @@
 namespace flyai {
 
 // ---- RMSNorm: y = bf16(w * (x * rsqrt(mean(x^2) + eps))), fp32 weight --------------------------
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
-                                                      const float* __restrict__ w, int H, float eps,
-                                                      uint16_t* __restrict__ y) {
-  __shared__ float red[4];
+constexpr int kRowThreads = 1024;  // one workgroup per token row: ~3 elements per thread at H = 2880
+
+__device__ __forceinline__ float block_sum_1024(float v, float* red) {
+  v = warp_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int w = 0; w < kRowThreads / 64; ++w) s += red[w];
+  return s;
+}
+
+__global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                              const float* __restrict__ w, int H,
+                                                              float eps, uint16_t* __restrict__ y) {
+  __shared__ float red[kRowThreads / 64];
   const int t = blockIdx.x, tid = threadIdx.x;
   const uint16_t* xr = x + (size_t)t * H;
   float ss = 0.f;
-  for (int i = tid; i < H; i += 256) {
+  for (int i = tid; i < H; i += kRowThreads) {
     const float v = bf2f(xr[i]);
     ss = fmaf(v, v, ss);
   }
-  ss = warp_sum(ss);
-  if ((tid & 63) == 0) red[tid >> 6] = ss;
-  __syncthreads();
-  const float total = red[0] + red[1] + red[2] + red[3];
+  const float total = block_sum_1024(ss, red);
   const float r = rsqrtf(total / (float)H + eps);
   uint16_t* yr = y + (size_t)t * H;
-  for (int i = tid; i < H; i += 256) {
+  for (int i = tid; i < H; i += kRowThreads) {
     const float hs = bf2f(xr[i]) * r;
     yr[i] = f2bf(w[i] * hs);
   }
@@ -30,117 +39,202 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
 int launch_rmsnorm(const uint16_t* x, const float* w, int T, int H, float eps, uint16_t* y,
                    hipStream_t s) {
   if (T == 0) return FLYAI_OK;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(256), 0, s, x, w, H, eps, y);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(kRowThreads), 0, s, x, w, H, eps, y);
   return check_launch("rmsnorm");
 }
 
-// ---- bf16 linear: y[M,N] = bf16(x[M,K] W[N,K]^T + b), split-K over the waves of a workgroup --------
-// Workgroup = KS waves on one 16-feature tile; wave w takes K groups of 128 (w, w+KS, ...); lane
-// (r, g) supplies K values 128*kq + 32*g + 8*j .. +7 at MFMA step j for both operands.  Partial
-// accumulators are reduced through LDS and wave 0 applies bias / residual.
-constexpr int kLinMT = 4;  // 64 activation rows per pass
+// ---- bf16 projections: split-K partial GEMM + fused finalize kernels -------------------------------
+// gemm_splitk: workgroup = 4 waves on 4 consecutive 16-feature tiles and one K slice of kKQW groups
+// of 128.  The activation slice (64 rows x 512 K, bf16) is staged once in LDS; each wave issues all
+// of its weight loads for the slice before its first MFMA (a single HBM round trip per wave) and
+// writes fp32 partial sums part[slice][row][feature].  A finalize kernel adds the slices in slice
+// order (so the result is independent of timing), the bias, and the fused epilogue.
+constexpr int kKQW = 4;       // K groups of 128 per slice
+constexpr int kGemmRows = 64; // activation rows per pass
 
-template <int KS>
-__global__ __launch_bounds__(KS * 64) void linear_bf16_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ W, const uint16_t* __restrict__ b,
-    int M, int N, int K, uint16_t* __restrict__ y, uint16_t* __restrict__ residual) {
-  __shared__ f32x4_t red[KS][kLinMT][64];
+__global__ __launch_bounds__(256) void gemm_splitk_bf16_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ W, int M, int N, int K,
+    float* __restrict__ part) {
+  __shared__ uint4 as[kGemmRows][kKQW * 16 + 1];  // 64 rows x 512 bf16, +16 B per row vs bank conflicts
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int nt = blockIdx.x;
-  const int feat = nt * 16 + r;
+  const int nt = blockIdx.x * 4 + wave;
+  const int slice = blockIdx.y;
   const int KQ = (K + 127) / 128;
-  const uint16_t* wrow = W + (size_t)feat * K + 32 * g;
-  for (int m0 = 0; m0 < M; m0 += 16 * kLinMT) {
-    const int mt_count = min(kLinMT, (M - m0 + 15) / 16);
-    f32x4_t acc[kLinMT];
+  const int kq0 = slice * kKQW;
+  const int nkq = min(kKQW, KQ - kq0);
+  const bool nval = nt * 16 < N;
+  const int feat = nt * 16 + r;
+  // weights for the whole slice, issued up front
+  uint4 wv[kKQW][4];
 #pragma unroll
-    for (int m = 0; m < kLinMT; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    for (int kq = wave; kq < KQ; kq += KS) {
-      const int k0 = 128 * kq + 32 * g;
-      const bool kv = k0 < K;
-      uint4 wv[4];
+  for (int q = 0; q < kKQW; ++q) {
+    const int k0 = 128 * (kq0 + q) + 32 * g;
+    const bool ok = nval && q < nkq && k0 < K;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        wv[j] = kv ? reinterpret_cast<const uint4*>(wrow + 128 * kq)[j] : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < 4; ++j)
+      wv[q][j] = ok ? reinterpret_cast<const uint4*>(W + (size_t)feat * K + k0)[j] : make_uint4(0, 0, 0, 0);
+  }
+  for (int m0 = 0; m0 < M; m0 += kGemmRows) {
+    const int rows = min(kGemmRows, M - m0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < kGemmRows * kKQW * 16; i += 256) {
+      const int row = i / (kKQW * 16), v = i % (kKQW * 16);
+      const int k = 128 * kq0 + 8 * v;
+      as[row][v] = (row < rows && k < K) ? *reinterpret_cast<const uint4*>(x + (size_t)(m0 + row) * K + k)
+                                         : make_uint4(0, 0, 0, 0);
+    }
+    __syncthreads();
+    if (!nval) continue;
+    const int mt_count = (rows + 15) / 16;
+    f32x4_t acc[4] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f},
+                      f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int m = 0; m < kLinMT; ++m) {
-        if (m < mt_count) {
-          const int row = m0 + 16 * m + r;
-          uint4 av[4];
-          if (kv && row < M) {
-            const uint4* ap = reinterpret_cast<const uint4*>(x + (size_t)row * K + k0);
+    for (int q = 0; q < kKQW; ++q) {
+      if (q >= nkq) break;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) av[j] = ap[j];
-          } else {
+      for (int m = 0; m < 4; ++m) {
+        if (m >= mt_count) break;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) av[j] = make_uint4(0, 0, 0, 0);
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) acc[m] = mfma16x16x32(as_bf16x8(av[j]), as_bf16x8(wv[j]), acc[m]);
+        for (int j = 0; j < 4; ++j) {
+          const uint4 av = as[16 * m + r][q * 16 + 4 * g + j];
+          acc[m] = mfma16x16x32(as_bf16x8(av), as_bf16x8(wv[q][j]), acc[m]);
         }
       }
     }
+    float* pp = part + (size_t)slice * M * N;
 #pragma unroll
-    for (int m = 0; m < kLinMT; ++m) red[wave][m][lane] = acc[m];
-    __syncthreads();
-    if (wave == 0) {
-      const float bias = b ? bf2f(b[feat]) : 0.f;
-      for (int m = 0; m < mt_count; ++m) {
-        f32x4_t s = red[0][m][lane];
+    for (int m = 0; m < 4; ++m) {
+      if (m >= mt_count) break;
 #pragma unroll
-        for (int w = 1; w < KS; ++w) s += red[w][m][lane];
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = m0 + 16 * m + 4 * g + v;
-          if (row < M) {
-            const float o = bf16_round(s[v] + bias);
-            if (residual) {
-              uint16_t* rp = residual + (size_t)row * N + feat;
-              *rp = f2bf(bf2f(*rp) + o);
-            } else {
-              y[(size_t)row * N + feat] = f2bf(o);
-            }
-          }
-        }
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + 16 * m + 4 * g + v;
+        if (row < M) pp[(size_t)row * N + feat] = acc[m][v];
       }
     }
-    __syncthreads();
   }
 }
 
-int launch_linear(const uint16_t* x, const uint16_t* W, const uint16_t* b, int M, int N, int K,
-                  uint16_t* y, uint16_t* residual, hipStream_t s) {
-  if (M == 0) return FLYAI_OK;
-  hipLaunchKernelGGL(linear_bf16_kernel<8>, dim3(N / 16), dim3(8 * 64), 0, s, x, W, b, M, N, K, y,
-                     residual);
-  return check_launch("linear_bf16");
+constexpr int kMaxSlices = 16;  // K <= 8192
+
+// Sum of the split-K partials in slice order; all loads are issued before the first add.
+__device__ __forceinline__ float sum_slices(const float* __restrict__ part, int slices, size_t stride,
+                                            size_t idx) {
+  float v[kMaxSlices];
+#pragma unroll
+  for (int i = 0; i < kMaxSlices; ++i) v[i] = i < slices ? part[i * stride + idx] : 0.f;
+  float s = v[0];
+#pragma unroll
+  for (int i = 1; i < kMaxSlices; ++i)
+    if (i < slices) s += v[i];
+  return s;
 }
 
-// ---- RoPE (GPT-OSS half split, per-op bf16 rounding) + K/V append --------------------------------
+// y = bf16(sum + b); with residual: residual <- bf16(residual + y)
+__global__ __launch_bounds__(256) void linear_finalize_kernel(const float* __restrict__ part, int slices,
+                                                              const uint16_t* __restrict__ b, int M,
+                                                              int N, uint16_t* __restrict__ y,
+                                                              uint16_t* __restrict__ residual) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (size_t)M * N) return;
+  const int f = idx % N;
+  const float o = bf16_round(sum_slices(part, slices, (size_t)M * N, idx) + (b ? bf2f(b[f]) : 0.f));
+  if (residual) residual[idx] = f2bf(bf2f(residual[idx]) + o);
+  else y[idx] = f2bf(o);
+}
+
+// o_proj epilogue fused with the post-attention RMSNorm: h <- bf16(h + bf16(sum + b)),
+// xn = bf16(w * (h * rsqrt(mean(h^2) + eps))).  One workgroup per token row.
+__global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_finalize_kernel(
+    const float* __restrict__ part, int slices, const uint16_t* __restrict__ b, int M, int H,
+    uint16_t* __restrict__ h, const float* __restrict__ lnw, float eps, uint16_t* __restrict__ xn) {
+  __shared__ float red[kRowThreads / 64];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const size_t stride = (size_t)M * H;
+  float ss = 0.f;
+  for (int i = tid; i < H; i += kRowThreads) {
+    const size_t idx = (size_t)t * H + i;
+    const float o = bf16_round(sum_slices(part, slices, stride, idx) + (b ? bf2f(b[i]) : 0.f));
+    const uint16_t hv = f2bf(bf2f(h[idx]) + o);
+    h[idx] = hv;
+    const float hf = bf2f(hv);
+    ss = fmaf(hf, hf, ss);
+  }
+  const float rr = rsqrtf(block_sum_1024(ss, red) / (float)H + eps);
+  for (int i = tid; i < H; i += kRowThreads) {
+    const size_t idx = (size_t)t * H + i;
+    xn[idx] = f2bf(lnw[i] * (bf2f(h[idx]) * rr));
+  }
+}
+
+int gemm_slices(int K) { return ((K + 127) / 128 + kKQW - 1) / kKQW; }
+
+size_t linear_partials_bytes(int M, int N, int K) { return (size_t)gemm_slices(K) * M * N * sizeof(float); }
+
+int launch_gemm_splitk(const uint16_t* x, const uint16_t* W, int M, int N, int K, float* part,
+                       hipStream_t s) {
+  hipLaunchKernelGGL(gemm_splitk_bf16_kernel, dim3(ceil_div(N, 64), gemm_slices(K)), dim3(256), 0, s,
+                     x, W, M, N, K, part);
+  return check_launch("gemm_splitk_bf16");
+}
+
+int launch_linear(const uint16_t* x, const uint16_t* W, const uint16_t* b, int M, int N, int K,
+                  uint16_t* y, uint16_t* residual, float* part, hipStream_t s) {
+  if (M == 0) return FLYAI_OK;
+  int rc = launch_gemm_splitk(x, W, M, N, K, part, s);
+  if (rc) return rc;
+  const size_t total = (size_t)M * N;
+  hipLaunchKernelGGL(linear_finalize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                     part, gemm_slices(K), b, M, N, y, residual);
+  return check_launch("linear_finalize");
+}
+
+int launch_linear_residual_rmsnorm(const uint16_t* x, const uint16_t* W, const uint16_t* b, int M,
+                                   int N, int K, uint16_t* h, const float* lnw, float eps,
+                                   uint16_t* xn, float* part, hipStream_t s) {
+  if (M == 0) return FLYAI_OK;
+  int rc = launch_gemm_splitk(x, W, M, N, K, part, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(residual_rmsnorm_finalize_kernel, dim3(M), dim3(kRowThreads), 0, s, part,
+                     gemm_slices(K),
+                     b, M, N, h, lnw, eps, xn);
+  return check_launch("residual_rmsnorm_finalize");
+}
+
+// ---- QKV finalize + RoPE (GPT-OSS half split, per-op bf16 rounding) + K/V append ------------------
+// qkv[t][f] = bf16(sum of the split-K partials + bias) -- exactly what the unfused Linear writes --
+// then q/k rotate (first = x1 c - x2 s, second = x2 c + x1 s, each product and sum rounded to bf16),
+// q goes to q_out and k/v to the sequence's slab at the token's position.  One workgroup per token.
+template <bool FROM_PARTIALS>
 __global__ __launch_bounds__(256) void rope_kv_append_kernel(
-    const uint16_t* __restrict__ qkv, const int32_t* __restrict__ positions,
+    const uint16_t* __restrict__ qkv, const float* __restrict__ part, int slices, int M,
+    const uint16_t* __restrict__ bias, const int32_t* __restrict__ positions,
     const int32_t* __restrict__ seq_id, const uint16_t* __restrict__ cos_tab,
     const uint16_t* __restrict__ sin_tab, int rope_positions, int Hq, int Hkv, int D,
-    const int64_t* __restrict__ kv_base,
-    const int32_t* __restrict__ kv_cap, uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool,
-    uint16_t* __restrict__ v_pool) {
+    const int64_t* __restrict__ kv_base, const int32_t* __restrict__ kv_cap,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool) {
   const int t = blockIdx.x;
   const int pos = positions[t];
   if (pos < 0 || pos >= rope_positions) return;  // outside the rotary table: no read, no write
   const int b = seq_id[t];
   const int cap = kv_cap[b];
-  const bool in_cap = pos >= 0 && pos < cap;
+  const bool in_cap = pos < cap;
   const int64_t base = kv_base[b];
   const int D2 = D / 2;
   const int width = (Hq + 2 * Hkv) * D;
-  const uint16_t* row = qkv + (size_t)t * width;
+  const size_t stride = (size_t)M * width;
+  auto val = [&](int f) -> float {
+    if (FROM_PARTIALS)
+      return bf16_round(sum_slices(part, slices, stride, (size_t)t * width + f) + (bias ? bf2f(bias[f]) : 0.f));
+    return bf2f(qkv[(size_t)t * width + f]);
+  };
   const uint16_t* cr = cos_tab + (size_t)pos * D2;
   const uint16_t* sr = sin_tab + (size_t)pos * D2;
   const int pairs = (Hq + Hkv) * D2;
-  for (int i = threadIdx.x; i < pairs; i += blockDim.x) {
+  const int nthr = blockDim.x * gridDim.y, tid = blockIdx.y * blockDim.x + threadIdx.x;
+  for (int i = tid; i < pairs; i += nthr) {
     const int h = i / D2, d = i % D2;
-    const float x1 = bf2f(row[h * D + d]), x2 = bf2f(row[h * D + d + D2]);
+    const float x1 = val(h * D + d), x2 = val(h * D + d + D2);
     const float c = bf2f(cr[d]), s = bf2f(sr[d]);
     const float first = bf16_round(bf16_round(x1 * c) - bf16_round(x2 * s));
     const float second = bf16_round(bf16_round(x2 * c) + bf16_round(x1 * s));
@@ -155,23 +249,38 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(
     }
   }
   if (in_cap) {
-    for (int i = threadIdx.x; i < Hkv * D; i += blockDim.x) {
+    for (int i = tid; i < Hkv * D; i += nthr) {
       const int gv = i / D, d = i % D;
-      v_pool[base + ((size_t)gv * D + d) * cap + pos] = row[(Hq + Hkv) * D + gv * D + d];
+      v_pool[base + ((size_t)gv * D + d) * cap + pos] = f2bf(val((Hq + Hkv) * D + gv * D + d));
     }
   }
 }
 
 int launch_rope_kv(const uint16_t* qkv, const int32_t* positions, const int32_t* seq_id,
                    const uint16_t* cos_tab, const uint16_t* sin_tab, int rope_positions, int T,
-                   int Hq, int Hkv, int D,
-                   const int64_t* kv_base, const int32_t* kv_cap, uint16_t* q_out,
-                   uint16_t* k_pool, uint16_t* v_pool, hipStream_t s) {
+                   int Hq, int Hkv, int D, const int64_t* kv_base, const int32_t* kv_cap,
+                   uint16_t* q_out, uint16_t* k_pool, uint16_t* v_pool, hipStream_t s) {
   if (T == 0) return FLYAI_OK;
-  hipLaunchKernelGGL(rope_kv_append_kernel, dim3(T), dim3(256), 0, s, qkv, positions, seq_id,
-                     cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base, kv_cap, q_out, k_pool,
-                     v_pool);
+  hipLaunchKernelGGL(rope_kv_append_kernel<false>, dim3(T), dim3(256), 0, s, qkv, nullptr, 0, T,
+                     nullptr, positions, seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base,
+                     kv_cap, q_out, k_pool, v_pool);
   return check_launch("rope_kv_append");
+}
+
+// QKV projection + RoPE + KV append: split-K GEMM, then the fused finalize
+int launch_qkv_rope_kv(const uint16_t* x, const uint16_t* Wqkv, const uint16_t* bqkv, float* part,
+                       const int32_t* positions, const int32_t* seq_id, const uint16_t* cos_tab,
+                       const uint16_t* sin_tab, int rope_positions, int T, int H, int Hq, int Hkv,
+                       int D, const int64_t* kv_base, const int32_t* kv_cap, uint16_t* q_out,
+                       uint16_t* k_pool, uint16_t* v_pool, hipStream_t s) {
+  if (T == 0) return FLYAI_OK;
+  const int width = (Hq + 2 * Hkv) * D;
+  int rc = launch_gemm_splitk(x, Wqkv, T, width, H, part, s);
+  if (rc) return rc;
+  hipLaunchKernelGGL(rope_kv_append_kernel<true>, dim3(T, 4), dim3(256), 0, s, nullptr, part,
+                     gemm_slices(H), T, bqkv, positions, seq_id, cos_tab, sin_tab, rope_positions, Hq,
+                     Hkv, D, kv_base, kv_cap, q_out, k_pool, v_pool);
+  return check_launch("qkv_rope_kv_append");
 }
 
 }  // namespace flyai
@@ -185,13 +294,18 @@ extern "C" int flyai_rmsnorm(const uint16_t* x, const float* w, int32_t T, int32
   return launch_rmsnorm(x, w, T, H, eps, y, as_stream(stream));
 }
 
+extern "C" size_t flyai_linear_workspace_bytes(int32_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return linear_partials_bytes(M, N, K);
+}
+
 extern "C" int flyai_linear_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t M,
                                  int32_t N, int32_t K, uint16_t* y, uint16_t* residual,
-                                 flyai_stream_t stream) {
-  FLYAI_REQUIRE(M >= 0 && N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0,
-                "linear: need N %% 16 == 0 and K %% 32 == 0");
-  FLYAI_REQUIRE(x && w && (y || residual), "linear: null pointer");
-  return launch_linear(x, w, b, M, N, K, y, residual, as_stream(stream));
+                                 float* workspace, flyai_stream_t stream) {
+  FLYAI_REQUIRE(M >= 0 && N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0 && K <= 8192,
+                "linear: need N %% 16 == 0, K %% 32 == 0, K <= 8192");
+  FLYAI_REQUIRE(x && w && (y || residual) && workspace, "linear: null pointer");
+  return launch_linear(x, w, b, M, N, K, y, residual, workspace, as_stream(stream));
 }
 
 extern "C" int flyai_rope_kv_append(const uint16_t* qkv, const int32_t* positions,

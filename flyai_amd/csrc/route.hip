@@ -7,113 +7,166 @@
 namespace flyai {
 
 // ------------------------------------------------------------------------------------------------
-// Router: one workgroup (4 waves) per TT tokens.  x rows staged in LDS; each wave owns every 4th
-// expert; the router weight row is read once per workgroup and reused for all TT tokens.
-template <int TT>
-__global__ __launch_bounds__(256) void router_topk_softmax_kernel(
+// Router logits: workgroup = (TT tokens, 4*EPW experts); x rows staged in LDS; wave w owns EPW
+// experts.  Lane l accumulates k = 512 j + 8 l + i (i = 0..7) in order -- one 16-byte load of the
+// weight row and one 16-byte LDS read of x per chunk -- then a xor butterfly.  All JMAX weight
+// chunks of the wave's experts are loaded before the first FMA (one memory round trip).
+template <int TT, int EPW, int JMAX, bool ROUND_BF16>
+__global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b,
-    int T, int H, int E, int k, int32_t* __restrict__ topk_ids, float* __restrict__ topk_w,
-    float* __restrict__ logits_out) {
-  extern __shared__ uint16_t xs[];                  // [TT][H]
-  __shared__ float logits[TT][256];
+    int T, int H, int E, float* __restrict__ logits) {
+  extern __shared__ uint16_t xs[];  // [TT][H]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t0 = blockIdx.x * TT;
   const int nt = min(TT, T - t0);
-  // stage x rows (16-byte vectors; H % 64 == 0 so rows are 16-byte aligned)
+  const int e0 = blockIdx.y * 4 * EPW + wave * EPW;
+  uint4 wv[EPW][JMAX];
+#pragma unroll
+  for (int c = 0; c < EPW; ++c)
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) {
+      const int k0 = 512 * j + 8 * lane;
+      wv[c][j] = (e0 + c < E && k0 < H) ? *reinterpret_cast<const uint4*>(w + (size_t)(e0 + c) * H + k0)
+                                        : make_uint4(0, 0, 0, 0);
+    }
   const int vecs = H / 8;
-  for (int i = tid; i < nt * vecs; i += 256) {
-    int t = i / vecs, v = i % vecs;
-    reinterpret_cast<uint4*>(xs + t * H)[v] = reinterpret_cast<const uint4*>(x + (size_t)(t0 + t) * H)[v];
+  for (int i = tid; i < TT * vecs; i += 256) {
+    const int t = i / vecs, v = i % vecs;
+    reinterpret_cast<uint4*>(xs + t * H)[v] =
+        t < nt ? reinterpret_cast<const uint4*>(x + (size_t)(t0 + t) * H)[v] : make_uint4(0, 0, 0, 0);
   }
   __syncthreads();
-  const int J = H / 64;
-  for (int e = wave; e < E; e += 4) {
-    float acc[TT];
+  float acc[EPW][TT];
 #pragma unroll
-    for (int t = 0; t < TT; ++t) acc[t] = 0.f;
-    const uint16_t* wr = w + (size_t)e * H + lane;
-    for (int j = 0; j < J; ++j) {
-      const float wv = bf2f(wr[64 * j]);
+  for (int c = 0; c < EPW; ++c)
 #pragma unroll
-      for (int t = 0; t < TT; ++t)
-        acc[t] = fmaf(bf2f(xs[t * H + lane + 64 * j]), wv, acc[t]);   // exact product: fma == mul+add
-    }
-    const float bias = bf2f(b[e]);
+    for (int t = 0; t < TT; ++t) acc[c][t] = 0.f;
+#pragma unroll
+  for (int j = 0; j < JMAX; ++j) {
+    const int k0 = 512 * j + 8 * lane;
+    if (k0 >= H) break;  // lanes past the row end keep their partial unchanged
 #pragma unroll
     for (int t = 0; t < TT; ++t) {
-      float v = acc[t];
+      const uint4 xv = *reinterpret_cast<const uint4*>(xs + t * H + k0);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
-      if (lane == 0) logits[t][e] = bf16_round(v + bias);
+      for (int c = 0; c < EPW; ++c) {
+        const uint32_t ww[4] = {wv[c][j].x, wv[c][j].y, wv[c][j].z, wv[c][j].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float xf = __uint_as_float((i & 1) ? (xw[i >> 1] & 0xffff0000u) : (xw[i >> 1] << 16));
+          const float wf = __uint_as_float((i & 1) ? (ww[i >> 1] & 0xffff0000u) : (ww[i >> 1] << 16));
+          acc[c][t] = fmaf(xf, wf, acc[c][t]);  // exact product: fma == mul + add
+        }
+      }
     }
   }
-  __syncthreads();
-  // top-k per token: wave w handles tokens w, w+4, ...
-  for (int t = wave; t < nt; t += 4) {
-    float cv[4];
-    int ci[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      ci[c] = lane + 64 * c;
-      cv[c] = ci[c] < E ? logits[t][ci[c]] : -INFINITY;
-      if (ci[c] >= E) ci[c] = 0x7fffffff;
-    }
-    if (logits_out) {
-      for (int c = 0; c < 4; ++c)
-        if (lane + 64 * c < E) logits_out[(size_t)(t0 + t) * E + lane + 64 * c] = cv[c];
-    }
-    float sv[8];
-    int si[8];
-    for (int r = 0; r < k; ++r) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
+  for (int c = 0; c < EPW; ++c) {
+    const float bias = (e0 + c < E && b) ? bf2f(b[e0 + c]) : 0.f;
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (cv[c] > bv || (cv[c] == bv && ci[c] < bi)) { bv = cv[c]; bi = ci[c]; }
+    for (int t = 0; t < TT; ++t) {
+      float v = acc[c][t];
 #pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        float ov = __shfl_xor(bv, off, 64);
-        int oi = __shfl_xor(bi, off, 64);
-        if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
-      }
-      sv[r] = bv;
-      si[r] = bi;
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (ci[c] == bi) { cv[c] = -INFINITY; ci[c] = 0x7fffffff; }
-    }
-    if (lane == 0) {
-      const float m = sv[0];
-      float ex[8], sum = 0.f;
-      for (int r = 0; r < k; ++r) { ex[r] = expf(sv[r] - m); sum += ex[r]; }
-      // ascending ids, weights carried along (insertion sort, k <= 8)
-      for (int r = 1; r < k; ++r) {
-        int id = si[r];
-        float e2 = ex[r];
-        int q = r - 1;
-        while (q >= 0 && si[q] > id) { si[q + 1] = si[q]; ex[q + 1] = ex[q]; --q; }
-        si[q + 1] = id;
-        ex[q + 1] = e2;
-      }
-      for (int r = 0; r < k; ++r) {
-        topk_ids[(size_t)(t0 + t) * k + r] = si[r];
-        topk_w[(size_t)(t0 + t) * k + r] = ex[r] / sum;
+      for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+      if (lane == 0 && t < nt && e0 + c < E) {
+        const float r = v + bias;
+        logits[(size_t)(t0 + t) * E + e0 + c] = ROUND_BF16 ? bf16_round(r) : r;
       }
     }
   }
 }
 
+// Top-k + softmax of one token by one lane.  The lane streams its token's logits in ascending expert
+// id and keeps a sorted list of K (value, id); a value enters only if strictly greater than the
+// current K-th and bubbles up past strictly smaller values, so equal values keep ascending ids --
+// the (value desc, id asc) order.  Softmax over the K selected values in fp32, then ids sorted
+// ascending carrying their weights.  Logit rows are 16-byte aligned (E % 4 == 0).
+template <int K>
+__device__ __forceinline__ void topk_softmax_lane(const float* __restrict__ lrow, int E,
+                                                  int32_t* ids_out, float* w_out) {
+  float sv[K];
+  int si[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) { sv[j] = -INFINITY; si[j] = 0x7fffffff; }
+  for (int e0 = 0; e0 < E; e0 += 16) {
+    float4 v4[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      v4[c] = (e0 + 4 * c < E) ? reinterpret_cast<const float4*>(lrow + e0)[c]
+                               : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float4& q = v4[i >> 2];
+      const float v = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
+      const int id = e0 + i;
+      if (id < E && v > sv[K - 1]) {
+        sv[K - 1] = v;
+        si[K - 1] = id;
+#pragma unroll
+        for (int j = K - 1; j > 0; --j) {
+          if (sv[j] > sv[j - 1]) {
+            const float tv = sv[j]; sv[j] = sv[j - 1]; sv[j - 1] = tv;
+            const int ti = si[j]; si[j] = si[j - 1]; si[j - 1] = ti;
+          }
+        }
+      }
+    }
+  }
+  float ex[K], sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < K; ++j) { ex[j] = expf(sv[j] - sv[0]); sum += ex[j]; }
+  // ascending ids (odd-even transposition sort, K passes)
+#pragma unroll
+  for (int pass = 0; pass < K; ++pass)
+#pragma unroll
+    for (int j = pass & 1; j + 1 < K; j += 2)
+      if (si[j] > si[j + 1]) {
+        const int ti = si[j]; si[j] = si[j + 1]; si[j + 1] = ti;
+        const float te = ex[j]; ex[j] = ex[j + 1]; ex[j + 1] = te;
+      }
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    ids_out[j] = si[j];
+    w_out[j] = ex[j] / sum;
+  }
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int T,
+                                                          int E, int32_t* __restrict__ topk_ids,
+                                                          float* __restrict__ topk_w) {
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= T) return;
+  topk_softmax_lane<K>(logits + (size_t)t * E, E, topk_ids + (size_t)t * K, topk_w + (size_t)t * K);
+}
+
+int launch_router_logits(const uint16_t* x, const uint16_t* w, const uint16_t* b, int T, int H,
+                         int E, float* logits, hipStream_t s) {
+  if (H <= 3072) {  // 8 staged rows stay under 48 KiB of LDS; 6 chunks of 512
+    hipLaunchKernelGGL((router_logits_kernel<8, 2, 6, true>), dim3(ceil_div(T, 8), ceil_div(E, 8)),
+                       dim3(256), 8 * H * sizeof(uint16_t), s, x, w, b, T, H, E, logits);
+  } else {
+    hipLaunchKernelGGL((router_logits_kernel<4, 1, 14, true>), dim3(ceil_div(T, 4), ceil_div(E, 4)),
+                       dim3(256), 4 * H * sizeof(uint16_t), s, x, w, b, T, H, E, logits);
+  }
+  return check_launch("router_logits");
+}
+
 int launch_router(const uint16_t* x, const uint16_t* w, const uint16_t* b, int T, int H, int E,
                   int k, int32_t* ids, float* wts, float* logits, hipStream_t s) {
   if (T == 0) return FLYAI_OK;
-  if (H <= 3072) {  // 8 rows of x + logits stay under 64 KiB of LDS
-    hipLaunchKernelGGL(router_topk_softmax_kernel<8>, dim3(ceil_div(T, 8)), dim3(256),
-                       8 * H * sizeof(uint16_t), s, x, w, b, T, H, E, k, ids, wts, logits);
-  } else {
-    hipLaunchKernelGGL(router_topk_softmax_kernel<4>, dim3(ceil_div(T, 4)), dim3(256),
-                       4 * H * sizeof(uint16_t), s, x, w, b, T, H, E, k, ids, wts, logits);
-  }
-  return check_launch("router_topk_softmax");
+  int rc = launch_router_logits(x, w, b, T, H, E, logits, s);
+  if (rc) return rc;
+  if (k == 4)
+    hipLaunchKernelGGL(router_topk_kernel<4>, dim3(ceil_div(T, 256)), dim3(256), 0, s, logits, T, E, ids, wts);
+  else if (k == 8)
+    hipLaunchKernelGGL(router_topk_kernel<8>, dim3(ceil_div(T, 256)), dim3(256), 0, s, logits, T, E, ids, wts);
+  else if (k == 2)
+    hipLaunchKernelGGL(router_topk_kernel<2>, dim3(ceil_div(T, 256)), dim3(256), 0, s, logits, T, E, ids, wts);
+  else
+    return set_error(FLYAI_EINVAL, "router: top_k must be 2, 4 or 8");
+  return check_launch("router_topk");
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -134,11 +187,10 @@ __device__ __forceinline__ uint64_t match_peers(int e, bool valid, int nbits) {
   return peers;
 }
 
-__global__ __launch_bounds__(kPermWaves * 64) void moe_permute_kernel(
-    const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ hist_out,
-    int32_t* __restrict__ off_out, int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
-  __shared__ int32_t cnt[kPermWaves][256];
-  __shared__ int32_t off[256];
+// ids may live in global memory or LDS; called by all kPermWaves*64 threads of the workgroup.
+__device__ void permute_block(const int32_t* ids, int P, int E, int32_t* __restrict__ hist_out,
+                              int32_t* __restrict__ off_out, int32_t* __restrict__ perm,
+                              int32_t* __restrict__ inv, int32_t (*cnt)[256], int32_t* off) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   for (int i = tid; i < kPermWaves * 256; i += kPermWaves * 64) (&cnt[0][0])[i] = 0;
   __syncthreads();
@@ -164,11 +216,11 @@ __global__ __launch_bounds__(kPermWaves * 64) void moe_permute_kernel(
   }
   __syncthreads();
   if (wave == 0) {  // exclusive scan of off[0..E), 4 entries per lane
-    int v[4], s = 0;
-    for (int c = 0; c < 4; ++c) { int i = lane * 4 + c; v[c] = i < E ? off[i] : 0; s += v[c]; }
-    int incl = s;
+    int v[4], sum = 0;
+    for (int c = 0; c < 4; ++c) { int i = lane * 4 + c; v[c] = i < E ? off[i] : 0; sum += v[c]; }
+    int incl = sum;
     for (int o = 1; o < 64; o <<= 1) { int y = __shfl_up(incl, o, 64); if (lane >= o) incl += y; }
-    int run = incl - s;
+    int run = incl - sum;
     for (int c = 0; c < 4; ++c) { int i = lane * 4 + c; if (i < E) off[i] = run; run += v[c]; }
   }
   __syncthreads();
@@ -194,6 +246,61 @@ __global__ __launch_bounds__(kPermWaves * 64) void moe_permute_kernel(
   }
 }
 
+__global__ __launch_bounds__(kPermWaves * 64) void moe_permute_kernel(
+    const int32_t* __restrict__ ids, int P, int E, int32_t* __restrict__ hist_out,
+    int32_t* __restrict__ off_out, int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
+  __shared__ int32_t cnt[kPermWaves][256];
+  __shared__ int32_t off[256];
+  permute_block(ids, P, E, hist_out, off_out, perm, inv, cnt, off);
+}
+
+// Small batches: top-k of every token (one lane per token) into LDS, then the permute, in one
+// workgroup -- one launch instead of two.
+constexpr int kFusedMaxAssign = 4096;
+
+template <int K>
+__global__ __launch_bounds__(kPermWaves * 64) void moe_topk_permute_kernel(
+    const float* __restrict__ logits, int T, int E, int32_t* __restrict__ topk_ids,
+    float* __restrict__ topk_w, int32_t* __restrict__ hist_out, int32_t* __restrict__ off_out,
+    int32_t* __restrict__ perm, int32_t* __restrict__ inv) {
+  __shared__ int32_t cnt[kPermWaves][256];
+  __shared__ int32_t off[256];
+  __shared__ int32_t ids_s[kFusedMaxAssign];
+  for (int t = threadIdx.x; t < T; t += kPermWaves * 64)
+    topk_softmax_lane<K>(logits + (size_t)t * E, E, ids_s + t * K, topk_w + (size_t)t * K);
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * K; i += kPermWaves * 64) topk_ids[i] = ids_s[i];
+  permute_block(ids_s, T * K, E, hist_out, off_out, perm, inv, cnt, off);
+}
+
+int launch_permute(const int32_t* ids, int T, int k, int E, int32_t* hist, int32_t* offsets,
+                   int32_t* perm, int32_t* inv, hipStream_t s);
+
+int launch_route_permute(const uint16_t* x, const uint16_t* w, const uint16_t* b, int T, int H,
+                         int E, int k, int32_t* ids, float* wts, float* logits, int32_t* hist,
+                         int32_t* offsets, int32_t* perm, int32_t* inv, hipStream_t s) {
+  if (T == 0) return FLYAI_OK;
+  if (T * k > kFusedMaxAssign) {
+    int rc = launch_router(x, w, b, T, H, E, k, ids, wts, logits, s);
+    if (rc) return rc;
+    return launch_permute(ids, T, k, E, hist, offsets, perm, inv, s);
+  }
+  int rc = launch_router_logits(x, w, b, T, H, E, logits, s);
+  if (rc) return rc;
+  if (k == 4)
+    hipLaunchKernelGGL(moe_topk_permute_kernel<4>, dim3(1), dim3(kPermWaves * 64), 0, s, logits, T, E,
+                       ids, wts, hist, offsets, perm, inv);
+  else if (k == 8)
+    hipLaunchKernelGGL(moe_topk_permute_kernel<8>, dim3(1), dim3(kPermWaves * 64), 0, s, logits, T, E,
+                       ids, wts, hist, offsets, perm, inv);
+  else if (k == 2)
+    hipLaunchKernelGGL(moe_topk_permute_kernel<2>, dim3(1), dim3(kPermWaves * 64), 0, s, logits, T, E,
+                       ids, wts, hist, offsets, perm, inv);
+  else
+    return set_error(FLYAI_EINVAL, "route: top_k must be 2, 4 or 8");
+  return check_launch("moe_topk_permute");
+}
+
 int launch_permute(const int32_t* ids, int T, int k, int E, int32_t* hist, int32_t* offsets,
                    int32_t* perm, int32_t* inv, hipStream_t s) {
   hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(kPermWaves * 64), 0, s, ids, T * k, E,
@@ -202,16 +309,23 @@ int launch_permute(const int32_t* ids, int T, int k, int E, int32_t* hist, int32
 }
 
 // ------------------------------------------------------------------------------------------------
-// Combine: out[t] = bf16(sum_s w[t,s] * y_perm[inv[t*k+s]]) (+ residual, rounded again).
-__global__ __launch_bounds__(256) void moe_combine_kernel(
+// Combine: out[t] = bf16(sum_s w[t,s] * y_perm[inv[t*k+s]]) (+ residual, rounded again).  When lnw is
+// given, the next layer's input RMSNorm of the new row is written to xn as well (fused: the row is
+// already in this workgroup).
+constexpr int kCombineThreads = 1024;
+
+__global__ __launch_bounds__(kCombineThreads) void moe_combine_kernel(
     const float* __restrict__ y_perm, const int32_t* __restrict__ inv,
-    const float* __restrict__ topk_w, int k, int H, const uint16_t* residual, uint16_t* out) {
-  const int t = blockIdx.x;
+    const float* __restrict__ topk_w, int k, int H, const uint16_t* residual, uint16_t* out,
+    const float* __restrict__ lnw, float eps, uint16_t* __restrict__ xn) {
+  __shared__ float red[kCombineThreads / 64];
+  const int t = blockIdx.x, tid = threadIdx.x;
   int rows[8];
   float wt[8];
   for (int s = 0; s < k; ++s) { rows[s] = inv[t * k + s]; wt[s] = topk_w[t * k + s]; }
   const int H4 = H / 4;
-  for (int i = threadIdx.x; i < H4; i += 256) {
+  float ss = 0.f;
+  for (int i = tid; i < H4; i += kCombineThreads) {
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s = 0; s < k; ++s) {
       const float4 y = reinterpret_cast<const float4*>(y_perm + (size_t)rows[s] * H)[i];
@@ -226,18 +340,36 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
       o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16);
       o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
     }
+    uint16_t ob[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      ob[c] = f2bf(o[c]);
+      const float hf = bf2f(ob[c]);
+      ss = fmaf(hf, hf, ss);
+    }
     uint2 ov;
-    ov.x = (uint32_t)f2bf(o[0]) | ((uint32_t)f2bf(o[1]) << 16);
-    ov.y = (uint32_t)f2bf(o[2]) | ((uint32_t)f2bf(o[3]) << 16);
+    ov.x = (uint32_t)ob[0] | ((uint32_t)ob[1] << 16);
+    ov.y = (uint32_t)ob[2] | ((uint32_t)ob[3] << 16);
     reinterpret_cast<uint2*>(out + (size_t)t * H)[i] = ov;
   }
+  if (!lnw) return;
+  ss = warp_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kCombineThreads / 64; ++w) tot += red[w];
+  const float rr = rsqrtf(tot / (float)H + eps);
+  for (int i = tid; i < H; i += kCombineThreads)
+    xn[(size_t)t * H + i] = f2bf(lnw[i] * (bf2f(out[(size_t)t * H + i]) * rr));
 }
 
 int launch_combine(const float* y_perm, const int32_t* inv, const float* w, int T, int k, int H,
-                   const uint16_t* residual, uint16_t* out, hipStream_t s) {
+                   const uint16_t* residual, uint16_t* out, const float* lnw, float eps,
+                   uint16_t* xn, hipStream_t s) {
   if (T == 0) return FLYAI_OK;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, s, y_perm, inv, w, k, H,
-                     residual, out);
+  hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(kCombineThreads), 0, s, y_perm, inv, w, k, H, residual,
+                     out, lnw, eps, xn);
   return check_launch("moe_combine");
 }
 
@@ -249,9 +381,11 @@ extern "C" int flyai_router_topk_softmax(const uint16_t* x, const uint16_t* w, c
                                          int32_t T, int32_t H, int32_t E, int32_t k,
                                          int32_t* topk_ids, float* topk_w, float* logits_out,
                                          flyai_stream_t stream) {
-  FLYAI_REQUIRE(T >= 0 && H > 0 && H % 64 == 0 && H <= 7168, "router: H must be a multiple of 64 <= 7168");
-  FLYAI_REQUIRE(E >= 1 && E <= 256 && k >= 1 && k <= 8 && k <= E, "router: need 1<=E<=256, 1<=k<=min(8,E)");
-  FLYAI_REQUIRE(x && w && b && topk_ids && topk_w, "router: null pointer");
+  FLYAI_REQUIRE(T >= 0 && H > 0 && H <= 7168, "router: H must be <= 7168");
+  FLYAI_REQUIRE(E >= 4 && E <= 256 && E % 4 == 0 && (k == 2 || k == 4 || k == 8) && k <= E,
+                "router: need E %% 4 == 0, 4 <= E <= 256, k in {2, 4, 8}");
+  FLYAI_REQUIRE(x && w && b && topk_ids && topk_w && logits_out, "router: null pointer");
+  FLYAI_REQUIRE(H % 8 == 0, "router: H must be a multiple of 8");
   return launch_router(x, w, b, T, H, E, k, topk_ids, topk_w, logits_out, as_stream(stream));
 }
 
@@ -269,5 +403,21 @@ extern "C" int flyai_moe_combine(const float* y_perm, const int32_t* inv, const 
                                  uint16_t* out, flyai_stream_t stream) {
   FLYAI_REQUIRE(T >= 0 && k >= 1 && k <= 8 && H > 0 && H % 4 == 0, "combine: bad shape");
   FLYAI_REQUIRE(y_perm && inv && topk_w && out, "combine: null pointer");
-  return launch_combine(y_perm, inv, topk_w, T, k, H, residual, out, as_stream(stream));
+  return launch_combine(y_perm, inv, topk_w, T, k, H, residual, out, nullptr, 0.f, nullptr,
+                        as_stream(stream));
+}
+
+extern "C" int flyai_moe_route_permute(const uint16_t* x, const uint16_t* w, const uint16_t* b,
+                                       int32_t T, int32_t H, int32_t E, int32_t k,
+                                       int32_t* topk_ids, float* topk_w, float* logits,
+                                       int32_t* hist, int32_t* offsets, int32_t* perm, int32_t* inv,
+                                       flyai_stream_t stream) {
+  FLYAI_REQUIRE(T >= 0 && H > 0 && H <= 7168 && H % 8 == 0, "route_permute: H must be a multiple of 8 <= 7168");
+  FLYAI_REQUIRE(E >= 4 && E <= 256 && E % 4 == 0 && (k == 2 || k == 4 || k == 8) && k <= E &&
+                    (int64_t)T * k <= 65536,
+                "route_permute: need E %% 4 == 0, 4 <= E <= 256, k in {2, 4, 8}, T*k <= 65536");
+  FLYAI_REQUIRE(x && w && b && topk_ids && topk_w && logits && hist && offsets && perm && inv,
+                "route_permute: null pointer");
+  return launch_route_permute(x, w, b, T, H, E, k, topk_ids, topk_w, logits, hist, offsets, perm, inv,
+                              as_stream(stream));
 }

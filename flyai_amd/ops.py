@@ -60,7 +60,7 @@ def router_topk_softmax(x, w, b, k, want_logits=False):
     _need(b, torch.bfloat16, (E,), "router bias")
     ids = torch.empty(T, k, dtype=torch.int32, device=x.device)
     wts = torch.empty(T, k, dtype=torch.float32, device=x.device)
-    logits = torch.empty(T, E, dtype=torch.float32, device=x.device) if want_logits else None
+    logits = torch.empty(T, E, dtype=torch.float32, device=x.device)
     check(lib().flyai_router_topk_softmax(_ptr(x), _ptr(w), _ptr(b), T, H, E, k, _ptr(ids), _ptr(wts),
                                           _ptr(logits), _stream()))
     return (ids, wts, logits) if want_logits else (ids, wts)
@@ -77,6 +77,27 @@ def moe_permute(ids, n_experts):
     check(lib().flyai_moe_permute(_ptr(ids), T, k, n_experts, _ptr(hist), _ptr(offsets), _ptr(perm),
                                   _ptr(inv), _stream()))
     return hist, offsets, perm, inv
+
+
+def moe_route_permute(x, w, b, k):
+    """Router + histogram/permute as the stage runs it -> (ids, weights, hist, offsets, perm, inv)."""
+    T, H = x.shape
+    E = w.shape[0]
+    _need(x, torch.bfloat16, (T, H), "x")
+    _need(w, torch.bfloat16, (E, H), "router weight")
+    _need(b, torch.bfloat16, (E,), "router bias")
+    dev = x.device
+    ids = torch.empty(T, k, dtype=torch.int32, device=dev)
+    wts = torch.empty(T, k, dtype=torch.float32, device=dev)
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    hist = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    perm = torch.empty(T * k, dtype=torch.int32, device=dev)
+    inv = torch.empty(T * k, dtype=torch.int32, device=dev)
+    check(lib().flyai_moe_route_permute(_ptr(x), _ptr(w), _ptr(b), T, H, E, k, _ptr(ids), _ptr(wts),
+                                        _ptr(logits), _ptr(hist), _ptr(offsets), _ptr(perm), _ptr(inv),
+                                        _stream()))
+    return ids, wts, hist, offsets, perm, inv
 
 
 def moe_combine(y_perm, inv, topk_w, residual=None, out=None):
@@ -156,7 +177,10 @@ def linear(x, w, b=None, residual=None):
         _need(residual, torch.bfloat16, (M, N), "residual")
     else:
         y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
-    check(lib().flyai_linear_bf16(_ptr(x), _ptr(w), _ptr(b), M, N, K, _ptr(y), _ptr(residual), _stream()))
+    ws = torch.empty(max(1, int(lib().flyai_linear_workspace_bytes(M, N, K)) // 4), dtype=torch.float32,
+                     device=x.device)
+    check(lib().flyai_linear_bf16(_ptr(x), _ptr(w), _ptr(b), M, N, K, _ptr(y), _ptr(residual), _ptr(ws),
+                                  _stream()))
     return residual if residual is not None else y
 
 
@@ -182,23 +206,23 @@ def rope_kv_append(qkv, positions, seq_id, cos_tab, sin_tab, n_q_heads, n_kv_hea
 
 
 def attn_plan(q_lens, starts, n_kv_heads, window, split_keys, max_items=1 << 20):
-    """Host planner -> (items tensor int32 [n, 8], groups tensor int32 [g, 8]) on the CPU."""
+    """Host planner -> (items int32 [n, 8], groups int32 [g, 8], n_small) on the CPU."""
     S = len(q_lens)
     ql = (C.c_int32 * S)(*[int(v) for v in q_lens])
     st = (C.c_int32 * S)(*[int(v) for v in starts])
     max_groups = (S + sum((int(v) + 3) // 4 for v in q_lens)) * n_kv_heads
     items = (_lib.AttnItem * max_items)()
     groups = (_lib.AttnGroup * max_groups)()
-    ni, ng = C.c_int32(0), C.c_int32(0)
+    ni, ng, ns = C.c_int32(0), C.c_int32(0), C.c_int32(0)
     check(lib().flyai_attn_plan(ql, st, S, n_kv_heads, window, split_keys, items, max_items, groups,
-                                max_groups, C.byref(ni), C.byref(ng)))
+                                max_groups, C.byref(ni), C.byref(ng), C.byref(ns)))
     it = torch.frombuffer(bytearray(items), dtype=torch.int32).view(max_items, 8)[:ni.value].clone()
     gr = torch.frombuffer(bytearray(groups), dtype=torch.int32).view(max_groups, 8)[:ng.value].clone()
-    return it, gr
+    return it, gr, ns.value
 
 
-def attn_ragged(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, items, groups, n_kv_heads):
-    """q bf16 [T, Hq, 64]; items/groups from attn_plan (moved to the GPU here)."""
+def attn_ragged(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, items, groups, n_small, n_kv_heads):
+    """q bf16 [T, Hq, 64]; items/groups/n_small from attn_plan (moved to the GPU here)."""
     T, Hq, D = q.shape
     _need(q, torch.bfloat16, (T, Hq, D), "q")
     _need(sinks, torch.float32, (Hq,), "sinks")
@@ -210,5 +234,6 @@ def attn_ragged(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, items, groups
     out = torch.empty_like(q)
     check(lib().flyai_attn_ragged(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(kv_base), _ptr(kv_cap),
                                   _ptr(sinks), window, Hq, n_kv_heads, D, _ptr(items_d), items.shape[0],
-                                  _ptr(groups_d), groups.shape[0], _ptr(parts), _ptr(out), _stream()))
+                                  n_small, _ptr(groups_d), groups.shape[0], _ptr(parts), _ptr(out),
+                                  _stream()))
     return out

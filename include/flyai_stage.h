@@ -59,10 +59,11 @@ int flyai_pack_ragged(const int32_t* q_lens, const int32_t* starts, const int64_
  * (transformers/models/gpt_oss/modeling_gpt_oss.py:126-130) and the native path's bf16 router
  * Linear + hub `routing` (transformers/integrations/mxfp4.py:484-487, torch restatement
  * routing_torch_dist :435-444).  x bf16 [T,H], w bf16 [E,H], b bf16 [E].  Logits are the bf16
- * rounding of an fp32 dot product in a fixed order (64 lane partials k = l + 64j, xor butterfly)
- * plus bias; top-k by (value desc, id asc); softmax over the k selected values in fp32; each row's
- * ids sorted ascending with their weights.  H % 64 == 0, H <= 7168, E <= 256, k <= 8.
- * logits_out (fp32 [T,E], may be NULL) receives the bf16-valued logits. */
+ * rounding of an fp32 dot product in a fixed order (64 lane partials, lane l summing
+ * k = 512j + 8l + i in order, then a xor butterfly 32..1) plus bias; top-k by (value desc, id asc);
+ * softmax over the k selected values in fp32; each row's ids sorted ascending with their weights.
+ * H % 8 == 0, H <= 7168, E % 4 == 0, E <= 256, k in {2, 4, 8}.  logits_out (fp32 [T,E], required) receives the
+ * bf16-valued logits and is the scratch between the logits and top-k kernels. */
 int flyai_router_topk_softmax(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t T,
                               int32_t H, int32_t E, int32_t k, int32_t* topk_ids, float* topk_w,
                               float* logits_out, flyai_stream_t stream);
@@ -75,6 +76,14 @@ int flyai_router_topk_softmax(const uint16_t* x, const uint16_t* w, const uint16
  * within an expert), inv[T*k] (inverse).  T*k <= 65536, E <= 256. */
 int flyai_moe_permute(const int32_t* topk_ids, int32_t T, int32_t k, int32_t E, int32_t* hist,
                       int32_t* offsets, int32_t* perm, int32_t* inv, flyai_stream_t stream);
+
+/* a2 + a3 in one call (the stage's path): router logits, then -- for T*k <= 4096 -- top-k of every
+ * token and the histogram / permute in a single one-workgroup kernel (separate kernels above that).
+ * Same outputs and bit-exact indices as flyai_router_topk_softmax followed by flyai_moe_permute. */
+int flyai_moe_route_permute(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t T,
+                            int32_t H, int32_t E, int32_t k, int32_t* topk_ids, float* topk_w,
+                            float* logits, int32_t* hist, int32_t* offsets, int32_t* perm,
+                            int32_t* inv, flyai_stream_t stream);
 
 /* ---- a4: unpermute / combine -------------------------------------------------------------------
  * Replaces the weighted index_add_ of GptOssExperts.forward (modeling_gpt_oss.py:108-113) / the
@@ -116,7 +125,8 @@ int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, const uint8_
  * RMSNorm: GptOssRMSNorm.forward (modeling_gpt_oss.py:57-62): y = bf16(w * (x * rsqrt(mean(x^2)+eps)))
  * with fp32 weight.  Linear: q/k/v/o projections (modeling_gpt_oss.py:280-291): y = bf16(x W^T + b),
  * W bf16 [N,K]; with residual non-NULL the result is bf16(residual + y) written to residual
- * (the residual add of modeling_gpt_oss.py:369).  RoPE + KV append: GPT-OSS half-split rotary
+ * (the residual add of modeling_gpt_oss.py:369); the product is a split-K GEMM whose fp32 partial
+ * sums (flyai_linear_workspace_bytes) are added in a fixed order by a finalize kernel.  RoPE + KV append: GPT-OSS half-split rotary
  * (modeling_gpt_oss.py:215-232) with per-op bf16 rounding, then the K/V write at each token's
  * position (StaticKV.update, phase0/fastverify.py:71-77; BatchedStaticKV.update,
  * phase0/batchverify.py:42-48).  KV pool layout per sequence slab (element offset kv_base[b]):
@@ -124,8 +134,10 @@ int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, const uint8_
  * [rope_positions][D/2]; a token whose position is outside the table or its slab is skipped. */
 int flyai_rmsnorm(const uint16_t* x, const float* w, int32_t T, int32_t H, float eps, uint16_t* y,
                   flyai_stream_t stream);
+size_t flyai_linear_workspace_bytes(int32_t M, int32_t N, int32_t K);
 int flyai_linear_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t M, int32_t N,
-                      int32_t K, uint16_t* y, uint16_t* residual, flyai_stream_t stream);
+                      int32_t K, uint16_t* y, uint16_t* residual, float* workspace,
+                      flyai_stream_t stream);
 int flyai_rope_kv_append(const uint16_t* qkv, const int32_t* positions, const int32_t* seq_id,
                          const uint16_t* cos_tab, const uint16_t* sin_tab, int32_t rope_positions,
                          int32_t T, int32_t Hq, int32_t Hkv, int32_t D, const int64_t* kv_base,
@@ -139,7 +151,9 @@ int flyai_rope_kv_append(const uint16_t* qkv, const int32_t* positions, const in
  * keys j in [lo, p], lo = 0 or max(0, p-window+1); logits scaled by D^-0.5; the per-head sink
  * logit joins the softmax denominator only.  q bf16 [T,Hq,D] (rotated); out bf16 [T,Hq,D].
  * Work is split over (sequence, kv head, group of <= 4 query tokens, key split); the host-side
- * plan (flyai_attn_plan) is uploaded into `plan_dev` by the caller.  D == 64, Hq/Hkv == 8.
+ * plan (flyai_attn_plan) is copied to the device by the caller.  The plan lists groups of <= 2
+ * tokens first (n_items_small items, run by a one-tile kernel variant), then the rest.  D == 64,
+ * Hq/Hkv == 8, kv_cap[b] % 64 == 0, kv_base[b] % 8 == 0, starts[b] + q_lens[b] <= kv_cap[b].
  * Partials scratch: flyai_attn_partials_bytes(n_items). */
 typedef struct {
   int32_t seq;      /* sequence index b */
@@ -164,12 +178,12 @@ typedef struct {
 int flyai_attn_plan(const int32_t* q_lens_host, const int32_t* starts_host, int32_t n_seqs,
                     int32_t Hkv, int32_t window, int32_t split_keys, flyai_attn_item* items_host,
                     int32_t max_items, flyai_attn_group* groups_host, int32_t max_groups,
-                    int32_t* n_items, int32_t* n_groups);
+                    int32_t* n_items, int32_t* n_groups, int32_t* n_items_small);
 size_t flyai_attn_partials_bytes(int32_t n_items);
 int flyai_attn_ragged(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
                       const int64_t* kv_base, const int32_t* kv_cap, const float* sinks,
                       int32_t window, int32_t Hq, int32_t Hkv, int32_t D,
-                      const flyai_attn_item* items_dev, int32_t n_items,
+                      const flyai_attn_item* items_dev, int32_t n_items, int32_t n_items_small,
                       const flyai_attn_group* groups_dev, int32_t n_groups, float* partials,
                       uint16_t* out, flyai_stream_t stream);
 
@@ -222,7 +236,7 @@ int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t dev_bytes, v
 int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens_host, const int32_t* starts_host,
                         const int64_t* kv_base_host, const int32_t* kv_cap_host, int32_t n_seqs,
                         uint16_t* hidden, flyai_stream_t stream);
-/* Device pointer of an internal buffer of the last step (for tests): 0 xn, 1 qkv, 2 q_rot,
+/* Device pointer of an internal buffer of the last step (for tests): 0 xn, 1 gemm partials, 2 q_rot,
  * 3 attn_out, 4 topk_ids, 5 topk_w, 6 offsets, 7 perm, 8 inv, 9 h_moe, 10 y_perm, 11 positions,
  * 12 seq_id, 13 cu_seqlens. */
 void* flyai_stage_debug_buffer(flyai_stage* st, int32_t which);

@@ -3,9 +3,11 @@
 Numerical contract (shared with the HIP kernels, which must match the INDICES bit-exactly):
 
 * ``dot_fixed`` -- every router logit is an fp32 dot product over K bf16 x bf16 terms in one fixed
-  order: 64 lane partials, lane l summing k = l, l+64, l+128, ... sequentially (each bf16*bf16
-  product is exact in fp32, so FMA and mul+add round identically), then a xor butterfly over lanes
-  with offsets 32, 16, 8, 4, 2, 1.  Fixing the order is what makes the indices reproducible.
+  order: 64 lane partials, lane l summing k = 512*j + 8*l + i for j = 0, 1, ... and i = 0..7 (only
+  k < K) sequentially (each bf16*bf16 product is exact in fp32, so FMA and mul+add round
+  identically), then a xor butterfly over lanes with offsets 32, 16, 8, 4, 2, 1.  Fixing the order
+  is what makes the indices reproducible; the lane-contiguous 8-element chunks are what a GPU lane
+  reads with one 16-byte load.
 * GPT-OSS (``transformers/models/gpt_oss/modeling_gpt_oss.py:126-130``; native MXFP4 path
   ``transformers/integrations/mxfp4.py:476-487``): logits = bf16(dot + bias) -- HF computes the
   router Linear in bf16, so the logits are bf16 values; top-k by (value desc, expert id asc), the
@@ -37,15 +39,20 @@ from .numerics import bf16
 
 def dot_fixed(x, w):
     """fp32 [T, K] x fp32 [E, K] -> fp32 [T, E] in the fixed 64-lane order described above.
-    x and w must hold bf16-representable values (exact products)."""
+    x and w must hold bf16-representable values (exact products); K % 8 == 0.  Zero padding to a
+    multiple of 512 adds exact +0.0 terms to partials that are never -0.0, so it changes nothing."""
     x = torch.as_tensor(x).float()
     w = torch.as_tensor(w).float()
     T, K = x.shape
     E = w.shape[0]
-    assert K % 64 == 0, "fixed-order router dot needs K % 64 == 0"
-    J = K // 64
-    xr = x.reshape(T, J, 64)
-    wr = w.reshape(E, J, 64)
+    assert K % 8 == 0, "fixed-order router dot needs K % 8 == 0"
+    J = (K + 511) // 512
+    pad = J * 512 - K
+    if pad:
+        x = torch.nn.functional.pad(x, (0, pad))
+        w = torch.nn.functional.pad(w, (0, pad))
+    xr = x.reshape(T, J, 64, 8)
+    wr = w.reshape(E, J, 64, 8)
     out = torch.empty(T, E, dtype=torch.float32)
     idx = torch.arange(64)
     step = max(1, (1 << 24) // max(1, E * 64))          # bound the [t, E, 64] temporaries
@@ -53,7 +60,8 @@ def dot_fixed(x, w):
         xs = xr[t0:t0 + step]
         acc = torch.zeros(xs.shape[0], E, 64, dtype=torch.float32)
         for j in range(J):
-            acc = acc + xs[:, None, j, :] * wr[None, :, j, :]
+            for i in range(8):
+                acc = acc + xs[:, None, j, :, i] * wr[None, :, j, :, i]
         for off in (32, 16, 8, 4, 2, 1):
             acc = acc + acc[..., idx ^ off]
         out[t0:t0 + step] = acc[..., 0]

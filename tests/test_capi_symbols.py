@@ -52,7 +52,7 @@ def test_packed_bytes_and_partials_bytes(lib):
 
 def test_attn_plan_host(lib):
     from flyai_amd import ops
-    items, groups = ops.attn_plan([1, 4, 6], [700, 0, 130], n_kv_heads=2, window=0, split_keys=512)
+    items, groups, n_small = ops.attn_plan([1, 4, 6], [700, 0, 130], n_kv_heads=2, window=0, split_keys=512)
     g = groups.numpy()
     it = items.numpy()
     # seq0: 1 group/kv head, keys [0, 701) -> 2 splits; seq1: [0,4) -> 1; seq2: tokens 0-3, 4-5
@@ -61,7 +61,7 @@ def test_attn_plan_host(lib):
     assert it[0].tolist()[:8] == [0, 0, 0, 1, 700, 0, 512, 0]
     assert it[1].tolist()[5:7] == [512, 701]
     # sliding window 128: keys of tokens 130..133 start at 3 (aligned block 0)
-    items_w, groups_w = ops.attn_plan([4], [130], n_kv_heads=1, window=128, split_keys=512)
+    items_w, groups_w, _ = ops.attn_plan([4], [130], n_kv_heads=1, window=128, split_keys=512)
     assert items_w.numpy()[0, 5] == 130 - 127 and items_w.numpy()[0, 6] == 134
 
 

@@ -94,7 +94,28 @@ def test_router_exact_ties_go_to_lower_id():
     ids, _ = ops.router_topk_softmax(x, w, b, 4)
     rids, _, _ = oroute.gptoss_route(x.float().cpu(), w.float().cpu(), b.float().cpu(), 4)
     assert np.array_equal(ids.cpu().numpy(), rids)
-    assert (ids.cpu().numpy() < 8).all()                     # every tie resolved to the lowest copy
+    # the winning row has 8 identical copies (r, r+8, ..., r+56): top-4 must be its 4 lowest ids
+    got = ids.cpu().numpy()
+    r = got[:, :1] % 8
+    assert (got == r + np.arange(4)[None, :] * 8).all()
+
+
+@pytest.mark.parametrize("T,E,H", [(56, 128, 2880), (12, 128, 2880), (1024, 128, 2880), (1025, 128, 2880),
+                                   (33, 256, 7168)])
+def test_fused_route_permute_bit_exact(T, E, H):
+    """The stage's fused path (one-workgroup top-k + permute for T*k <= 4096, split above)."""
+    from flyai_amd import ops
+    k = 4 if E == 128 else 8
+    x = _rms_input(T, H, 12)
+    w = (torch.randn(E, H, device=DEV, generator=_gen(13)) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(E, device=DEV, generator=_gen(14)) * 0.02).to(torch.bfloat16)
+    ids, wts, hist, off, perm, inv = ops.moe_route_permute(x, w, b, k)
+    rids, rw, _ = oroute.gptoss_route(x.float().cpu(), w.float().cpu(), b.float().cpu(), k)
+    rh, ro, rp, ri = oroute.permute(rids, E)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+    for got, ref in ((hist, rh), (off, ro), (perm, rp), (inv, ri)):
+        assert np.array_equal(got.cpu().numpy(), ref)
 
 
 @pytest.mark.parametrize("T,k,E,mode", [(1, 4, 128, "rand"), (56, 4, 128, "rand"), (2096, 4, 128, "rand"),
@@ -237,8 +258,8 @@ def test_attention_vs_oracle(window, q_lens, starts):
     sinks = torch.randn(Hq, device=DEV, generator=_gen(53)).to(torch.bfloat16).float()
     base = torch.tensor([b * slab for b in range(S)], dtype=torch.int64, device=DEV)
     capt = torch.tensor([cap] * S, dtype=torch.int32, device=DEV)
-    items, groups = ops.attn_plan(q_lens, starts, Hkv, window, 512)
-    out = ops.attn_ragged(q, kp, vp, base, capt, sinks, window, items, groups, Hkv)
+    items, groups, n_small = ops.attn_plan(q_lens, starts, Hkv, window, 512)
+    out = ops.attn_ragged(q, kp, vp, base, capt, sinks, window, items, groups, n_small, Hkv)
     ks = [kp[b * slab:(b + 1) * slab].float().cpu().view(Hkv, cap, D) for b in range(S)]
     vs = [vp[b * slab:(b + 1) * slab].float().cpu().view(Hkv, D, cap).transpose(1, 2) for b in range(S)]
     ref = oattn.ragged_attention(q.float().cpu(), ks, vs, q_lens, starts, sinks.cpu(), window)
@@ -266,8 +287,8 @@ def test_attention_ignores_unwritten_nan_slots():
     base = torch.tensor([0, slab], dtype=torch.int64, device=DEV)
     capt = torch.tensor([cap, cap], dtype=torch.int32, device=DEV)
     for window in (0, 128):
-        items, groups = ops.attn_plan(q_lens, starts, Hkv, window, 128)
-        out = ops.attn_ragged(q, kp, vp, base, capt, sinks, window, items, groups, Hkv)
+        items, groups, n_small = ops.attn_plan(q_lens, starts, Hkv, window, 128)
+        out = ops.attn_ragged(q, kp, vp, base, capt, sinks, window, items, groups, n_small, Hkv)
         assert torch.isfinite(out.float()).all()
 
 

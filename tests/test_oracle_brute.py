@@ -64,17 +64,23 @@ def _bf16_rand(rng, shape, std=1.0):
 
 
 def test_dot_fixed_matches_sequential_restatement():
+    """Lane l sums k = 512 j + 8 l + i (k < K) in order, then the xor butterfly; K = 600 leaves
+    lanes 11..63 without a second chunk."""
     rng = np.random.default_rng(1)
-    x = _bf16_rand(rng, (2, 192))
-    w = _bf16_rand(rng, (3, 192))
+    K = 600
+    x = _bf16_rand(rng, (2, K))
+    w = _bf16_rand(rng, (3, K))
     got = routing.dot_fixed(x, w)
     for t in range(2):
         for e in range(3):
             lanes = []
             for l in range(64):
                 acc = np.float32(0.0)
-                for j in range(3):
-                    acc = np.float32(acc + np.float32(x[t, l + 64 * j]) * np.float32(w[e, l + 64 * j]))
+                for j in range(2):
+                    for i in range(8):
+                        k = 512 * j + 8 * l + i
+                        if k < K:
+                            acc = np.float32(acc + np.float32(x[t, k]) * np.float32(w[e, k]))
                 lanes.append(acc)
             for off in (32, 16, 8, 4, 2, 1):
                 lanes = [np.float32(lanes[i] + lanes[i ^ off]) for i in range(64)]

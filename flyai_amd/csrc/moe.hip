@@ -64,8 +64,20 @@ __global__ __launch_bounds__(256) void mxfp4_repack_kernel(const uint8_t* __rest
 }
 
 // ---- expert kernels ---------------------------------------------------------------------------
-constexpr int kMT = 2;   // 16-row activation tiles per pass (32 rows)
-constexpr int kNTW = 2;  // 16-row weight tiles per wave
+// Workgroup = 4 waves = 4*NTW weight tiles (16 output rows each) of one expert, full K.  The
+// expert's activation rows are staged in LDS, kRowsPerPass at a time, with fully coalesced loads
+// (one pass serves every tile of the workgroup), so the only vector-memory loads in the K loop are
+// the weights: 1 KiB per tile per group of 128 K, streamed through a 3-deep register ring with
+// non-temporal loads.  Each group is dequantised in registers (gfx950 v_cvt_scalef32_pk_bf16_fp4,
+// E8M0 scale in the exponent field) and fed to v_mfma_f32_16x16x32_bf16 with the activation
+// fragment read from LDS (rows >= the pass's row count read as zero).  Larger groups take further
+// passes over the weights.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_nt(const uint8_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 __device__ __forceinline__ float swiglu_gptoss(float gate, float up) {
   // modeling_gpt_oss.py:82-88: gate clamped above at 7, up clamped to [-7, 7]
@@ -75,137 +87,139 @@ __device__ __forceinline__ float swiglu_gptoss(float gate, float up) {
   return (u + 1.0f) * glu;
 }
 
-template <bool GATE_UP>
+constexpr int kRowsPerPass = 8;
+
+__host__ __device__ inline int mx_lds_row_bytes(int K) { return K * 2 + 16; }  // +16 B vs bank conflicts
+
+template <bool GATE_UP, int NTW>
 __global__ __launch_bounds__(256) void moe_mxfp4_kernel(
     const uint16_t* __restrict__ act, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, int k_top, const uint8_t* __restrict__ packed,
     const float* __restrict__ bias, int E, int N, int K, void* __restrict__ out) {
+  extern __shared__ uint4 xs_lds[];  // [kRowsPerPass][K*2+16 bytes]
   const MxGeom gm = mx_geom(E, N, K);
-  constexpr int kTilesPerWG = 4 * kNTW;
+  constexpr int kTilesPerWG = 4 * NTW;
   const int wg_per_e = (gm.NT + kTilesPerWG - 1) / kTilesPerWG;
   const int e = blockIdx.x / wg_per_e;
   const int wgi = blockIdx.x % wg_per_e;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int nt0 = wgi * kTilesPerWG + wave * kNTW;
-  if (nt0 >= gm.NT) return;
   const int row_lo = offsets[e];
   const int n_e = offsets[e + 1] - row_lo;
-  if (n_e <= 0) return;
+  if (n_e <= 0) return;  // uniform over the workgroup
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nt0 = wgi * kTilesPerWG + wave * NTW;
+  const int ntw = max(0, min(NTW, gm.NT - nt0));  // waves past the last tile still join the barriers
   const int r = lane & 15, g = lane >> 4;
-  const int ntw = min(kNTW, gm.NT - nt0);
+  const int row_bytes = mx_lds_row_bytes(K);
+  const int row_vecs = K / 8;  // 16-byte vectors per activation row
 
   const uint8_t* data = packed + ((size_t)e * gm.NT + nt0) * gm.G * 256 + lane * 16;
   const uint32_t* scl = reinterpret_cast<const uint32_t*>(
                             packed + gm.data_bytes + ((size_t)e * gm.NT + nt0) * gm.KG4 * 256) + lane;
   const size_t tile_stride = (size_t)gm.G * 256;
   const size_t scale_stride = (size_t)gm.KG4 * 64;
+  const char* lds = reinterpret_cast<const char*>(xs_lds);
 
-  for (int m0 = 0; m0 < n_e; m0 += 16 * kMT) {
-    const int mt_count = min(kMT, (n_e - m0 + 15) / 16);
-    const uint16_t* arow[kMT];
-    bool aval[kMT];
-#pragma unroll
-    for (int m = 0; m < kMT; ++m) {
-      const int row = m0 + 16 * m + r;
-      aval[m] = row < n_e;
-      int src = 0;
-      if (aval[m]) src = GATE_UP ? perm[row_lo + row] / k_top : row_lo + row;
-      arow[m] = act + (size_t)src * K;
+  for (int m0 = 0; m0 < n_e; m0 += kRowsPerPass) {
+    const int rows = min(kRowsPerPass, n_e - m0);
+    __syncthreads();  // the previous pass is done with the LDS rows
+    for (int i = threadIdx.x; i < rows * row_vecs; i += 256) {
+      const int rr = i / row_vecs, v = i % row_vecs;
+      const int p = row_lo + m0 + rr;
+      const int src = GATE_UP ? perm[p] / k_top : p;
+      *reinterpret_cast<uint4*>(const_cast<char*>(lds) + rr * row_bytes + v * 16) =
+          reinterpret_cast<const uint4*>(act + (size_t)src * K)[v];
     }
-    f32x4_t acc[kMT][kNTW];
-#pragma unroll
-    for (int m = 0; m < kMT; ++m)
-#pragma unroll
-      for (int n = 0; n < kNTW; ++n) acc[m][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    if (ntw == 0) continue;
+    const bool aval = r < rows;
+    const char* arow = lds + r * row_bytes + 64 * g;
 
-    uint4 wq[kNTW], wq_next[kNTW];
-    uint32_t scw[kNTW];
-    {
-      const bool bv = g < gm.G;
+    auto load_w = [&](uint4 (&w)[NTW], int kg) {
+      const bool bvalid = kg < gm.KG && 4 * kg + g < gm.G;
 #pragma unroll
-      for (int n = 0; n < kNTW; ++n)
-        wq[n] = (bv && n < ntw) ? *reinterpret_cast<const uint4*>(data + n * tile_stride)
-                                : make_uint4(0, 0, 0, 0);
+      for (int n = 0; n < NTW; ++n)
+        w[n] = (bvalid && n < ntw) ? ld_nt(data + n * tile_stride + (size_t)kg * 1024) : make_uint4(0, 0, 0, 0);
+    };
+    auto load_sc = [&](uint32_t (&sc)[NTW], int kg4) {
+#pragma unroll
+      for (int n = 0; n < NTW; ++n) sc[n] = (kg4 < gm.KG4 && n < ntw) ? scl[n * scale_stride + kg4 * 64] : 0u;
+    };
+    f32x4_t acc[NTW];
+#pragma unroll
+    for (int n = 0; n < NTW; ++n) acc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    // byte b of sc[n] is the E8M0 scale of group 4*kg4 + b
+    auto compute = [&](const uint4 (&w)[NTW], const uint32_t (&sc)[NTW], int kg, int b) {
+      uint4 a[4];
+      const bool ok = aval && kg < gm.KG && 4 * kg + g < gm.G;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        a[j] = ok ? *reinterpret_cast<const uint4*>(arow + 256 * kg + 16 * j) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int n = 0; n < NTW; ++n) {
+        const float scale = e8m0_operand((sc[n] >> (8 * b)) & 0xffu);
+        const uint32_t wd[4] = {w[n].x, w[n].y, w[n].z, w[n].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          acc[n] = mfma16x16x32(as_bf16x8(a[j]), fp4x8_to_bf16x8(wd[j], scale), acc[n]);
+      }
+    };
+
+    // Static bodies of 4 groups: a 4-deep weight ring (3 groups in flight while one computes) and
+    // the next body's scale dword loaded one body ahead, so no wait ever drains the ring.
+    uint4 w0[NTW], w1[NTW], w2[NTW], w3[NTW];
+    uint32_t sc_cur[NTW], sc_nxt[NTW];
+    load_sc(sc_cur, 0);
+    load_w(w0, 0);
+    load_w(w1, 1);
+    load_w(w2, 2);
+    for (int kg4 = 0; kg4 < gm.KG4; ++kg4) {
+      const int kg = 4 * kg4;
+      load_sc(sc_nxt, kg4 + 1);
+      load_w(w3, kg + 3);
+      compute(w0, sc_cur, kg, 0);
+      load_w(w0, kg + 4);
+      compute(w1, sc_cur, kg + 1, 1);
+      load_w(w1, kg + 5);
+      compute(w2, sc_cur, kg + 2, 2);
+      load_w(w2, kg + 6);
+      compute(w3, sc_cur, kg + 3, 3);
+#pragma unroll
+      for (int n = 0; n < NTW; ++n) sc_cur[n] = sc_nxt[n];
     }
-    for (int kg = 0; kg < gm.KG; ++kg) {
-      const int blk = 4 * kg + g;
-      const bool bvalid = blk < gm.G;
-      // prefetch next group's weights
-      if (kg + 1 < gm.KG) {
-        const bool nv = (blk + 4) < gm.G;
+
+    // epilogue: lane holds D[act row 4g+v][feature r] of each tile
 #pragma unroll
-        for (int n = 0; n < kNTW; ++n)
-          wq_next[n] = (nv && n < ntw)
-                           ? *reinterpret_cast<const uint4*>(data + n * tile_stride + (size_t)(kg + 1) * 1024)
-                           : make_uint4(0, 0, 0, 0);
-      }
-      if ((kg & 3) == 0) {
-#pragma unroll
-        for (int n = 0; n < kNTW; ++n) scw[n] = (n < ntw) ? scl[n * scale_stride + (kg >> 2) * 64] : 0u;
-      }
-      uint4 a[kMT][4];
-#pragma unroll
-      for (int m = 0; m < kMT; ++m) {
-        if (aval[m] && bvalid) {
-          const uint4* ap = reinterpret_cast<const uint4*>(arow[m] + blk * 32);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) a[m][j] = ap[j];
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) a[m][j] = make_uint4(0, 0, 0, 0);
-        }
-      }
-      float sc[kNTW];
-#pragma unroll
-      for (int n = 0; n < kNTW; ++n) sc[n] = e8m0_operand((scw[n] >> (8 * (kg & 3))) & 0xffu);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-#pragma unroll
-        for (int n = 0; n < kNTW; ++n) {
-          const uint32_t word = j == 0 ? wq[n].x : j == 1 ? wq[n].y : j == 2 ? wq[n].z : wq[n].w;
-          const bf16x8_t bw = fp4x8_to_bf16x8(word, sc[n]);
-#pragma unroll
-          for (int m = 0; m < kMT; ++m)
-            if (m < mt_count) acc[m][n] = mfma16x16x32(as_bf16x8(a[m][j]), bw, acc[m][n]);
-        }
-      }
-#pragma unroll
-      for (int n = 0; n < kNTW; ++n) wq[n] = wq_next[n];
-    }
-    // epilogue: lane holds D[act row 4g+v][feature r] of each (m, n) tile
-#pragma unroll
-    for (int n = 0; n < kNTW; ++n) {
+    for (int n = 0; n < NTW; ++n) {
       const int feat = (nt0 + n) * 16 + r;
       const bool nval = n < ntw;
       const float bsum = nval ? bias[(size_t)e * N + feat] : 0.f;
 #pragma unroll
-      for (int m = 0; m < kMT; ++m) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = m0 + 16 * m + 4 * g + v;
-          const float val = acc[m][n][v] + bsum;
-          if (GATE_UP) {
-            const float partner = __shfl_xor(val, 1, 64);
-            if (nval && (r & 1) == 0 && row < n_e && m < mt_count) {
-              const float hval = swiglu_gptoss(val, partner);
-              reinterpret_cast<uint16_t*>(out)[(size_t)(row_lo + row) * (N / 2) + feat / 2] = f2bf(hval);
-            }
-          } else {
-            if (nval && row < n_e && m < mt_count)
-              reinterpret_cast<float*>(out)[(size_t)(row_lo + row) * N + feat] = val;
-          }
+      for (int v = 0; v < 4; ++v) {
+        const int orow = 4 * g + v;
+        const float val = acc[n][v] + bsum;
+        if (GATE_UP) {
+          const float partner = __shfl_xor(val, 1, 64);
+          if (nval && (r & 1) == 0 && orow < rows)
+            reinterpret_cast<uint16_t*>(out)[(size_t)(row_lo + m0 + orow) * (N / 2) + feat / 2] =
+                f2bf(swiglu_gptoss(val, partner));
+        } else {
+          if (nval && orow < rows)
+            reinterpret_cast<float*>(out)[(size_t)(row_lo + m0 + orow) * N + feat] = val;
         }
       }
     }
   }
 }
 
+constexpr int kNTW = 2;  // weight tiles per wave
+
 int launch_moe_gate_up(const uint16_t* x, const int32_t* perm, const int32_t* offsets, int k_top,
                        const uint8_t* w13, const float* b13, int E, int H, int I, uint16_t* h,
                        hipStream_t s) {
   const MxGeom gm = mx_geom(E, 2 * I, H);
   const int wg_per_e = ceil_div(gm.NT, 4 * kNTW);
-  hipLaunchKernelGGL(moe_mxfp4_kernel<true>, dim3(E * wg_per_e), dim3(256), 0, s, x, perm, offsets,
+  hipLaunchKernelGGL((moe_mxfp4_kernel<true, kNTW>), dim3(E * wg_per_e), dim3(256),
+                     kRowsPerPass * mx_lds_row_bytes(H), s, x, perm, offsets,
                      k_top, w13, b13, E, 2 * I, H, (void*)h);
   return check_launch("moe_gate_up_mxfp4");
 }
@@ -214,7 +228,8 @@ int launch_moe_down(const uint16_t* h, const int32_t* offsets, const uint8_t* w2
                     int E, int H, int I, float* y, hipStream_t s) {
   const MxGeom gm = mx_geom(E, H, I);
   const int wg_per_e = ceil_div(gm.NT, 4 * kNTW);
-  hipLaunchKernelGGL(moe_mxfp4_kernel<false>, dim3(E * wg_per_e), dim3(256), 0, s, h, nullptr,
+  hipLaunchKernelGGL((moe_mxfp4_kernel<false, kNTW>), dim3(E * wg_per_e), dim3(256),
+                     kRowsPerPass * mx_lds_row_bytes(I), s, h, nullptr,
                      offsets, 1, w2, b2, E, H, I, (void*)y);
   return check_launch("moe_down_mxfp4");
 }
@@ -245,8 +260,8 @@ extern "C" int flyai_moe_gate_up_mxfp4(const uint16_t* x, const int32_t* perm,
                                        const int32_t* offsets, int32_t k, const uint8_t* w13_packed,
                                        const float* b13, int32_t E, int32_t H, int32_t I,
                                        uint16_t* h, flyai_stream_t stream) {
-  FLYAI_REQUIRE(E > 0 && H > 0 && I > 0 && H % 32 == 0 && (2 * I) % 16 == 0 && k >= 1,
-                "gate_up: need H %% 32 == 0, 2I %% 16 == 0");
+  FLYAI_REQUIRE(E > 0 && H > 0 && I > 0 && H % 32 == 0 && (2 * I) % 16 == 0 && k >= 1 && H <= 4064,
+                "gate_up: need H %% 32 == 0, H <= 4064, 2I %% 16 == 0");
   FLYAI_REQUIRE(x && perm && offsets && w13_packed && b13 && h, "gate_up: null pointer");
   return launch_moe_gate_up(x, perm, offsets, k, w13_packed, b13, E, H, I, h, as_stream(stream));
 }
@@ -254,8 +269,8 @@ extern "C" int flyai_moe_gate_up_mxfp4(const uint16_t* x, const int32_t* perm,
 extern "C" int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets,
                                     const uint8_t* w2_packed, const float* b2, int32_t E, int32_t H,
                                     int32_t I, float* y_perm, flyai_stream_t stream) {
-  FLYAI_REQUIRE(E > 0 && H > 0 && I > 0 && I % 32 == 0 && H % 16 == 0,
-                "down: need I %% 32 == 0, H %% 16 == 0");
+  FLYAI_REQUIRE(E > 0 && H > 0 && I > 0 && I % 32 == 0 && H % 16 == 0 && I <= 4064,
+                "down: need I %% 32 == 0, I <= 4064, H %% 16 == 0");
   FLYAI_REQUIRE(h && offsets && w2_packed && b2 && y_perm, "down: null pointer");
   return launch_moe_down(h, offsets, w2_packed, b2, E, H, I, y_perm, as_stream(stream));
 }

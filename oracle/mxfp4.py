@@ -21,6 +21,8 @@ import numpy as np
 FP4_VALUES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
               -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0)
 LUT = np.array(FP4_VALUES, dtype=np.float32)
+# byte -> (value of low nibble, value of high nibble): element 2i then 2i+1
+PAIR_LUT = np.stack([LUT[np.arange(256) & 0x0F], LUT[np.arange(256) >> 4]], axis=-1)
 
 
 def e8m0_to_f32(s):
@@ -36,10 +38,8 @@ def dequant(blocks, scales):
     blocks = np.asarray(blocks, dtype=np.uint8)
     scales = np.asarray(scales, dtype=np.uint8)
     assert blocks.shape[:-1] == scales.shape and blocks.shape[-1] == 16
-    lo = LUT[blocks & 0x0F]
-    hi = LUT[blocks >> 4]
-    vals = np.stack([lo, hi], axis=-1).reshape(*blocks.shape[:-1], 32)   # low nibble first
-    vals = vals * e8m0_to_f32(scales)[..., None]
+    vals = PAIR_LUT[blocks].reshape(*blocks.shape[:-1], 32)   # low nibble first
+    vals *= e8m0_to_f32(scales)[..., None]
     return vals.reshape(*blocks.shape[:-2], blocks.shape[-2] * 32).astype(np.float32)
 
 

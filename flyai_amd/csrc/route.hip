@@ -170,6 +170,170 @@ int launch_router(const uint16_t* x, const uint16_t* w, const uint16_t* b, int T
 }
 
 // ------------------------------------------------------------------------------------------------
+// DeepSeek-V3 grouped sigmoid routing (vendor/kimi_k3_ref/modeling_kimi_linear.py:703-759) on fp32
+// logits, one wave per token; lane l owns experts 4l .. 4l+3 (E <= 256, a group spans E/n_group
+// experts = a power-of-two run of lanes).  scores = sigmoid_det(logit); choice = scores + bias;
+// group score = top1 + top2 of the group's choices; the topk_group best groups (ties -> lower group)
+// stay; the k best unmasked choices (ties -> lower id) are selected; ids ascending; weights =
+// score / (sum in ascending id order + 1e-20) * route_scale, all fp32.
+//
+// sigmoid_det is exp by Cody-Waite reduction (n = rint(z log2 e); r = (z - n LN2_HI) - n LN2_LO,
+// LN2_HI with 12 significant bits) and the degree-7 Taylor polynomial by Horner with separate
+// multiplies and adds, times 2^n; then 1 / (1 + e) correctly rounded.  FP contraction is off so
+// every operation rounds exactly as the oracle's numpy float32 sequence does.
+__device__ __forceinline__ float sigmoid_det(float x) {
+#pragma clang fp contract(off)
+  const float kLog2e = (float)1.4426950408889634;
+  const float kLn2Hi = 0.693145751953125f;
+  const float kLn2Lo = (float)(0.69314718055994530942 - 0.693145751953125);
+  const float z = fminf(fmaxf(-x, -87.0f), 88.0f);
+  const float n = rintf(z * kLog2e);
+  float r = z - n * kLn2Hi;
+  r = r - n * kLn2Lo;
+  float p = (float)(1.0 / 5040.0);
+  p = p * r; p = p + (float)(1.0 / 720.0);
+  p = p * r; p = p + (float)(1.0 / 120.0);
+  p = p * r; p = p + (float)(1.0 / 24.0);
+  p = p * r; p = p + (float)(1.0 / 6.0);
+  p = p * r; p = p + 0.5f;
+  p = p * r; p = p + 1.0f;
+  p = p * r; p = p + 1.0f;
+  const float e = ldexpf(p, (int)n);
+  return __fdiv_rn(1.0f, 1.0f + e);
+}
+
+// (value desc, id asc) "a before b"
+__device__ __forceinline__ bool route_better(float va, int ia, float vb, int ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+template <int K>
+__global__ __launch_bounds__(256) void grouped_topk_kernel(const float* __restrict__ logits,
+                                                           const float* __restrict__ e_bias, int T,
+                                                           int E, int n_group, int topk_group,
+                                                           float route_scale, int32_t* __restrict__ ids,
+                                                           float* __restrict__ wts) {
+#pragma clang fp contract(off)
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;  // uniform per wave
+  const int lane = threadIdx.x & 63;
+  const float kNegInf = -__builtin_inff();
+  float sc[4], ch[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * lane + j;
+    if (e < E) {
+      sc[j] = sigmoid_det(logits[(size_t)t * E + e]);
+      ch[j] = sc[j] + (e_bias ? e_bias[e] : 0.0f);
+    } else {
+      sc[j] = 0.0f;
+      ch[j] = kNegInf;
+    }
+  }
+  if (n_group > 1 && n_group > topk_group) {
+    // top-2 values of the lane's 4 choices, then merged across the group's lanes
+    float a1 = kNegInf, a2 = kNegInf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (ch[j] > a1) { a2 = a1; a1 = ch[j]; } else if (ch[j] > a2) { a2 = ch[j]; }
+    }
+    const int lpg = E / n_group / 4;  // lanes per group (power of two)
+    for (int o = 1; o < lpg; o <<= 1) {
+      const float b1 = __shfl_xor(a1, o, 64), b2 = __shfl_xor(a2, o, 64);
+      const float n1 = fmaxf(a1, b1);
+      const float n2 = fmaxf(fminf(a1, b1), fmaxf(a2, b2));
+      a1 = n1; a2 = n2;
+    }
+    const float gs = a1 + a2;
+    const int my_g = lane / lpg;
+    int rank = 0;
+    for (int gg = 0; gg < n_group; ++gg) {
+      const float o = __shfl(gs, gg * lpg, 64);
+      rank += route_better(o, gg, gs, my_g) ? 1 : 0;
+    }
+    if (rank >= topk_group || 4 * lane >= E) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) ch[j] = kNegInf;
+    }
+  }
+  // k rounds of a wave-wide argmax over (value desc, id asc)
+  int sel[K];
+  bool taken[4] = {false, false, false, false};
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    float bv = kNegInf;
+    int bi = 1 << 30;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * lane + j;
+      if (!taken[j] && e < E && route_better(ch[j], e, bv, bi)) { bv = ch[j]; bi = e; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (route_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+    }
+    sel[i] = bi;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * lane + j == bi) taken[j] = true;
+  }
+  // ids ascending (static odd-even transposition sort), then their unbiased scores
+#pragma unroll
+  for (int pass = 0; pass < K; ++pass)
+#pragma unroll
+    for (int i = pass & 1; i + 1 < K; i += 2)
+      if (sel[i] > sel[i + 1]) { const int tmp = sel[i]; sel[i] = sel[i + 1]; sel[i + 1] = tmp; }
+  float sv[K];
+  float den = 0.0f;
+#pragma unroll
+  for (int i = 0; i < K; ++i) {
+    const int j = sel[i] & 3;
+    const float mine = j == 0 ? sc[0] : j == 1 ? sc[1] : j == 2 ? sc[2] : sc[3];
+    sv[i] = __shfl(mine, sel[i] >> 2, 64);
+    den = den + sv[i];
+  }
+  den = den + (float)1e-20;  // np.float32(1e-20): the double literal rounded once
+  if (lane < K) {
+    float v = 0.0f;
+    int id = 0;
+#pragma unroll
+    for (int i = 0; i < K; ++i)
+      if (i == lane) { v = sv[i]; id = sel[i]; }
+    ids[(size_t)t * K + lane] = id;
+    wts[(size_t)t * K + lane] = __fdiv_rn(v, den) * route_scale;
+  }
+}
+
+int launch_router_grouped(const uint16_t* x, const uint16_t* w, const float* e_bias, int T, int H, int E,
+                          int n_group, int topk_group, int k, float route_scale, float* logits,
+                          int32_t* ids, float* wts, hipStream_t s) {
+  if (T == 0) return FLYAI_OK;
+  if (H <= 3072)
+    hipLaunchKernelGGL((router_logits_kernel<8, 2, 6, false>), dim3(ceil_div(T, 8), ceil_div(E, 8)),
+                       dim3(256), 8 * H * sizeof(uint16_t), s, x, w, nullptr, T, H, E, logits);
+  else
+    hipLaunchKernelGGL((router_logits_kernel<4, 1, 14, false>), dim3(ceil_div(T, 4), ceil_div(E, 4)),
+                       dim3(256), 4 * H * sizeof(uint16_t), s, x, w, nullptr, T, H, E, logits);
+  int rc = check_launch("router_logits(fp32)");
+  if (rc) return rc;
+  const dim3 grid(ceil_div(T, 4));
+  if (k == 8)
+    hipLaunchKernelGGL(grouped_topk_kernel<8>, grid, dim3(256), 0, s, logits, e_bias, T, E, n_group,
+                       topk_group, route_scale, ids, wts);
+  else if (k == 4)
+    hipLaunchKernelGGL(grouped_topk_kernel<4>, grid, dim3(256), 0, s, logits, e_bias, T, E, n_group,
+                       topk_group, route_scale, ids, wts);
+  else if (k == 6)
+    hipLaunchKernelGGL(grouped_topk_kernel<6>, grid, dim3(256), 0, s, logits, e_bias, T, E, n_group,
+                       topk_group, route_scale, ids, wts);
+  else
+    return set_error(FLYAI_EINVAL, "grouped router: top_k must be 4, 6 or 8");
+  return check_launch("grouped_topk");
+}
+
+// ------------------------------------------------------------------------------------------------
 // Histogram + exclusive scan + stable permute in one 16-wave workgroup.  Each wave owns a
 // contiguous segment of the flattened assignments; within a 64-assignment chunk, lanes with the
 // same expert find each other with 8 ballots (one per id bit), rank = popcount of lower peers, and
@@ -420,4 +584,25 @@ extern "C" int flyai_moe_route_permute(const uint16_t* x, const uint16_t* w, con
                 "route_permute: null pointer");
   return launch_route_permute(x, w, b, T, H, E, k, topk_ids, topk_w, logits, hist, offsets, perm, inv,
                               as_stream(stream));
+}
+
+extern "C" int flyai_router_grouped_sigmoid(const uint16_t* x, const uint16_t* w, const float* e_bias,
+                                            int32_t T, int32_t H, int32_t E, int32_t n_group,
+                                            int32_t topk_group, int32_t k, float route_scale,
+                                            float* logits, int32_t* topk_ids, float* topk_w,
+                                            flyai_stream_t stream) {
+  FLYAI_REQUIRE(T >= 0 && H > 0 && H <= 7168 && H % 8 == 0, "grouped router: H must be a multiple of 8 <= 7168");
+  FLYAI_REQUIRE(E >= 4 && E <= 256 && E % 4 == 0 && (k == 4 || k == 6 || k == 8) && k <= E,
+                "grouped router: need E %% 4 == 0, 4 <= E <= 256, k in {4, 6, 8}");
+  FLYAI_REQUIRE(n_group >= 1 && E % n_group == 0 && topk_group >= 1 && topk_group <= n_group,
+                "grouped router: need n_group | E and 1 <= topk_group <= n_group");
+  const int lpg = E / n_group / 4;
+  FLYAI_REQUIRE(n_group == 1 || n_group <= topk_group ||
+                    ((E / n_group) % 4 == 0 && lpg >= 1 && (lpg & (lpg - 1)) == 0),
+                "grouped router: a group must be 4 * 2^j experts");
+  FLYAI_REQUIRE(n_group == 1 || n_group <= topk_group || topk_group * (E / n_group) >= k,
+                "grouped router: kept groups hold fewer than k experts");
+  FLYAI_REQUIRE(x && w && logits && topk_ids && topk_w, "grouped router: null pointer");
+  return launch_router_grouped(x, w, e_bias, T, H, E, n_group, topk_group, k, route_scale, logits,
+                               topk_ids, topk_w, as_stream(stream));
 }

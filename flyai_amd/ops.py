@@ -237,3 +237,104 @@ def attn_ragged(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, items, groups
                                   n_small, _ptr(groups_d), groups.shape[0], _ptr(parts), _ptr(out),
                                   _stream()))
     return out
+
+
+# ---- DeepSeek-V3-shaped FP8 MoE ------------------------------------------------------------------
+
+def router_grouped_sigmoid(x, w, e_bias, n_group, topk_group, k, route_scale):
+    """Grouped sigmoid routing on fp32 logits -> (ids int32 [T,k] ascending, weights fp32 [T,k],
+    logits fp32 [T,E])."""
+    T, H = x.shape
+    E = w.shape[0]
+    _need(x, torch.bfloat16, (T, H), "x")
+    _need(w, torch.bfloat16, (E, H), "router weight")
+    if e_bias is not None:
+        _need(e_bias, torch.float32, (E,), "e_bias")
+    dev = x.device
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    ids = torch.empty(T, k, dtype=torch.int32, device=dev)
+    wts = torch.empty(T, k, dtype=torch.float32, device=dev)
+    check(lib().flyai_router_grouped_sigmoid(_ptr(x), _ptr(w), _ptr(e_bias), T, H, E, n_group, topk_group,
+                                             k, float(route_scale), _ptr(logits), _ptr(ids), _ptr(wts),
+                                             _stream()))
+    return ids, wts, logits
+
+
+def fp8_act_quant(x):
+    """bf16 [M, K] -> (e4m3 bytes u8 [M, K], E8M0 scale bytes u8 [M, K/128])."""
+    M, K = x.shape
+    _need(x, torch.bfloat16, (M, K), "x")
+    q = torch.empty(M, K, dtype=torch.uint8, device=x.device)
+    s = torch.empty(M, K // 128, dtype=torch.uint8, device=x.device)
+    check(lib().flyai_fp8_act_quant(_ptr(x), M, K, _ptr(q), _ptr(s), _stream()))
+    return q, s
+
+
+def fp8_packed_bytes(E, N, K):
+    return int(lib().flyai_fp8_packed_bytes(E, N, K))
+
+
+def fp8_repack(w1, s1, w3=None, s3=None):
+    """e4m3 bytes w [E, N, K] + E8M0 block scales [E, ceil(N/128), K/128] -> packed u8 buffer.
+    With w3/s3 (gate_up), rows of w1 and w3 are interleaved and the packed N is 2N."""
+    E, N, K = w1.shape
+    sb = (E, (N + 127) // 128, K // 128)
+    _need(w1, torch.uint8, (E, N, K), "w1")
+    _need(s1, torch.uint8, sb, "s1")
+    if w3 is not None:
+        _need(w3, torch.uint8, (E, N, K), "w3")
+        _need(s3, torch.uint8, sb, "s3")
+    Np = 2 * N if w3 is not None else N
+    packed = torch.empty(fp8_packed_bytes(E, Np, K), dtype=torch.uint8, device=w1.device)
+    check(lib().flyai_fp8_repack(_ptr(w1), _ptr(s1), _ptr(w3), _ptr(s3), E, N, K, _ptr(packed), _stream()))
+    return packed
+
+
+def moe_gate_up_fp8(xq, xs, perm, offsets, k, topk_w, w13_packed, n_experts, inter):
+    """Rows of expert e: token perm[p] // k (perm None: token p); h = bf16(silu(bf16 gate) * bf16 up
+    * topk_w[perm[p]]) (topk_w None: 1) -> h bf16 [P, inter], P = offsets[-1] rows."""
+    T, H = xq.shape
+    _need(xq, torch.uint8, (T, H), "xq")
+    _need(xs, torch.uint8, (T, H // 128), "xs")
+    _need(offsets, torch.int32, (n_experts + 1,), "offsets")
+    P = T * k if perm is not None else T
+    if perm is not None:
+        _need(perm, torch.int32, (P,), "perm")
+    if topk_w is not None:
+        _need(topk_w, torch.float32, None, "topk_w")
+        if topk_w.numel() != P:
+            raise ValueError("topk_w must hold one weight per routed row")
+    _need(w13_packed, torch.uint8, (fp8_packed_bytes(n_experts, 2 * inter, H),), "w13_packed")
+    h = torch.empty(P, inter, dtype=torch.bfloat16, device=xq.device)
+    check(lib().flyai_moe_gate_up_fp8(_ptr(xq), _ptr(xs), _ptr(perm), _ptr(offsets), k, _ptr(topk_w),
+                                      _ptr(w13_packed), n_experts, H, inter, _ptr(h), _stream()))
+    return h
+
+
+def moe_down_fp8(hq, hs, offsets, w2_packed, n_experts, hidden):
+    P, inter = hq.shape
+    _need(hq, torch.uint8, (P, inter), "hq")
+    _need(hs, torch.uint8, (P, inter // 128), "hs")
+    _need(offsets, torch.int32, (n_experts + 1,), "offsets")
+    _need(w2_packed, torch.uint8, (fp8_packed_bytes(n_experts, hidden, inter),), "w2_packed")
+    y = torch.empty(P, hidden, dtype=torch.bfloat16, device=hq.device)
+    check(lib().flyai_moe_down_fp8(_ptr(hq), _ptr(hs), _ptr(offsets), _ptr(w2_packed), n_experts, hidden,
+                                   inter, _ptr(y), _stream()))
+    return y
+
+
+def moe_combine_sum(y_perm, inv, k, shared=None, residual=None, out=None):
+    """out[t] = bf16(sum_s y_perm[inv[t*k+s]] + shared[t]) (fp32), then bf16(residual + out)."""
+    P, H = y_perm.shape
+    T = P // k
+    _need(y_perm, torch.bfloat16, (P, H), "y_perm")
+    _need(inv, torch.int32, (P,), "inv")
+    for n, t in (("shared", shared), ("residual", residual)):
+        if t is not None:
+            _need(t, torch.bfloat16, (T, H), n)
+    if out is None:
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=y_perm.device)
+    _need(out, torch.bfloat16, (T, H), "out")
+    check(lib().flyai_moe_combine_sum(_ptr(y_perm), _ptr(inv), T, k, H, _ptr(shared), _ptr(residual),
+                                      _ptr(out), _stream()))
+    return out

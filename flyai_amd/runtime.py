@@ -16,7 +16,7 @@ import ctypes as C
 import numpy as np
 import torch
 
-from . import _lib
+from . import _lib, ops
 from ._lib import ContextOverflow, check, lib
 from .weights import GptOssShape
 
@@ -239,3 +239,37 @@ class BatchedFastVerifyStage:
         self.stage.forward(flat, [kp1] * B, st, list(range(B)))
         self.out = flat.view(B, kp1, H)
         return self.out
+
+
+class Fp8MoeStage:
+    """A stage of DeepSeek-V3-shaped FP8 MoE layers over a flat ragged token batch: per layer
+    h += MoE(RMSNorm(h)) with grouped sigmoid routing, FP8 routed experts and the shared expert
+    (vendor/deepseek_v4_ref/inference/model.py:634-650 MoE, :592-611 Expert).  Every op is a
+    libflyai_stage launch on the current stream."""
+
+    def __init__(self, shape, layers):
+        self.shape, self.layers = shape, layers
+
+    def moe(self, lw, x, residual):
+        sh = self.shape
+        T = x.shape[0]
+        E, k, H, I = sh.n_experts, sh.top_k, sh.hidden, sh.intermediate
+        xn = ops.rmsnorm(x, lw.ln, sh.rms_eps)
+        ids, wts, _ = ops.router_grouped_sigmoid(xn, lw.router_w, lw.e_bias, sh.n_group, sh.topk_group, k,
+                                                 sh.route_scale)
+        _, off, perm, inv = ops.moe_permute(ids, E)
+        xq, xs = ops.fp8_act_quant(xn)
+        h = ops.moe_gate_up_fp8(xq, xs, perm, off, k, wts, lw.w13_packed, E, I)
+        hq, hs = ops.fp8_act_quant(h)
+        y = ops.moe_down_fp8(hq, hs, off, lw.w2_packed, E, H)
+        off1 = torch.tensor([0, T], dtype=torch.int32, device=x.device)
+        hsh = ops.moe_gate_up_fp8(xq, xs, None, off1, 1, None, lw.sh13_packed, 1, I)
+        hshq, hshs = ops.fp8_act_quant(hsh)
+        ysh = ops.moe_down_fp8(hshq, hshs, off1, lw.sh2_packed, 1, H)
+        return ops.moe_combine_sum(y, inv, k, shared=ysh, residual=residual, out=residual)
+
+    def forward(self, hidden):
+        """hidden bf16 [T, H], updated in place through every layer."""
+        for lw in self.layers:
+            self.moe(lw, hidden, hidden)
+        return hidden

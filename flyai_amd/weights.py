@@ -79,3 +79,80 @@ def synthetic_layer(shape: GptOssShape, seed, device="cuda", sliding=False, keep
         **synthetic_moe(shape, gen, device),
     )
     return lw.repack(keep_hf=keep_hf)
+
+
+# ---- DeepSeek-V3-shaped FP8 MoE stage ------------------------------------------------------------
+
+@dataclass
+class DsV3Shape:
+    hidden: int = 7168
+    intermediate: int = 2048
+    n_experts: int = 256
+    top_k: int = 8
+    n_group: int = 8
+    topk_group: int = 4
+    route_scale: float = 2.5
+    rms_eps: float = 1e-6
+    zipf_s: float = 1.1
+
+
+def fp8_block_quant(w):
+    """fp32 [..., N, K] -> (e4m3 bytes u8 [..., N, K], E8M0 scale bytes u8 [..., N/128, K/128]):
+    one power-of-two scale 2^ceil(log2(amax/448)) per 128x128 block, the weight layout of
+    engines/deepseek_v4/v4_moe_grouped.py:769-783 (``_fp8_block_quant``)."""
+    *lead, N, K = w.shape
+    b = w.float().reshape(*lead, N // 128, 128, K // 128, 128)
+    amax = b.abs().amax(dim=(-3, -1)).clamp_min(1e-4)
+    e = torch.ceil(torch.log2(amax / 448.0))
+    q = (b / torch.exp2(e)[..., :, None, :, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q.reshape(*lead, N, K).view(torch.uint8), (e + 127).to(torch.uint8)
+
+
+def synthetic_fp8_experts(n_experts, hidden, inter, gen, device, std=0.02, chunk=16):
+    """Random N(0, std) expert weights quantised per 128x128 block: dict of w1/w3 [E, I, H],
+    w2 [E, H, I] e4m3 bytes and s1/s3 [E, I/128, H/128], s2 [E, H/128, I/128] E8M0 bytes."""
+    out = {n: [] for n in ("w1", "s1", "w3", "s3", "w2", "s2")}
+    for e0 in range(0, n_experts, chunk):
+        n = min(chunk, n_experts - e0)
+        for wn, sn, shp in (("w1", "s1", (n, inter, hidden)), ("w3", "s3", (n, inter, hidden)),
+                            ("w2", "s2", (n, hidden, inter))):
+            q, s = fp8_block_quant(torch.randn(*shp, device=device, generator=gen) * std)
+            out[wn].append(q)
+            out[sn].append(s)
+    return {k: torch.cat(v) for k, v in out.items()}
+
+
+class Fp8MoeLayerWeights:
+    """Device tensors of one FP8 MoE layer: ln (fp32), router_w (bf16 [E, H]), e_bias (fp32 [E]),
+    w13_packed / w2_packed (routed experts) and sh13_packed / sh2_packed (the shared expert).
+    ``raw`` / ``shared_raw`` keep the unpacked e4m3 + E8M0 tensors when asked (for the oracle)."""
+
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def zipf_bias(n_experts, s, gen, device, amplitude=0.25):
+    """Selection-only bias (e_score_correction_bias) making expert popularity fall off like a Zipf
+    law of exponent s over a random expert order: bias_e = -amplitude * s * ln(rank_e)."""
+    rank = torch.randperm(n_experts, generator=gen, device=device).float() + 1.0
+    return (-amplitude * s * torch.log(rank)).float()
+
+
+def synthetic_fp8_moe_layer(shape: DsV3Shape, seed, device="cuda", keep_raw=False):
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    H, I, E = shape.hidden, shape.intermediate, shape.n_experts
+    routed = synthetic_fp8_experts(E, H, I, gen, device)
+    shared = synthetic_fp8_experts(1, H, I, gen, device)
+    lw = Fp8MoeLayerWeights(
+        ln=(1.0 + 0.05 * torch.randn(H, device=device, generator=gen)).float(),
+        router_w=(torch.randn(E, H, device=device, generator=gen) * 0.02).to(torch.bfloat16),
+        e_bias=zipf_bias(E, shape.zipf_s, gen, device),
+        w13_packed=ops.fp8_repack(routed["w1"], routed["s1"], routed["w3"], routed["s3"]),
+        w2_packed=ops.fp8_repack(routed["w2"], routed["s2"]),
+        sh13_packed=ops.fp8_repack(shared["w1"], shared["s1"], shared["w3"], shared["s3"]),
+        sh2_packed=ops.fp8_repack(shared["w2"], shared["s2"]),
+    )
+    if keep_raw:
+        lw.raw, lw.shared_raw = routed, shared
+    return lw

@@ -121,6 +121,52 @@ int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, const uint8_
                          const float* b2, int32_t E, int32_t H, int32_t I, float* y_perm,
                          flyai_stream_t stream);
 
+/* ---- a2 (DeepSeek-V3 shape): grouped sigmoid router ---------------------------------------------
+ * Replaces KimiMoEGate.forward (vendor/kimi_k3_ref/modeling_kimi_linear.py:703-759) / the V4 Gate
+ * (vendor/deepseek_v4_ref/inference/model.py:560-589) for score_func sigmoid with group limits.
+ * logits (fp32 [T,E], written) = the fixed-order fp32 dot of x and w (no bias); scores =
+ * sigmoid(logits); choice = scores + e_bias (e_bias fp32 [E], may be NULL); the topk_group groups
+ * with the largest top-2 sums stay (ties -> lower group); the k largest choices among them are
+ * selected (ties -> lower id); topk_ids ascending; topk_w = score / (sum + 1e-20) * route_scale.
+ * Indices are bit-exact against the oracle (deterministic sigmoid, fixed summation orders).
+ * E % 4 == 0, E <= 256, E / n_group = 4 * 2^j, k in {4, 6, 8}, H % 8 == 0, H <= 7168. */
+int flyai_router_grouped_sigmoid(const uint16_t* x, const uint16_t* w, const float* e_bias,
+                                 int32_t T, int32_t H, int32_t E, int32_t n_group,
+                                 int32_t topk_group, int32_t k, float route_scale, float* logits,
+                                 int32_t* topk_ids, float* topk_w, flyai_stream_t stream);
+
+/* ---- a7: FP8 e4m3 128x128 block-scaled experts (DeepSeek-V3 shape) ------------------------------
+ * act_quant replaces act_quant (vendor/deepseek_v4_ref/inference/kernel.py:42-80 with power-of-two
+ * scales; engines/deepseek_v4/v4_kernels_cpu.py:89-104): per row per 128-K block,
+ * s = 2^ceil(log2(max(amax, 1e-4) / 448)) stored as its E8M0 byte (s_e8m0 u8 [M, K/128]) and
+ * q = e4m3 RNE of clamp(x / s, -448, 448) (q u8 [M, K]).
+ * Weights: e4m3 bytes w [E][N][K] with E8M0 block scales [E][ceil(N/128)][K/128]
+ * (model.py:143-149).  flyai_fp8_repack converts them once into the kernels' tile layout; with
+ * w3/s3 given (gate_up), the packed N is 2N with w1/w3 rows interleaved.  K % 1024 == 0, K <= 8192.
+ * gate_up replaces Expert.forward up to w2 (model.py:601-610) for every routed row of every expert:
+ *   row p of expert e takes token perm[p] / k (perm NULL: token p); gate = bf16(x . W1[e]),
+ *   up = bf16(x . W3[e]) (fp8_gemm semantics, kernel.py:241-254); h[p] = bf16(silu(gate) * up *
+ *   topk_w[perm[p]]) (topk_w NULL: weight 1) -- h bf16 [P, I].
+ * down: y[p] = bf16(hq[p] . W2[e]) with hq/hs = act_quant(h) -- y bf16 [P, H].
+ * combine_sum replaces MoE.forward's accumulation (model.py:640-650): out[t] = bf16(sum over slots
+ * in order of y[inv[t*k+s]] + shared[t]) in fp32, then out = bf16(residual + out) when residual is
+ * given (shared and residual may be NULL; residual may equal out). */
+int flyai_fp8_act_quant(const uint16_t* x, int32_t M, int32_t K, uint8_t* q, uint8_t* s_e8m0,
+                        flyai_stream_t stream);
+size_t flyai_fp8_packed_bytes(int32_t E, int32_t N, int32_t K);
+int flyai_fp8_repack(const uint8_t* w1, const uint8_t* s1, const uint8_t* w3, const uint8_t* s3,
+                     int32_t E, int32_t N, int32_t K, uint8_t* packed, flyai_stream_t stream);
+int flyai_moe_gate_up_fp8(const uint8_t* xq, const uint8_t* xs, const int32_t* perm,
+                          const int32_t* offsets, int32_t k, const float* topk_w,
+                          const uint8_t* w13_packed, int32_t E, int32_t H, int32_t I, uint16_t* h,
+                          flyai_stream_t stream);
+int flyai_moe_down_fp8(const uint8_t* hq, const uint8_t* hs, const int32_t* offsets,
+                       const uint8_t* w2_packed, int32_t E, int32_t H, int32_t I, uint16_t* y,
+                       flyai_stream_t stream);
+int flyai_moe_combine_sum(const uint16_t* y_perm, const int32_t* inv, int32_t T, int32_t k,
+                          int32_t H, const uint16_t* shared, const uint16_t* residual,
+                          uint16_t* out, flyai_stream_t stream);
+
 /* ---- a9: layer glue ------------------------------------------------------------------------------
  * RMSNorm: GptOssRMSNorm.forward (modeling_gpt_oss.py:57-62): y = bf16(w * (x * rsqrt(mean(x^2)+eps)))
  * with fp32 weight.  Linear: q/k/v/o projections (modeling_gpt_oss.py:280-291): y = bf16(x W^T + b),

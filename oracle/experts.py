@@ -161,3 +161,32 @@ def fp8_block_quant_weight(w):
     scale = np.exp2(np.ceil(np.log2(amax / np.float32(448.0)))).astype(np.float32)
     q = np.clip(b / scale[:, None, :, None], -448.0, 448.0)
     return e4m3_round(q).reshape(out, inn), scale
+
+
+class Fp8ExpertWeights:
+    """FP8 expert weights as numpy fp32 arrays holding e4m3 values, with fp32 power-of-two scales:
+    w1, w3 [E, I, H], s1, s3 [E, I/128, H/128]; w2 [E, H, I], s2 [E, H/128, I/128]
+    (``vendor/deepseek_v4_ref/inference/model.py:143-149`` layout, scale per 128x128 block)."""
+
+    def __init__(self, w1, s1, w3, s3, w2, s2):
+        self.w1, self.s1, self.w3, self.s3, self.w2, self.s2 = w1, s1, w3, s3, w2, s2
+
+    def expert(self, e, x_bf16, weight=None):
+        return deepseek_expert(x_bf16, self.w1[e], self.s1[e], self.w3[e], self.s3[e],
+                               self.w2[e], self.s2[e], weight)
+
+
+def deepseek_moe(x_bf16, ids, wts, experts: Fp8ExpertWeights, shared: Fp8ExpertWeights):
+    """MoE.forward (model.py:634-650): fp32 y; for each expert in ascending id, y[tokens] += its
+    bf16 output (routing weight applied before w2); y += shared expert (expert 0 of ``shared``);
+    returned as bf16 values.  x_bf16 fp32 [T, H] holding bf16 values; ids/wts [T, k]."""
+    x = np.asarray(x_bf16, dtype=np.float32)
+    ids = np.asarray(ids)
+    wts = np.asarray(wts, dtype=np.float32)
+    y = torch.zeros(x.shape, dtype=torch.float32)
+    for e in np.unique(ids):
+        tok, slot = np.nonzero(ids == e)                 # token order, like torch.where
+        ye = experts.expert(int(e), x[tok], wts[tok, slot])
+        y[torch.from_numpy(tok)] += ye
+    y += shared.expert(0, x)
+    return bf16(y)

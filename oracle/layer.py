@@ -162,3 +162,17 @@ def stage_step(h, layers, kv_per_layer, q_lens, starts, cos_tab, sin_tab, traces
         if traces is not None:
             traces.append(tr)
     return h
+
+
+def deepseek_moe_layer(h, ln_w, eps, router_w, e_bias, n_group, topk_group, k, route_scale,
+                       moe: "experts.Fp8ExpertWeights", shared: "experts.Fp8ExpertWeights"):
+    """One FP8 MoE layer of the DeepSeek-V3-shaped stage: h + MoE(RMSNorm(h)) in bf16 (the FFN half
+    of a pre-norm block; ``vendor/deepseek_v4_ref/inference/model.py:634-650`` MoE with the
+    grouped sigmoid gate of ``vendor/kimi_k3_ref/modeling_kimi_linear.py:703-759``).
+    Returns (new h, ids, weights)."""
+    hf = torch.as_tensor(h).float()
+    xn = rmsnorm(hf, ln_w, eps)
+    ids, wts, _ = routing.grouped_sigmoid_route(xn.numpy(), router_w, e_bias, n_group, topk_group, k,
+                                                route_scale)
+    y = experts.deepseek_moe(xn.numpy(), ids, wts, moe, shared)
+    return bf16(hf + y), ids, wts

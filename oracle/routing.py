@@ -139,8 +139,14 @@ def grouped_sigmoid_route(x, w, e_bias, n_group, topk_group, k, scale):
     sel = _topk_desc(masked, k)
     order = np.argsort(sel, axis=1, kind="stable")
     ids = np.take_along_axis(sel, order, axis=1).astype(np.int32)
-    wsel = np.take_along_axis(scores, ids, axis=1).astype(np.float64)
-    wts = (wsel / (wsel.sum(axis=1, keepdims=True) + 1e-20) * scale).astype(np.float32)
+    wsel = np.take_along_axis(scores, ids, axis=1).astype(np.float32)
+    # fp32 like the reference (modeling_kimi_linear.py:752-756): sum in ascending id order,
+    # (+1e-20), one division, then the scaling factor
+    den = np.zeros(T, dtype=np.float32)
+    for j in range(k):
+        den = (den + wsel[:, j]).astype(np.float32)
+    den = (den + np.float32(1e-20)).astype(np.float32)
+    wts = ((wsel / den[:, None]).astype(np.float32) * np.float32(scale)).astype(np.float32)
     return ids, wts, scores
 
 

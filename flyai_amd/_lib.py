@@ -59,8 +59,8 @@ _PROTOS = {
     "flyai_fp8_act_quant": (C.c_int, [P, I32, I32, P, P, P]),
     "flyai_fp8_packed_bytes": (SZ, [I32, I32, I32]),
     "flyai_fp8_repack": (C.c_int, [P, P, P, P, I32, I32, I32, P, P]),
-    "flyai_moe_gate_up_fp8": (C.c_int, [P, P, P, P, I32, P, P, I32, I32, I32, P, P]),
-    "flyai_moe_down_fp8": (C.c_int, [P, P, P, P, I32, I32, I32, P, P]),
+    "flyai_moe_gate_up_fp8": (C.c_int, [P, P, P, P, I32, P, P, I32, I32, I32, I32, P, P]),
+    "flyai_moe_down_fp8": (C.c_int, [P, P, P, P, I32, I32, I32, I32, P, P]),
     "flyai_moe_combine_sum": (C.c_int, [P, P, I32, I32, I32, P, P, P, P]),
     "flyai_mxfp4_packed_bytes": (SZ, [I32, I32, I32]),
     "flyai_mxfp4_repack": (C.c_int, [P, P, I32, I32, I32, P, P]),

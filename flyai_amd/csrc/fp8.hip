@@ -129,8 +129,11 @@ __global__ __launch_bounds__(256) void fp8_repack_kernel(const uint8_t* __restri
 // GATE_UP: rows are tokens (act row = perm[p] / k, or p when perm is null); the epilogue rounds gate
 // and up to bf16 (w1(x), w3(x) are bf16 Linear outputs), h = silu(gate) * up * routing weight,
 // written as bf16 [P][N/2].  DOWN: rows are the permuted h rows; y = bf16 [P][N].
+// With n_shared > 0, expert E (packed after the E routed ones) is the shared expert: its rows
+// P .. P+n_shared-1 (P = offsets[E]) take tokens 0 .. n_shared-1 with weight 1, so one launch
+// covers routed and shared experts.
 // Experts with fewer than min_rows or more than max_rows rows are left to another launch.
-__host__ __device__ constexpr int fp8_chunk(int MT) { return MT == 1 ? 1024 : 512; }
+__host__ __device__ constexpr int fp8_chunk(int MT) { return MT == 1 ? 1024 : 256; }
 
 __host__ __device__ inline int fp8_lds_bytes(int MT, int K) {
   return MT * 16 * (fp8_chunk(MT) + 16 + K / 128);
@@ -147,21 +150,22 @@ template <bool GATE_UP, int MT, int NTW>
 __global__ __launch_bounds__(256) void moe_fp8_kernel(
     const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, int k_top, const float* __restrict__ row_w,
-    const uint8_t* __restrict__ packed, int E, int N, int K, int min_rows, int max_rows,
-    uint16_t* __restrict__ out) {
+    const uint8_t* __restrict__ packed, int E, int n_shared, int N, int K, int min_rows,
+    int max_rows, uint16_t* __restrict__ out) {
   extern __shared__ uint4 f8_lds[];
   constexpr int KC = fp8_chunk(MT);          // K bytes per LDS chunk
   constexpr int SPC = KC / 128;              // MFMA steps per chunk
   constexpr int ROWB = KC + 16;              // padded LDS row
   constexpr int VPR = KC / 16;               // 16-byte vectors per row chunk
   constexpr int SREG = MT * 16 * VPR / 256;  // staging vectors per thread
-  const Fp8Geom gm = fp8_geom(E, N, K);
+  const Fp8Geom gm = fp8_geom(E + (n_shared > 0), N, K);
   constexpr int kTilesPerWG = 4 * NTW;
   const int wg_per_e = (gm.NT + kTilesPerWG - 1) / kTilesPerWG;
   const int e = blockIdx.x / wg_per_e;
   const int wgi = blockIdx.x % wg_per_e;
+  const bool shared = e == E;
   const int row_lo = offsets[e];
-  const int n_e = offsets[e + 1] - row_lo;
+  const int n_e = shared ? n_shared : offsets[e + 1] - row_lo;
   if (n_e <= 0 || n_e < min_rows || n_e > max_rows) return;  // uniform over the workgroup
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nt0 = wgi * kTilesPerWG + wave * NTW;
@@ -179,12 +183,12 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
 
   auto src_row = [&](int p) -> int {
     if (!GATE_UP) return p;
+    if (shared) return p - row_lo;
     return perm ? perm[p] / k_top : p;
   };
 
   for (int m0 = 0; m0 < n_e; m0 += MT * 16) {
     const int rows = min(MT * 16, n_e - m0);
-    const int mtiles = (rows + 15) / 16;
     // activation source rows of this thread's staging vectors (rows past the pass clamp to row 0)
     const uint8_t* asrc[SREG];
 #pragma unroll
@@ -222,7 +226,7 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
       const int kc = (kb % SPC) * 128 + 32 * g;  // byte offset in the LDS chunk row
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        if (m < mtiles) {
+        {  // every row tile, valid or not: rows past the pass hold a clamped row, never stored
           const char* ap = lds_a + (m * 16 + r) * ROWB + kc;
           const uint4 lo = *reinterpret_cast<const uint4*>(ap);
           const uint4 hi = *reinterpret_cast<const uint4*>(ap + 16);
@@ -236,16 +240,10 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
       }
     };
 
-    v8i_t w0[NTW], w1[NTW], w2[NTW], w3[NTW];
-    uint32_t sc_cur[NTW], sc_nxt[NTW];
-    if (ntw > 0) {
-      load_sc(sc_cur, 0);
-      load_w(w0, 0);
-      load_w(w1, 1);
-      load_w(w2, 2);
-    }
+    // The ring runs in static bodies of 4 steps over the whole K; a step that opens a new LDS chunk
+    // first switches chunks (every wave takes part, so waves without tiles still meet the barriers).
     const int nchunks = K / KC;
-    for (int c = 0; c < nchunks; ++c) {
+    auto next_chunk = [&](int c) {
       __syncthreads();  // every wave is done with the previous chunk
 #pragma unroll
       for (int j = 0; j < SREG; ++j) {
@@ -257,30 +255,47 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
 #pragma unroll
         for (int j = 0; j < SREG; ++j) stg[j] = *reinterpret_cast<const uint4*>(asrc[j] + (size_t)(c + 1) * KC);
       }
-      if (ntw > 0) {
+    };
+    v8i_t w0[NTW], w1[NTW], w2[NTW], w3[NTW];
+    uint32_t sc_cur[NTW], sc_nxt[NTW];
+    const bool has_tiles = ntw > 0;
+    if (has_tiles) {
+      load_sc(sc_cur, 0);
+      load_w(w0, 0);
+      load_w(w1, 1);
+      load_w(w2, 2);
+    }
+    for (int kb = 0; kb < KB; kb += 4) {
+      if (kb % SPC == 0) next_chunk(kb / SPC);
+      if (has_tiles) {
+        load_sc(sc_nxt, kb / 4 + 1);
+        load_w(w3, kb + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(w0, sc_cur, kb, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(w0, kb + 4);
+      }
+      if ((kb + 1) % SPC == 0) next_chunk((kb + 1) / SPC);
+      if (has_tiles) {
+        __builtin_amdgcn_sched_barrier(0);
+        compute(w1, sc_cur, kb + 1, 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(w1, kb + 5);
+      }
+      if ((kb + 2) % SPC == 0) next_chunk((kb + 2) / SPC);
+      if (has_tiles) {
+        __builtin_amdgcn_sched_barrier(0);
+        compute(w2, sc_cur, kb + 2, 2);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(w2, kb + 6);
+      }
+      if ((kb + 3) % SPC == 0) next_chunk((kb + 3) / SPC);
+      if (has_tiles) {
+        __builtin_amdgcn_sched_barrier(0);
+        compute(w3, sc_cur, kb + 3, 3);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int body = 0; body < SPC / 4; ++body) {
-          const int kb = c * SPC + 4 * body;
-          load_sc(sc_nxt, kb / 4 + 1);
-          load_w(w3, kb + 3);
-          __builtin_amdgcn_sched_barrier(0);
-          compute(w0, sc_cur, kb, 0);
-          __builtin_amdgcn_sched_barrier(0);
-          load_w(w0, kb + 4);
-          __builtin_amdgcn_sched_barrier(0);
-          compute(w1, sc_cur, kb + 1, 1);
-          __builtin_amdgcn_sched_barrier(0);
-          load_w(w1, kb + 5);
-          __builtin_amdgcn_sched_barrier(0);
-          compute(w2, sc_cur, kb + 2, 2);
-          __builtin_amdgcn_sched_barrier(0);
-          load_w(w2, kb + 6);
-          __builtin_amdgcn_sched_barrier(0);
-          compute(w3, sc_cur, kb + 3, 3);
-          __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int n = 0; n < NTW; ++n) sc_cur[n] = sc_nxt[n];
-        }
+        for (int n = 0; n < NTW; ++n) sc_cur[n] = sc_nxt[n];
       }
     }
 
@@ -299,7 +314,7 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
             const float val = bf16_round(acc[m][n][v]);
             const float up = __shfl_xor(val, 1, 64);
             if (nval && (r & 1) == 0 && orow < rows) {
-              const float wt = row_w ? row_w[perm ? perm[p] : p] : 1.0f;
+              const float wt = (row_w && !shared) ? row_w[perm ? perm[p] : p] : 1.0f;
               const float hval = val / (1.0f + expf(-val)) * up * wt;
               out[(size_t)p * (N / 2) + col / 2] = f2bf(hval);
             }
@@ -313,23 +328,25 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
 }
 
 // Experts with at most kF8TailRows rows take the one-row-tile kernel (two weight tiles per wave,
-// small LDS); larger groups take the 4-row-tile kernel (one weight tile per wave, to stay at two
-// waves per SIMD), whose weight stream serves 64 rows per pass.
+// small LDS); larger groups take the 8-row-tile kernel (one weight tile per wave, 128 rows per
+// pass, so groups up to that size stream their weights once; two waves per SIMD).
 constexpr int kF8TailRows = 16;
+constexpr int kF8DenseMT = 8;
 
 template <bool GATE_UP>
 int launch_moe_fp8(const uint8_t* aq, const uint8_t* as, const int32_t* perm, const int32_t* offsets,
-                   int k_top, const float* row_w, const uint8_t* packed, int E, int N, int K,
-                   uint16_t* out, hipStream_t s) {
+                   int k_top, const float* row_w, const uint8_t* packed, int E, int n_shared, int N,
+                   int K, uint16_t* out, hipStream_t s) {
   const Fp8Geom gm = fp8_geom(E, N, K);
-  hipLaunchKernelGGL((moe_fp8_kernel<GATE_UP, 1, 2>), dim3(E * ceil_div(gm.NT, 8)), dim3(256),
-                     fp8_lds_bytes(1, K), s, aq, as, perm, offsets, k_top, row_w, packed, E, N, K, 1,
-                     kF8TailRows, out);
+  const int groups = E + (n_shared > 0);
+  hipLaunchKernelGGL((moe_fp8_kernel<GATE_UP, 1, 2>), dim3(groups * ceil_div(gm.NT, 8)), dim3(256),
+                     fp8_lds_bytes(1, K), s, aq, as, perm, offsets, k_top, row_w, packed, E, n_shared,
+                     N, K, 1, kF8TailRows, out);
   int rc = check_launch(GATE_UP ? "moe_gate_up_fp8(tail)" : "moe_down_fp8(tail)");
   if (rc) return rc;
-  hipLaunchKernelGGL((moe_fp8_kernel<GATE_UP, 4, 1>), dim3(E * ceil_div(gm.NT, 4)), dim3(256),
-                     fp8_lds_bytes(4, K), s, aq, as, perm, offsets, k_top, row_w, packed, E, N, K,
-                     kF8TailRows + 1, 1 << 30, out);
+  hipLaunchKernelGGL((moe_fp8_kernel<GATE_UP, kF8DenseMT, 1>), dim3(groups * ceil_div(gm.NT, 4)),
+                     dim3(256), fp8_lds_bytes(kF8DenseMT, K), s, aq, as, perm, offsets, k_top, row_w,
+                     packed, E, n_shared, N, K, kF8TailRows + 1, 1 << 30, out);
   return check_launch(GATE_UP ? "moe_gate_up_fp8(dense)" : "moe_down_fp8(dense)");
 }
 
@@ -404,21 +421,22 @@ extern "C" int flyai_fp8_repack(const uint8_t* w1, const uint8_t* s1, const uint
 extern "C" int flyai_moe_gate_up_fp8(const uint8_t* xq, const uint8_t* xs, const int32_t* perm,
                                      const int32_t* offsets, int32_t k, const float* topk_w,
                                      const uint8_t* w13_packed, int32_t E, int32_t H, int32_t I,
-                                     uint16_t* h, flyai_stream_t stream) {
-  FLYAI_REQUIRE(E > 0 && H > 0 && I > 0 && H % 1024 == 0 && H <= 8192 && I % 8 == 0 && k >= 1,
-                "gate_up_fp8: need H %% 1024 == 0, H <= 8192, I %% 8 == 0");
+                                     int32_t n_shared, uint16_t* h, flyai_stream_t stream) {
+  FLYAI_REQUIRE(E > 0 && H > 0 && I > 0 && H % 1024 == 0 && H <= 8192 && I % 8 == 0 && k >= 1 &&
+                    n_shared >= 0,
+                "gate_up_fp8: need H %% 1024 == 0, H <= 8192, I %% 8 == 0, n_shared >= 0");
   FLYAI_REQUIRE(xq && xs && offsets && w13_packed && h, "gate_up_fp8: null pointer");
-  return launch_moe_fp8<true>(xq, xs, perm, offsets, k, topk_w, w13_packed, E, 2 * I, H, h,
+  return launch_moe_fp8<true>(xq, xs, perm, offsets, k, topk_w, w13_packed, E, n_shared, 2 * I, H, h,
                               as_stream(stream));
 }
 
 extern "C" int flyai_moe_down_fp8(const uint8_t* hq, const uint8_t* hs, const int32_t* offsets,
                                   const uint8_t* w2_packed, int32_t E, int32_t H, int32_t I,
-                                  uint16_t* y, flyai_stream_t stream) {
-  FLYAI_REQUIRE(E > 0 && H > 0 && I > 0 && I % 1024 == 0 && I <= 8192 && H % 16 == 0,
-                "down_fp8: need I %% 1024 == 0, I <= 8192, H %% 16 == 0");
+                                  int32_t n_shared, uint16_t* y, flyai_stream_t stream) {
+  FLYAI_REQUIRE(E > 0 && H > 0 && I > 0 && I % 1024 == 0 && I <= 8192 && H % 16 == 0 && n_shared >= 0,
+                "down_fp8: need I %% 1024 == 0, I <= 8192, H %% 16 == 0, n_shared >= 0");
   FLYAI_REQUIRE(hq && hs && offsets && w2_packed && y, "down_fp8: null pointer");
-  return launch_moe_fp8<false>(hq, hs, nullptr, offsets, 1, nullptr, w2_packed, E, H, I, y,
+  return launch_moe_fp8<false>(hq, hs, nullptr, offsets, 1, nullptr, w2_packed, E, n_shared, H, I, y,
                                as_stream(stream));
 }
 

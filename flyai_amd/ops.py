@@ -290,13 +290,17 @@ def fp8_repack(w1, s1, w3=None, s3=None):
     return packed
 
 
-def moe_gate_up_fp8(xq, xs, perm, offsets, k, topk_w, w13_packed, n_experts, inter):
+def moe_gate_up_fp8(xq, xs, perm, offsets, k, topk_w, w13_packed, n_experts, inter, n_shared=0):
     """Rows of expert e: token perm[p] // k (perm None: token p); h = bf16(silu(bf16 gate) * bf16 up
-    * topk_w[perm[p]]) (topk_w None: 1) -> h bf16 [P, inter], P = offsets[-1] rows."""
+    * topk_w[perm[p]]) (topk_w None: 1) -> h bf16 [P + n_shared, inter], P = routed rows.  With
+    n_shared > 0 the packed buffer holds the shared expert as expert n_experts; its rows P.. take
+    tokens 0 .. n_shared-1 with weight 1."""
     T, H = xq.shape
     _need(xq, torch.uint8, (T, H), "xq")
     _need(xs, torch.uint8, (T, H // 128), "xs")
     _need(offsets, torch.int32, (n_experts + 1,), "offsets")
+    if not 0 <= n_shared <= T:
+        raise ValueError("n_shared must be in [0, T]")
     P = T * k if perm is not None else T
     if perm is not None:
         _need(perm, torch.int32, (P,), "perm")
@@ -304,22 +308,26 @@ def moe_gate_up_fp8(xq, xs, perm, offsets, k, topk_w, w13_packed, n_experts, int
         _need(topk_w, torch.float32, None, "topk_w")
         if topk_w.numel() != P:
             raise ValueError("topk_w must hold one weight per routed row")
-    _need(w13_packed, torch.uint8, (fp8_packed_bytes(n_experts, 2 * inter, H),), "w13_packed")
-    h = torch.empty(P, inter, dtype=torch.bfloat16, device=xq.device)
+    groups = n_experts + (n_shared > 0)
+    _need(w13_packed, torch.uint8, (fp8_packed_bytes(groups, 2 * inter, H),), "w13_packed")
+    h = torch.empty(P + n_shared, inter, dtype=torch.bfloat16, device=xq.device)
     check(lib().flyai_moe_gate_up_fp8(_ptr(xq), _ptr(xs), _ptr(perm), _ptr(offsets), k, _ptr(topk_w),
-                                      _ptr(w13_packed), n_experts, H, inter, _ptr(h), _stream()))
+                                      _ptr(w13_packed), n_experts, H, inter, n_shared, _ptr(h), _stream()))
     return h
 
 
-def moe_down_fp8(hq, hs, offsets, w2_packed, n_experts, hidden):
-    P, inter = hq.shape
-    _need(hq, torch.uint8, (P, inter), "hq")
-    _need(hs, torch.uint8, (P, inter // 128), "hs")
+def moe_down_fp8(hq, hs, offsets, w2_packed, n_experts, hidden, n_shared=0):
+    """y[p] = bf16(hq[p] . W2[e]) for routed rows and, with n_shared > 0, the shared expert's rows
+    (the last n_shared rows of hq) -> y bf16 [rows, hidden]."""
+    R, inter = hq.shape
+    _need(hq, torch.uint8, (R, inter), "hq")
+    _need(hs, torch.uint8, (R, inter // 128), "hs")
     _need(offsets, torch.int32, (n_experts + 1,), "offsets")
-    _need(w2_packed, torch.uint8, (fp8_packed_bytes(n_experts, hidden, inter),), "w2_packed")
-    y = torch.empty(P, hidden, dtype=torch.bfloat16, device=hq.device)
+    groups = n_experts + (n_shared > 0)
+    _need(w2_packed, torch.uint8, (fp8_packed_bytes(groups, hidden, inter),), "w2_packed")
+    y = torch.empty(R, hidden, dtype=torch.bfloat16, device=hq.device)
     check(lib().flyai_moe_down_fp8(_ptr(hq), _ptr(hs), _ptr(offsets), _ptr(w2_packed), n_experts, hidden,
-                                   inter, _ptr(y), _stream()))
+                                   inter, n_shared, _ptr(y), _stream()))
     return y
 
 

@@ -259,14 +259,12 @@ class Fp8MoeStage:
                                                  sh.route_scale)
         _, off, perm, inv = ops.moe_permute(ids, E)
         xq, xs = ops.fp8_act_quant(xn)
-        h = ops.moe_gate_up_fp8(xq, xs, perm, off, k, wts, lw.w13_packed, E, I)
+        # routed rows 0..P-1 then the shared expert's T rows, in one launch per projection
+        h = ops.moe_gate_up_fp8(xq, xs, perm, off, k, wts, lw.w13_packed, E, I, n_shared=T)
         hq, hs = ops.fp8_act_quant(h)
-        y = ops.moe_down_fp8(hq, hs, off, lw.w2_packed, E, H)
-        off1 = torch.tensor([0, T], dtype=torch.int32, device=x.device)
-        hsh = ops.moe_gate_up_fp8(xq, xs, None, off1, 1, None, lw.sh13_packed, 1, I)
-        hshq, hshs = ops.fp8_act_quant(hsh)
-        ysh = ops.moe_down_fp8(hshq, hshs, off1, lw.sh2_packed, 1, H)
-        return ops.moe_combine_sum(y, inv, k, shared=ysh, residual=residual, out=residual)
+        y = ops.moe_down_fp8(hq, hs, off, lw.w2_packed, E, H, n_shared=T)
+        P = T * k
+        return ops.moe_combine_sum(y[:P], inv, k, shared=y[P:], residual=residual, out=residual)
 
     def forward(self, hidden):
         """hidden bf16 [T, H], updated in place through every layer."""

@@ -148,6 +148,9 @@ int flyai_router_grouped_sigmoid(const uint16_t* x, const uint16_t* w, const flo
  *   up = bf16(x . W3[e]) (fp8_gemm semantics, kernel.py:241-254); h[p] = bf16(silu(gate) * up *
  *   topk_w[perm[p]]) (topk_w NULL: weight 1) -- h bf16 [P, I].
  * down: y[p] = bf16(hq[p] . W2[e]) with hq/hs = act_quant(h) -- y bf16 [P, H].
+ * Shared expert (model.py:632, :648): with n_shared > 0 the packed buffers hold E+1 experts, the
+ * last being the shared one; its rows P .. P+n_shared-1 (P = offsets[E]) take tokens 0 ..
+ * n_shared-1 with weight 1, so h and y have P + n_shared rows and one launch serves both.
  * combine_sum replaces MoE.forward's accumulation (model.py:640-650): out[t] = bf16(sum over slots
  * in order of y[inv[t*k+s]] + shared[t]) in fp32, then out = bf16(residual + out) when residual is
  * given (shared and residual may be NULL; residual may equal out). */
@@ -158,11 +161,11 @@ int flyai_fp8_repack(const uint8_t* w1, const uint8_t* s1, const uint8_t* w3, co
                      int32_t E, int32_t N, int32_t K, uint8_t* packed, flyai_stream_t stream);
 int flyai_moe_gate_up_fp8(const uint8_t* xq, const uint8_t* xs, const int32_t* perm,
                           const int32_t* offsets, int32_t k, const float* topk_w,
-                          const uint8_t* w13_packed, int32_t E, int32_t H, int32_t I, uint16_t* h,
-                          flyai_stream_t stream);
+                          const uint8_t* w13_packed, int32_t E, int32_t H, int32_t I,
+                          int32_t n_shared, uint16_t* h, flyai_stream_t stream);
 int flyai_moe_down_fp8(const uint8_t* hq, const uint8_t* hs, const int32_t* offsets,
-                       const uint8_t* w2_packed, int32_t E, int32_t H, int32_t I, uint16_t* y,
-                       flyai_stream_t stream);
+                       const uint8_t* w2_packed, int32_t E, int32_t H, int32_t I, int32_t n_shared,
+                       uint16_t* y, flyai_stream_t stream);
 int flyai_moe_combine_sum(const uint16_t* y_perm, const int32_t* inv, int32_t T, int32_t k,
                           int32_t H, const uint16_t* shared, const uint16_t* residual,
                           uint16_t* out, flyai_stream_t stream);

@@ -21,11 +21,23 @@
 //           row r for steps 4kb4 .. 4kb4+3 in bytes 0..3.
 //   gate_up packs w1 and w3 interleaved: packed row 2j = w1 row j, 2j+1 = w3 row j, so the gate and
 //   up of one unit land in neighbouring lanes of the MFMA output.
+#include <type_traits>
+
 #include "common.h"
 
 namespace flyai {
 
 typedef int v8i_t __attribute__((ext_vector_type(8)));
+
+// Calls f(integral_constant<int, I>) for I = B .. N-1: register arrays indexed this way keep
+// constant indices from the start, so they stay in registers.
+template <int B, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < N) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, N>(f);
+  }
+}
 
 struct Fp8Geom {
   int NT, KB, KB4;
@@ -181,7 +193,7 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
   const size_t tile_stride = (size_t)KB * 2048;
   const size_t scale_stride = (size_t)gm.KB4 * 64;
 
-  auto src_row = [&](int p) -> int {
+  auto src_row = [&](int p) __attribute__((always_inline)) -> int {
     if (!GATE_UP) return p;
     if (shared) return p - row_lo;
     return perm ? perm[p] / k_top : p;
@@ -191,27 +203,26 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
     const int rows = min(MT * 16, n_e - m0);
     // activation source rows of this thread's staging vectors (rows past the pass clamp to row 0)
     const uint8_t* asrc[SREG];
-#pragma unroll
-    for (int j = 0; j < SREG; ++j) {
-      const int i = j * 256 + tid;
+    static_for<0, SREG>([&](auto J) {
+      const int i = J * 256 + tid;
       const int rr = i / VPR;
-      asrc[j] = aq + (size_t)src_row(row_lo + m0 + (rr < rows ? rr : 0)) * K + (i % VPR) * 16;
-    }
+      asrc[J] = aq + (size_t)src_row(row_lo + m0 + (rr < rows ? rr : 0)) * K + (i % VPR) * 16;
+    });
     __syncthreads();  // the previous pass is done with LDS
     for (int i = tid; i < MT * 16 * KB; i += 256) {
       const int rr = i / KB, kb = i % KB;
       lds_s[i] = rr < rows ? as[(size_t)src_row(row_lo + m0 + rr) * KB + kb] : (uint8_t)127;
     }
-    uint4 stg[SREG];
-#pragma unroll
-    for (int j = 0; j < SREG; ++j) stg[j] = *reinterpret_cast<const uint4*>(asrc[j]);
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // plain loads, no struct copies
+    u32x4 stg[SREG];
+    static_for<0, SREG>([&](auto J) { stg[J] = *reinterpret_cast<const u32x4*>(asrc[J]); });
 
-    auto load_w = [&](v8i_t (&w)[NTW], int kb) {
+    auto load_w = [&](v8i_t (&w)[NTW], int kb) __attribute__((always_inline)) {
       const size_t kk = (size_t)min(kb, KB - 1) * 2048;
 #pragma unroll
       for (int n = 0; n < NTW; ++n) w[n] = ld_nt_v8(data + min(n, ntw - 1) * tile_stride + kk);
     };
-    auto load_sc = [&](uint32_t (&sc)[NTW], int kb4) {
+    auto load_sc = [&](uint32_t (&sc)[NTW], int kb4) __attribute__((always_inline)) {
       const int kk = min(kb4, gm.KB4 - 1) * 64;
 #pragma unroll
       for (int n = 0; n < NTW; ++n) sc[n] = scl[min(n, ntw - 1) * scale_stride + kk];
@@ -222,7 +233,7 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
 #pragma unroll
       for (int n = 0; n < NTW; ++n) acc[m][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-    auto compute = [&](const v8i_t (&w)[NTW], const uint32_t (&sc)[NTW], int kb, int b) {
+    auto compute = [&](const v8i_t (&w)[NTW], const uint32_t (&sc)[NTW], int kb, int b) __attribute__((always_inline)) {
       const int kc = (kb % SPC) * 128 + 32 * g;  // byte offset in the LDS chunk row
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
@@ -243,18 +254,15 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
     // The ring runs in static bodies of 4 steps over the whole K; a step that opens a new LDS chunk
     // first switches chunks (every wave takes part, so waves without tiles still meet the barriers).
     const int nchunks = K / KC;
-    auto next_chunk = [&](int c) {
+    auto next_chunk = [&](int c) __attribute__((always_inline)) {
       __syncthreads();  // every wave is done with the previous chunk
-#pragma unroll
-      for (int j = 0; j < SREG; ++j) {
-        const int i = j * 256 + tid;
-        *reinterpret_cast<uint4*>(lds_a + (i / VPR) * ROWB + (i % VPR) * 16) = stg[j];
-      }
+      static_for<0, SREG>([&](auto J) {
+        const int i = J * 256 + tid;
+        *reinterpret_cast<u32x4*>(lds_a + (i / VPR) * ROWB + (i % VPR) * 16) = stg[J];
+      });
       __syncthreads();
-      if (c + 1 < nchunks) {
-#pragma unroll
-        for (int j = 0; j < SREG; ++j) stg[j] = *reinterpret_cast<const uint4*>(asrc[j] + (size_t)(c + 1) * KC);
-      }
+      if (c + 1 < nchunks)
+        static_for<0, SREG>([&](auto J) { stg[J] = *reinterpret_cast<const u32x4*>(asrc[J] + (size_t)(c + 1) * KC); });
     };
     v8i_t w0[NTW], w1[NTW], w2[NTW], w3[NTW];
     uint32_t sc_cur[NTW], sc_nxt[NTW];

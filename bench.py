@@ -13,6 +13,10 @@ scales once plus activations in and out.  cpu_baseline runs the CPU oracle on on
 layers (same inputs) and scales to the stage.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+--workload c3 measures the DeepSeek-V3-shaped FP8 stage instead: 4 MoE layers (H 7168, 256 experts,
+top-8 grouped sigmoid routing with a Zipf-shaped selection bias, one shared expert, I 2048, e4m3
+weights with 128x128 E8M0 block scales), a ragged batch of 64 sequences of 1, 2 or 4 tokens.
 """
 import argparse
 import json
@@ -61,12 +65,29 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after timing, copy a buffer of this many MiB 3 times (a known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
+    ap.add_argument("--workload", choices=("c1", "c3"), default="c1")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the stage is single-GPU by design: no collectives, no sharding)", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "c3":
+        run_c3(args)
+    else:
+        run_c1(args)
 
+
+def copy_probe(mib, dev):
+    import torch
+    if mib > 0:
+        src = torch.empty(mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
+
+def run_c1(args):
     import torch
     from flyai_amd import ops
     from flyai_amd.rope import YarnRotary
@@ -139,13 +160,7 @@ def main():
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
 
-    if args.copy_probe_mib > 0:
-        src = torch.empty(args.copy_probe_mib << 20, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
+    copy_probe(args.copy_probe_mib, dev)
 
     cpu = None
     if not args.no_cpu:
@@ -171,6 +186,135 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
+
+
+def c3_batch(seed=0):
+    rng = np.random.default_rng(seed)
+    return [int(v) for v in rng.choice([1, 2, 4], size=64)]
+
+
+def run_c3(args):
+    import torch
+    from flyai_amd import ops
+    from flyai_amd.runtime import Fp8MoeStage
+    from flyai_amd.weights import DsV3Shape, synthetic_fp8_moe_layer
+
+    dev = "cuda"
+    torch.cuda.set_device(0)
+    sh = DsV3Shape()
+    n_layers = 4
+    q_lens = c3_batch(0)
+    T = sum(q_lens)
+    E, k, H, I = sh.n_experts, sh.top_k, sh.hidden, sh.intermediate
+    print(f"[bench] building {n_layers}-layer FP8 stage (T={T}) ...", file=sys.stderr, flush=True)
+    layers = [synthetic_fp8_moe_layer(sh, 2000 + i, dev, keep_raw=(i == 0 and not args.no_cpu))
+              for i in range(n_layers)]
+    stage = Fp8MoeStage(sh, layers)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    hidden0 = torch.randn(T, H, device=dev, generator=g).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    print("[bench] warmup", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        stage.forward(hidden0.clone())
+    torch.cuda.synchronize()
+    print("[bench] timed steps", file=sys.stderr, flush=True)
+    hs = [hidden0.clone() for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        stage.forward(hs[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    value = T * args.steps / elapsed
+
+    # dominant op: the FP8 gate_up of layer 0 (routed + shared groups; tail and dense launches)
+    lw = layers[0]
+    xn = ops.rmsnorm(hidden0, lw.ln, sh.rms_eps)
+    ids, wts, _ = ops.router_grouped_sigmoid(xn, lw.router_w, lw.e_bias, sh.n_group, sh.topk_group, k,
+                                             sh.route_scale)
+    hist, off, perm, inv = ops.moe_permute(ids, E)
+    xq, xs = ops.fp8_act_quant(xn)
+    h = ops.moe_gate_up_fp8(xq, xs, perm, off, k, wts, lw.w13_packed, E, I, n_shared=T)
+    hq, hsc = ops.fp8_act_quant(h)
+    torch.cuda.synchronize()
+    hist_np = hist.cpu().numpy()
+    groups = int((hist_np > 0).sum()) + 1
+    reps = args.kernel_reps
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    ev[0].record()
+    for _ in range(reps):
+        ops.moe_gate_up_fp8(xq, xs, perm, off, k, wts, lw.w13_packed, E, I, n_shared=T)
+    ev[1].record()
+    for _ in range(reps):
+        ops.moe_down_fp8(hq, hsc, off, lw.w2_packed, E, H, n_shared=T)
+    ev[2].record()
+    torch.cuda.synchronize()
+    gu_us = ev[0].elapsed_time(ev[1]) * 1e3 / reps
+    dn_us = ev[1].elapsed_time(ev[2]) * 1e3 / reps
+    P = T * k + T
+    gu_bytes = groups * (2 * I * H + 2 * (I // 128) * (H // 128)) + T * H + T * (H // 128) + P * I * 2
+    dn_bytes = groups * (H * I + (H // 128) * (I // 128)) + P * I + P * (I // 128) + P * H * 2
+    gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
+    dn_gbs = dn_bytes / (dn_us * 1e-6) / 1e9
+    copy_probe(args.copy_probe_mib, dev)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_c3(sh, lw, hidden0, n_layers, n_tokens=16)
+
+    line = {
+        "metric": "stage tokens/sec at ragged batch 64 (FP8 MoE stage); MoE layer us; % HBM roofline",
+        "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(elapsed * 1e3 / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp8-e4m3 (E8M0 128x128 block scales), fp32 accumulate",
+        "data": "synthetic (seeded random-init weights quantised per 128x128 block, N(0,1) activations)",
+        "config": {"workload": "DeepSeek-V3-shaped 4-layer FP8 MoE stage, ragged batch of 64 sequences of "
+                               "1/2/4 tokens, 256 experts top-8 grouped sigmoid (Zipf-shaped bias) + 1 shared",
+                   "layers": n_layers, "tokens": T, "sequences": len(q_lens), "experts": E, "top_k": k,
+                   "hidden": H, "intermediate": I, "parallelism": "single GPU"},
+        "moe_layer_us": round(gu_us + dn_us, 2),
+        "roofline": {"bound": "hbm", "kernel": "moe_fp8_kernel<gate_up> (tail + dense launches)",
+                     "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": gu_bytes,
+                     "avg_us": round(gu_us, 2), "groups_touched": groups},
+        "kernels": {"moe_down_fp8": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),
+                                     "frac": round(dn_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": dn_bytes}},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+def cpu_baseline_c3(sh, lw, hidden0, n_layers, n_tokens):
+    """The CPU oracle's FP8 MoE layer on the first n_tokens tokens of the batch (every expert those
+    tokens route to, plus the shared expert); stage tokens/s = n_tokens / (n_layers * t)."""
+    import torch
+    from oracle import experts as oexperts
+    from oracle import layer as olayer
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+
+    class Experts:
+        def __init__(self, raw):
+            self.raw = raw
+
+        def expert(self, e, x, weight=None):
+            r = self.raw
+            f8 = lambda t: t[e].cpu().view(torch.float8_e4m3fn).float().numpy()
+            e8 = lambda t: np.ldexp(np.float32(1.0), t[e].cpu().numpy().astype(np.int32) - 127).astype(np.float32)
+            return oexperts.deepseek_expert(x, f8(r["w1"]), e8(r["s1"]), f8(r["w3"]), e8(r["s3"]),
+                                            f8(r["w2"]), e8(r["s2"]), weight)
+
+    h = hidden0[:n_tokens].float().cpu()
+    print("[bench] cpu oracle: one FP8 MoE layer", file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    olayer.deepseek_moe_layer(h, lw.ln.cpu(), sh.rms_eps, lw.router_w.float().cpu().numpy(), lw.e_bias.cpu().numpy(),
+                              sh.n_group, sh.topk_group, sh.top_k, sh.route_scale, Experts(lw.raw),
+                              Experts(lw.shared_raw))
+    dt = time.perf_counter() - t0
+    return {"value": round(n_tokens / (dt * n_layers), 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle (numpy fp64 block GEMMs + torch) on 1 of {n_layers} layers for the first "
+                      f"{n_tokens} tokens of the batch: {dt:.2f} s; stage rate = {n_tokens} / ({n_layers} x layer time)"}
 
 
 def cpu_baseline(lw, kv, layer_idx, hidden0, q_lens, starts, slots, shape, maxlen, n_layers):

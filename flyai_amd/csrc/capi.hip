@@ -36,8 +36,8 @@ int launch_route_permute(const uint16_t*, const uint16_t*, const uint16_t*, int,
 int launch_combine(const float*, const int32_t*, const float*, int, int, int, const uint16_t*,
                    uint16_t*, const float*, float, uint16_t*, hipStream_t);
 int launch_moe_gate_up(const uint16_t*, const int32_t*, const int32_t*, int, const uint8_t*,
-                       const float*, int, int, int, uint16_t*, hipStream_t);
-int launch_moe_down(const uint16_t*, const int32_t*, const uint8_t*, const float*, int, int, int,
+                       const float*, int, int, int, int, uint16_t*, hipStream_t);
+int launch_moe_down(const uint16_t*, const int32_t*, const uint8_t*, const float*, int, int, int, int,
                     float*, hipStream_t);
 int launch_rmsnorm(const uint16_t*, const float*, int, int, float, uint16_t*, hipStream_t);
 int launch_linear_residual_rmsnorm(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int,
@@ -343,8 +343,9 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
                              F32(st->o_w), F32(st->o_logits), I32(st->o_hist), I32(st->o_off),
                              I32(st->o_perm), I32(st->o_inv), s));
     RUN(launch_moe_gate_up(B16(st->o_xn), I32(st->o_perm), I32(st->o_off), k, L.w13_packed, L.b13,
-                           E, H, I, B16(st->o_hmoe), s));
-    RUN(launch_moe_down(B16(st->o_hmoe), I32(st->o_off), L.w2_packed, L.b2, E, H, I, F32(st->o_y), s));
+                           Tn, E, H, I, B16(st->o_hmoe), s));
+    RUN(launch_moe_down(B16(st->o_hmoe), I32(st->o_off), L.w2_packed, L.b2, Tn * k, E, H, I,
+                        F32(st->o_y), s));
     const float* next_ln1 = (l + 1 < c.n_layers) ? st->layers[l + 1].ln1 : nullptr;
     RUN(launch_combine(F32(st->o_y), I32(st->o_inv), F32(st->o_w), Tn, k, H, hidden, hidden, next_ln1,
                        c.rms_eps, B16(st->o_xn), s));

@@ -138,7 +138,7 @@ def moe_gate_up(x, perm, offsets, k, w13_packed, b13, n_experts, inter):
     _need(b13, torch.float32, (n_experts, 2 * inter), "b13")
     _need(w13_packed, torch.uint8, (mxfp4_packed_bytes(n_experts, 2 * inter, H),), "w13_packed")
     h = torch.empty(T * k, inter, dtype=torch.bfloat16, device=x.device)
-    check(lib().flyai_moe_gate_up_mxfp4(_ptr(x), _ptr(perm), _ptr(offsets), k, _ptr(w13_packed),
+    check(lib().flyai_moe_gate_up_mxfp4(_ptr(x), _ptr(perm), _ptr(offsets), T, k, _ptr(w13_packed),
                                         _ptr(b13), n_experts, H, inter, _ptr(h), _stream()))
     return h
 
@@ -150,7 +150,7 @@ def moe_down(h, offsets, w2_packed, b2, n_experts, hidden):
     _need(b2, torch.float32, (n_experts, hidden), "b2")
     _need(w2_packed, torch.uint8, (mxfp4_packed_bytes(n_experts, hidden, inter),), "w2_packed")
     y = torch.empty(P, hidden, dtype=torch.float32, device=h.device)
-    check(lib().flyai_moe_down_mxfp4(_ptr(h), _ptr(offsets), _ptr(w2_packed), _ptr(b2), n_experts,
+    check(lib().flyai_moe_down_mxfp4(_ptr(h), _ptr(offsets), P, _ptr(w2_packed), _ptr(b2), n_experts,
                                      hidden, inter, _ptr(y), _stream()))
     return y
 

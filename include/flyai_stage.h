@@ -112,14 +112,16 @@ int flyai_mxfp4_repack(const uint8_t* blocks, const uint8_t* scales, int32_t E, 
  *   h[p, j] = bf16((clamp(up,-7,7)+1) * min(gate,7) * sigmoid(1.702*min(gate,7))).
  * down: y_perm[p] = h[p] . W2[e]^T + b2[e] (fp32).
  * x bf16 [T,H]; w13_packed/w2_packed from flyai_mxfp4_repack; b13 fp32 [E,2I]; b2 fp32 [E,H];
- * h bf16 [T*k, I]; y_perm fp32 [T*k, H].  Groups of any row count are handled: MFMA on
- * dequantised tiles for every group (16 rows per MFMA tile). */
+ * h bf16 [T*k, I]; y_perm fp32 [T*k, H] (rows = T*k).  Groups of any row count are handled, with
+ * MFMA on tiles dequantised in registers: decode-sized groups stream the expert's weights once per
+ * 8 rows; when the batch averages at least 8 rows per expert, groups of more than 8 rows take the
+ * dense kernel (96 rows per weight pass). */
 int flyai_moe_gate_up_mxfp4(const uint16_t* x, const int32_t* perm, const int32_t* offsets,
-                            int32_t k, const uint8_t* w13_packed, const float* b13, int32_t E,
-                            int32_t H, int32_t I, uint16_t* h, flyai_stream_t stream);
-int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, const uint8_t* w2_packed,
-                         const float* b2, int32_t E, int32_t H, int32_t I, float* y_perm,
-                         flyai_stream_t stream);
+                            int32_t T, int32_t k, const uint8_t* w13_packed, const float* b13,
+                            int32_t E, int32_t H, int32_t I, uint16_t* h, flyai_stream_t stream);
+int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, int32_t rows,
+                         const uint8_t* w2_packed, const float* b2, int32_t E, int32_t H, int32_t I,
+                         float* y_perm, flyai_stream_t stream);
 
 /* ---- a2 (DeepSeek-V3 shape): grouped sigmoid router ---------------------------------------------
  * Replaces KimiMoEGate.forward (vendor/kimi_k3_ref/modeling_kimi_linear.py:703-759) / the V4 Gate

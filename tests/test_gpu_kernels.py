@@ -156,9 +156,11 @@ def test_combine_matches_oracle():
 
 # ---- a5 / a6 -----------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("T,E,lens", [(12, 128, None), (128, 8, None), (3, 4, None)])
-def test_moe_experts_vs_oracle(T, E, lens):
-    """gate_up (+SwiGLU) and down through the packed MXFP4 layout, decode-sized and dense groups."""
+@pytest.mark.parametrize("T,E", [(12, 128), (128, 8), (3, 4), (320, 4)])
+def test_moe_experts_vs_oracle(T, E):
+    """gate_up (+SwiGLU) and down through the packed MXFP4 layout.  (12, 128) and (3, 4) are
+    decode-sized (row-pass kernel); (128, 8) averages 64 rows per expert (dense kernel, one pass);
+    (320, 4) puts all 320 tokens on every expert (dense kernel, four passes of up to 96 rows)."""
     from flyai_amd import ops
     from flyai_amd.weights import GptOssShape, synthetic_moe
     shape = GptOssShape(n_experts=E)
@@ -179,8 +181,6 @@ def test_moe_experts_vs_oracle(T, E, lens):
                                     return_h=True)
     mar, cos = _metrics(h.float().cpu().numpy(), rh.numpy())
     assert mar <= MAR and cos >= COS, f"gate_up+swiglu: {mar:.3g} {cos:.6f}"
-    # down is checked against the oracle applied to the GPU's own h (isolates the second GEMM)
-    yd = oexperts.experts_mxfp4  # noqa: F841
     mar, cos = _metrics(y.cpu().numpy(), ry.numpy())
     assert mar <= MAR and cos >= COS, f"down: {mar:.3g} {cos:.6f}"
 

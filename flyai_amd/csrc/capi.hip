@@ -42,6 +42,11 @@ int launch_moe_down(const uint16_t*, const int32_t*, const uint8_t*, const float
 int launch_rmsnorm(const uint16_t*, const float*, int, int, float, uint16_t*, hipStream_t);
 int launch_linear_residual_rmsnorm(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int,
                                    uint16_t*, const float*, float, uint16_t*, float*, hipStream_t);
+int launch_linear_residual_rmsnorm_logits(const uint16_t*, const uint16_t*, const uint16_t*, int, int,
+                                          int, const uint16_t*, uint16_t*, const float*, float, uint16_t*,
+                                          float*, const uint16_t*, const uint16_t*, int, float*, hipStream_t);
+int launch_topk_permute(const float*, int, int, int, int32_t*, float*, int32_t*, int32_t*, int32_t*,
+                        int32_t*, hipStream_t);
 int launch_qkv_rope_kv(const uint16_t*, const uint16_t*, const uint16_t*, float*, const int32_t*,
                        const int32_t*, const uint16_t*, const uint16_t*, int, int, int, int, int, int,
                        const int64_t*, const int32_t*, uint16_t*, uint16_t*, uint16_t*, hipStream_t);
@@ -81,6 +86,7 @@ struct flyai_stage {
   size_t o_blob, blob_max, o_cu, o_pos, o_sid, o_kvlen, o_slot, o_status;
   size_t o_xn, o_gemm, o_qrot, o_attn, o_parts;
   size_t o_ids, o_w, o_logits, o_hist, o_off, o_perm, o_inv, o_hmoe, o_y;
+  size_t o_h2;  // the post-attention residual stream of the decode-sized path
   size_t dev_bytes = 0;
   size_t host_half = 0;  // bytes of one pinned staging half (== blob_max)
   std::vector<flyai_attn_item> plan_items[2];
@@ -128,6 +134,7 @@ static void layout(flyai_stage* st) {
   st->o_inv = d.take(P * 4);
   st->o_hmoe = d.take(P * c.intermediate * 2);
   st->o_y = d.take(P * c.hidden * 4);
+  st->o_h2 = d.take(T * c.hidden * 2);
   st->dev_bytes = d.off;
   st->host_half = st->blob_max;
 }
@@ -337,17 +344,29 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
                     reinterpret_cast<const flyai_attn_item*>(blob + off_items[p]), n_items[p], n_small[p],
                     reinterpret_cast<const flyai_attn_group*>(blob + off_groups[p]), n_groups[p],
                     F32(st->o_parts), B16(st->o_attn), s));
-    RUN(launch_linear_residual_rmsnorm(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
-                                       hidden, L.ln2, c.rms_eps, B16(st->o_xn), F32(st->o_gemm), s));
-    RUN(launch_route_permute(B16(st->o_xn), L.router_w, L.router_b, Tn, H, E, k, I32(st->o_ids),
-                             F32(st->o_w), F32(st->o_logits), I32(st->o_hist), I32(st->o_off),
-                             I32(st->o_perm), I32(st->o_inv), s));
+    if (Tn <= 256 && Tn * k <= 4096) {
+      // decode-sized: o-proj finalize + residual + RMSNorm + router logits, then top-k + permute
+      RUN(launch_linear_residual_rmsnorm_logits(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
+                                                hidden, B16(st->o_h2), L.ln2, c.rms_eps, B16(st->o_xn),
+                                                F32(st->o_gemm), L.router_w, L.router_b, E,
+                                                F32(st->o_logits), s));
+      RUN(launch_topk_permute(F32(st->o_logits), Tn, E, k, I32(st->o_ids), F32(st->o_w), I32(st->o_hist),
+                              I32(st->o_off), I32(st->o_perm), I32(st->o_inv), s));
+    } else {
+      RUN(launch_linear_residual_rmsnorm(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
+                                         hidden, L.ln2, c.rms_eps, B16(st->o_xn), F32(st->o_gemm), s));
+      RUN(launch_route_permute(B16(st->o_xn), L.router_w, L.router_b, Tn, H, E, k, I32(st->o_ids),
+                               F32(st->o_w), F32(st->o_logits), I32(st->o_hist), I32(st->o_off),
+                               I32(st->o_perm), I32(st->o_inv), s));
+    }
     RUN(launch_moe_gate_up(B16(st->o_xn), I32(st->o_perm), I32(st->o_off), k, L.w13_packed, L.b13,
                            Tn, E, H, I, B16(st->o_hmoe), s));
     RUN(launch_moe_down(B16(st->o_hmoe), I32(st->o_off), L.w2_packed, L.b2, Tn * k, E, H, I,
                         F32(st->o_y), s));
     const float* next_ln1 = (l + 1 < c.n_layers) ? st->layers[l + 1].ln1 : nullptr;
-    RUN(launch_combine(F32(st->o_y), I32(st->o_inv), F32(st->o_w), Tn, k, H, hidden, hidden, next_ln1,
+    // the fused path left the post-attention residual in o_h2; the other path updated hidden in place
+    const uint16_t* resid = (Tn <= 256 && Tn * k <= 4096) ? B16(st->o_h2) : hidden;
+    RUN(launch_combine(F32(st->o_y), I32(st->o_inv), F32(st->o_w), Tn, k, H, resid, hidden, next_ln1,
                        c.rms_eps, B16(st->o_xn), s));
   }
   return FLYAI_OK;

@@ -73,4 +73,200 @@ inline hipStream_t as_stream(flyai_stream_t s) { return reinterpret_cast<hipStre
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Top-k + softmax of one token by one lane.  The lane streams its token's logits in ascending expert
+// id and keeps a sorted list of K (value, id); a value enters only if strictly greater than the
+// current K-th and bubbles up past strictly smaller values, so equal values keep ascending ids --
+// the (value desc, id asc) order.  Softmax over the K selected values in fp32, then ids sorted
+// ascending carrying their weights.  Logit rows are 16-byte aligned (E % 4 == 0).
+template <int K>
+__device__ __forceinline__ void topk_softmax_lane(const float* __restrict__ lrow, int E,
+                                                  int32_t* ids_out, float* w_out) {
+  float sv[K];
+  int si[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) { sv[j] = -INFINITY; si[j] = 0x7fffffff; }
+  for (int e0 = 0; e0 < E; e0 += 16) {
+    float4 v4[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      v4[c] = (e0 + 4 * c < E) ? reinterpret_cast<const float4*>(lrow + e0)[c]
+                               : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float4& q = v4[i >> 2];
+      const float v = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
+      const int id = e0 + i;
+      if (id < E && v > sv[K - 1]) {
+        sv[K - 1] = v;
+        si[K - 1] = id;
+#pragma unroll
+        for (int j = K - 1; j > 0; --j) {
+          if (sv[j] > sv[j - 1]) {
+            const float tv = sv[j]; sv[j] = sv[j - 1]; sv[j - 1] = tv;
+            const int ti = si[j]; si[j] = si[j - 1]; si[j - 1] = ti;
+          }
+        }
+      }
+    }
+  }
+  float ex[K], sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < K; ++j) { ex[j] = expf(sv[j] - sv[0]); sum += ex[j]; }
+  // ascending ids (odd-even transposition sort, K passes)
+#pragma unroll
+  for (int pass = 0; pass < K; ++pass)
+#pragma unroll
+    for (int j = pass & 1; j + 1 < K; j += 2)
+      if (si[j] > si[j + 1]) {
+        const int ti = si[j]; si[j] = si[j + 1]; si[j + 1] = ti;
+        const float te = ex[j]; ex[j] = ex[j + 1]; ex[j + 1] = te;
+      }
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    ids_out[j] = si[j];
+    w_out[j] = ex[j] / sum;
+  }
+}
+
+// The same top-k + softmax by a whole wave (E <= 256): each lane holds E/64 logits; K rounds of a
+// wave-wide argmax over (value desc, id asc) give the same selection in the same order as
+// topk_softmax_lane, and every lane then does the identical softmax / id sort, so ids and weights
+// are bit-identical to it.  Lanes 0..K-1 write the outputs.
+template <int K>
+__device__ __forceinline__ void topk_softmax_wave_vals(const float (&v)[4], int E, int lane,
+                                                       int32_t* ids_out, float* w_out) {
+  bool taken[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) taken[j] = 4 * lane + j >= E;
+  float sv[K];
+  int si[K];
+#pragma unroll
+  for (int r = 0; r < K; ++r) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * lane + j;
+      if (!taken[j] && (v[j] > bv || (v[j] == bv && e < bi))) { bv = v[j]; bi = e; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oi = __shfl_xor(bi, o, 64);
+      if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    }
+    sv[r] = bv;
+    si[r] = bi;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * lane + j == bi) taken[j] = true;
+  }
+  float ex[K], sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < K; ++j) { ex[j] = expf(sv[j] - sv[0]); sum += ex[j]; }
+#pragma unroll
+  for (int pass = 0; pass < K; ++pass)
+#pragma unroll
+    for (int j = pass & 1; j + 1 < K; j += 2)
+      if (si[j] > si[j + 1]) {
+        const int ti = si[j]; si[j] = si[j + 1]; si[j + 1] = ti;
+        const float te = ex[j]; ex[j] = ex[j + 1]; ex[j + 1] = te;
+      }
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+    if (lane == j) {
+      ids_out[j] = si[j];
+      w_out[j] = ex[j] / sum;
+    }
+}
+
+// lane l's logits of a row: experts 4l .. 4l+3 (-inf past E)
+__device__ __forceinline__ void load_logits_lane(const float* __restrict__ lrow, int E, int lane, float (&v)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = 4 * lane + j;
+    v[j] = e < E ? lrow[e] : -INFINITY;
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void topk_softmax_wave(const float* __restrict__ lrow, int E, int lane,
+                                                  int32_t* ids_out, float* w_out) {
+  float v[4];
+  load_logits_lane(lrow, E, lane, v);
+  topk_softmax_wave_vals<K>(v, E, lane, ids_out, w_out);
+}
+
+// The same top-k + softmax with four lanes per token (lanes 4t .. 4t+3, `sub` = lane % 4): each
+// lane keeps the sorted top K of its quarter of the logits (ascending ids, strict > insertion), then
+// two xor-shuffle rounds merge the lists under (value desc, id asc), so all four lanes hold the
+// same sorted selection as topk_softmax_lane and compute the identical softmax; sub 0 writes.
+// lrow must be 16-byte aligned and the quarter Q = E/4 a multiple of 4 (E % 16 == 0).
+template <int K>
+__device__ __forceinline__ void topk_softmax_quad(const float* __restrict__ lrow, int E, int sub,
+                                                  int32_t* ids_out, float* w_out) {
+  float sv[K];
+  int si[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) { sv[j] = -INFINITY; si[j] = 0x7fffffff; }
+  const int Q = E / 4;
+  for (int e0 = sub * Q; e0 < (sub + 1) * Q; e0 += 4) {
+    const float4 q = *reinterpret_cast<const float4*>(lrow + e0);
+    const float vv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (vv[i] > sv[K - 1]) {
+        sv[K - 1] = vv[i];
+        si[K - 1] = e0 + i;
+#pragma unroll
+        for (int j = K - 1; j > 0; --j)
+          if (sv[j] > sv[j - 1]) {
+            const float tv = sv[j]; sv[j] = sv[j - 1]; sv[j - 1] = tv;
+            const int ti = si[j]; si[j] = si[j - 1]; si[j - 1] = ti;
+          }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 1; o <= 2; o <<= 1) {
+    float pv[K];
+    int pi[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) { pv[j] = __shfl_xor(sv[j], o, 64); pi[j] = __shfl_xor(si[j], o, 64); }
+#pragma unroll
+    for (int m = 0; m < K; ++m) {
+      // insert (pv[m], pi[m]) under (value desc, id asc)
+      const bool in = pv[m] > sv[K - 1] || (pv[m] == sv[K - 1] && pi[m] < si[K - 1]);
+      if (in) {
+        sv[K - 1] = pv[m];
+        si[K - 1] = pi[m];
+#pragma unroll
+        for (int j = K - 1; j > 0; --j)
+          if (sv[j] > sv[j - 1] || (sv[j] == sv[j - 1] && si[j] < si[j - 1])) {
+            const float tv = sv[j]; sv[j] = sv[j - 1]; sv[j - 1] = tv;
+            const int ti = si[j]; si[j] = si[j - 1]; si[j - 1] = ti;
+          }
+      }
+    }
+  }
+  float ex[K], sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < K; ++j) { ex[j] = expf(sv[j] - sv[0]); sum += ex[j]; }
+#pragma unroll
+  for (int pass = 0; pass < K; ++pass)
+#pragma unroll
+    for (int j = pass & 1; j + 1 < K; j += 2)
+      if (si[j] > si[j + 1]) {
+        const int ti = si[j]; si[j] = si[j + 1]; si[j + 1] = ti;
+        const float te = ex[j]; ex[j] = ex[j + 1]; ex[j + 1] = te;
+      }
+  if (sub == 0) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      ids_out[j] = si[j];
+      w_out[j] = ex[j] / sum;
+    }
+  }
+}
+
 }  // namespace flyai

@@ -167,6 +167,89 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_finalize_kernel(
   }
 }
 
+// Residual + RMSNorm finalize fused with the GPT-OSS router logits of the same token (decode-sized
+// batches).  Grid (T, kRouteSplit): every workgroup of a token computes the finalize (the new
+// residual stream goes to h_out, never in place, since all of them read h_in; workgroup 0 writes it
+// and xn), keeps xn in LDS and computes the logits of its E/kRouteSplit experts with exactly the
+// fixed order of router_logits_kernel (lane l sums k = 512 j + 8 l + i in order, then a xor
+// butterfly 32..1; bf16(dot + bias)).  The top-k follows in the next kernel: workgroups of one
+// kernel never exchange data (a device-scope fence would write back the L2).
+constexpr int kRouteSplit = 4;
+
+template <int JMAX>
+__global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_logits_kernel(
+    const float* __restrict__ part, int slices, const uint16_t* __restrict__ b, int M, int H,
+    const uint16_t* __restrict__ h_in, uint16_t* __restrict__ h_out, const float* __restrict__ lnw,
+    float eps, uint16_t* __restrict__ xn, const uint16_t* __restrict__ rw,
+    const uint16_t* __restrict__ rb, int E, float* __restrict__ logits) {
+  __shared__ float red[kRowThreads / 64];
+  __shared__ __align__(16) uint16_t xs[JMAX * 512];
+  const int t = blockIdx.x, split = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int per = (E + kRouteSplit - 1) / kRouteSplit;
+  const int e_lo = split * per, e_hi = min(E, e_lo + per);
+  constexpr int kBatch = JMAX <= 6 ? 2 : 1;  // experts per wave in flight
+  // the first batch of router weights does not depend on xn: issue it before the finalize
+  uint4 wv[kBatch][JMAX];
+  auto load_batch = [&](int e0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int c = 0; c < kBatch; ++c)
+#pragma unroll
+      for (int j = 0; j < JMAX; ++j) {
+        const int k0 = 512 * j + 8 * lane;
+        wv[c][j] = (e0 + c < e_hi && k0 < H) ? *reinterpret_cast<const uint4*>(rw + (size_t)(e0 + c) * H + k0)
+                                             : make_uint4(0, 0, 0, 0);
+      }
+  };
+  load_batch(e_lo + wave * kBatch);
+  const size_t stride = (size_t)M * H;
+  float ss = 0.f;
+  for (int i = tid; i < H; i += kRowThreads) {
+    const size_t idx = (size_t)t * H + i;
+    const float o = bf16_round(sum_slices(part, slices, stride, idx) + (b ? bf2f(b[i]) : 0.f));
+    const uint16_t hv = f2bf(bf2f(h_in[idx]) + o);
+    xs[i] = hv;  // the new residual, normalised in place below
+    if (split == 0) h_out[idx] = hv;
+    const float hf = bf2f(hv);
+    ss = fmaf(hf, hf, ss);
+  }
+  const float rr = rsqrtf(block_sum_1024(ss, red) / (float)H + eps);
+  for (int i = tid; i < H; i += kRowThreads) {
+    const uint16_t v = f2bf(lnw[i] * (bf2f(xs[i]) * rr));
+    if (split == 0) xn[(size_t)t * H + i] = v;
+    xs[i] = v;
+  }
+  __syncthreads();
+  for (int e0 = e_lo + wave * kBatch; e0 < e_hi; e0 += (kRowThreads / 64) * kBatch) {
+    if (e0 != e_lo + wave * kBatch) load_batch(e0);
+    float acc[kBatch] = {};
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) {
+      const int k0 = 512 * j + 8 * lane;
+      if (k0 >= H) break;  // lanes past the row end keep their partial unchanged
+      const uint4 xv = *reinterpret_cast<const uint4*>(xs + k0);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int c = 0; c < kBatch; ++c) {
+        const uint32_t ww[4] = {wv[c][j].x, wv[c][j].y, wv[c][j].z, wv[c][j].w};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float xf = __uint_as_float((i & 1) ? (xw[i >> 1] & 0xffff0000u) : (xw[i >> 1] << 16));
+          const float wf = __uint_as_float((i & 1) ? (ww[i >> 1] & 0xffff0000u) : (ww[i >> 1] << 16));
+          acc[c] = fmaf(xf, wf, acc[c]);  // exact product: fma == mul + add
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < kBatch; ++c) {
+      float v = acc[c];
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+      if (lane == 0 && e0 + c < e_hi) logits[(size_t)t * E + e0 + c] = bf16_round(v + bf2f(rb[e0 + c]));
+    }
+  }
+}
+
 int gemm_slices(int K) { return ((K + 127) / 128 + kKQW - 1) / kKQW; }
 
 size_t linear_partials_bytes(int M, int N, int K) { return (size_t)gemm_slices(K) * M * N * sizeof(float); }
@@ -199,6 +282,31 @@ int launch_linear_residual_rmsnorm(const uint16_t* x, const uint16_t* W, const u
                      gemm_slices(K),
                      b, M, N, h, lnw, eps, xn);
   return check_launch("residual_rmsnorm_finalize");
+}
+
+// Output projection + residual + RMSNorm + router logits for batches of at most kFusedRouteTokens
+// tokens (each token's kRouteSplit workgroups read the router matrix once between them, from L2).
+// The new residual stream is written to h_out.
+constexpr int kFusedRouteTokens = 256;
+
+int launch_linear_residual_rmsnorm_logits(const uint16_t* x, const uint16_t* W, const uint16_t* b, int M,
+                                          int N, int K, const uint16_t* h_in, uint16_t* h_out,
+                                          const float* lnw, float eps, uint16_t* xn, float* part,
+                                          const uint16_t* rw, const uint16_t* rb, int E, float* logits,
+                                          hipStream_t s) {
+  if (M == 0) return FLYAI_OK;
+  if (M > kFusedRouteTokens || N > 7168 || N % 8 || E > 256)
+    return set_error(FLYAI_EINVAL, "fused router logits: needs T <= 256, H %% 8 == 0, H <= 7168, E <= 256");
+  int rc = launch_gemm_splitk(x, W, M, N, K, part, s);
+  if (rc) return rc;
+  const int slices = gemm_slices(K);
+  if (N <= 3072)
+    hipLaunchKernelGGL((residual_rmsnorm_logits_kernel<6>), dim3(M, kRouteSplit), dim3(kRowThreads), 0, s,
+                       part, slices, b, M, N, h_in, h_out, lnw, eps, xn, rw, rb, E, logits);
+  else
+    hipLaunchKernelGGL((residual_rmsnorm_logits_kernel<14>), dim3(M, kRouteSplit), dim3(kRowThreads), 0, s,
+                       part, slices, b, M, N, h_in, h_out, lnw, eps, xn, rw, rb, E, logits);
+  return check_launch("residual_rmsnorm_logits");
 }
 
 // ---- QKV finalize + RoPE (GPT-OSS half split, per-op bf16 rounding) + K/V append ------------------

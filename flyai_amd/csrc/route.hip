@@ -77,61 +77,6 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   }
 }
 
-// Top-k + softmax of one token by one lane.  The lane streams its token's logits in ascending expert
-// id and keeps a sorted list of K (value, id); a value enters only if strictly greater than the
-// current K-th and bubbles up past strictly smaller values, so equal values keep ascending ids --
-// the (value desc, id asc) order.  Softmax over the K selected values in fp32, then ids sorted
-// ascending carrying their weights.  Logit rows are 16-byte aligned (E % 4 == 0).
-template <int K>
-__device__ __forceinline__ void topk_softmax_lane(const float* __restrict__ lrow, int E,
-                                                  int32_t* ids_out, float* w_out) {
-  float sv[K];
-  int si[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) { sv[j] = -INFINITY; si[j] = 0x7fffffff; }
-  for (int e0 = 0; e0 < E; e0 += 16) {
-    float4 v4[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      v4[c] = (e0 + 4 * c < E) ? reinterpret_cast<const float4*>(lrow + e0)[c]
-                               : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float4& q = v4[i >> 2];
-      const float v = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
-      const int id = e0 + i;
-      if (id < E && v > sv[K - 1]) {
-        sv[K - 1] = v;
-        si[K - 1] = id;
-#pragma unroll
-        for (int j = K - 1; j > 0; --j) {
-          if (sv[j] > sv[j - 1]) {
-            const float tv = sv[j]; sv[j] = sv[j - 1]; sv[j - 1] = tv;
-            const int ti = si[j]; si[j] = si[j - 1]; si[j - 1] = ti;
-          }
-        }
-      }
-    }
-  }
-  float ex[K], sum = 0.f;
-#pragma unroll
-  for (int j = 0; j < K; ++j) { ex[j] = expf(sv[j] - sv[0]); sum += ex[j]; }
-  // ascending ids (odd-even transposition sort, K passes)
-#pragma unroll
-  for (int pass = 0; pass < K; ++pass)
-#pragma unroll
-    for (int j = pass & 1; j + 1 < K; j += 2)
-      if (si[j] > si[j + 1]) {
-        const int ti = si[j]; si[j] = si[j + 1]; si[j + 1] = ti;
-        const float te = ex[j]; ex[j] = ex[j + 1]; ex[j + 1] = te;
-      }
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    ids_out[j] = si[j];
-    w_out[j] = ex[j] / sum;
-  }
-}
-
 template <int K>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int T,
                                                           int E, int32_t* __restrict__ topk_ids,
@@ -422,6 +367,8 @@ __global__ __launch_bounds__(kPermWaves * 64) void moe_permute_kernel(
 // workgroup -- one launch instead of two.
 constexpr int kFusedMaxAssign = 4096;
 
+constexpr int kStagedLogits = 8192;  // floats of logits staged in LDS (T * (E + 4) <= this)
+
 template <int K>
 __global__ __launch_bounds__(kPermWaves * 64) void moe_topk_permute_kernel(
     const float* __restrict__ logits, int T, int E, int32_t* __restrict__ topk_ids,
@@ -430,8 +377,27 @@ __global__ __launch_bounds__(kPermWaves * 64) void moe_topk_permute_kernel(
   __shared__ int32_t cnt[kPermWaves][256];
   __shared__ int32_t off[256];
   __shared__ int32_t ids_s[kFusedMaxAssign];
-  for (int t = threadIdx.x; t < T; t += kPermWaves * 64)
-    topk_softmax_lane<K>(logits + (size_t)t * E, E, ids_s + t * K, topk_w + (size_t)t * K);
+  __shared__ __align__(16) float lg_s[kStagedLogits];
+  // one lane per token (a wave selects for 64 tokens at once); small batches first stage all logits
+  // in LDS with coalesced loads (rows padded by 16 bytes), so the selection never waits on memory
+  const bool staged = T * (E + 4) <= kStagedLogits;
+  if (staged) {
+    for (int i = threadIdx.x; i < T * E; i += kPermWaves * 64) lg_s[(i / E) * (E + 4) + i % E] = logits[i];
+    __syncthreads();
+  }
+  if (staged && E % 16 == 0) {
+    // four lanes per token: 256 tokens per pass of the workgroup
+    const int sub = threadIdx.x & 3;
+    for (int t0 = 0; t0 < T; t0 += kPermWaves * 16) {
+      const int t = t0 + (threadIdx.x >> 2);
+      // whole quads stay together (T rounds the quad index, never splits one)
+      if (t < T) topk_softmax_quad<K>(lg_s + t * (E + 4), E, sub, ids_s + t * K, topk_w + (size_t)t * K);
+    }
+  } else {
+    for (int t = threadIdx.x; t < T; t += kPermWaves * 64)
+      topk_softmax_lane<K>(staged ? lg_s + t * (E + 4) : logits + (size_t)t * E, E, ids_s + t * K,
+                           topk_w + (size_t)t * K);
+  }
   __syncthreads();
   for (int i = threadIdx.x; i < T * K; i += kPermWaves * 64) topk_ids[i] = ids_s[i];
   permute_block(ids_s, T * K, E, hist_out, off_out, perm, inv, cnt, off);
@@ -460,6 +426,25 @@ int launch_route_permute(const uint16_t* x, const uint16_t* w, const uint16_t* b
   else if (k == 2)
     hipLaunchKernelGGL(moe_topk_permute_kernel<2>, dim3(1), dim3(kPermWaves * 64), 0, s, logits, T, E,
                        ids, wts, hist, offsets, perm, inv);
+  else
+    return set_error(FLYAI_EINVAL, "route: top_k must be 2, 4 or 8");
+  return check_launch("moe_topk_permute");
+}
+
+// Top-k + softmax of precomputed logits, then histogram / permute (T*k <= 4096: one workgroup).
+int launch_topk_permute(const float* logits, int T, int E, int k, int32_t* ids, float* wts, int32_t* hist,
+                        int32_t* offsets, int32_t* perm, int32_t* inv, hipStream_t s) {
+  if (T == 0) return FLYAI_OK;
+  if ((int64_t)T * k > kFusedMaxAssign) return set_error(FLYAI_EINVAL, "topk_permute: T*k > %d", kFusedMaxAssign);
+  if (k == 4)
+    hipLaunchKernelGGL(moe_topk_permute_kernel<4>, dim3(1), dim3(kPermWaves * 64), 0, s, logits, T, E, ids,
+                       wts, hist, offsets, perm, inv);
+  else if (k == 8)
+    hipLaunchKernelGGL(moe_topk_permute_kernel<8>, dim3(1), dim3(kPermWaves * 64), 0, s, logits, T, E, ids,
+                       wts, hist, offsets, perm, inv);
+  else if (k == 2)
+    hipLaunchKernelGGL(moe_topk_permute_kernel<2>, dim3(1), dim3(kPermWaves * 64), 0, s, logits, T, E, ids,
+                       wts, hist, offsets, perm, inv);
   else
     return set_error(FLYAI_EINVAL, "route: top_k must be 2, 4 or 8");
   return check_launch("moe_topk_permute");

@@ -118,6 +118,23 @@ def test_fused_route_permute_bit_exact(T, E, H):
         assert np.array_equal(got.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("T,E,k", [(20, 128, 4), (56, 128, 8), (7, 64, 2)])
+def test_fused_route_permute_ties_go_to_lower_id(T, E, k):
+    """Zero router weights leave logits = bias; a bias with many equal values makes ties inside a
+    lane's quarter and across the four lanes that share a token.  Bit-exact ids and weights."""
+    from flyai_amd import ops
+    x = _rms_input(T, 2880, 15)
+    w = torch.zeros(E, 2880, device=DEV, dtype=torch.bfloat16)
+    b = torch.tensor([((e * 7) % 5) * 0.125 for e in range(E)], device=DEV).to(torch.bfloat16)
+    ids, wts, hist, off, perm, inv = ops.moe_route_permute(x, w, b, k)
+    rids, rw, _ = oroute.gptoss_route(x.float().cpu(), w.float().cpu(), b.float().cpu(), k)
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    np.testing.assert_allclose(wts.cpu().numpy(), rw, rtol=2e-6, atol=1e-7)
+    rh, ro, rp, ri = oroute.permute(rids, E)
+    for got, ref in ((hist, rh), (off, ro), (perm, rp), (inv, ri)):
+        assert np.array_equal(got.cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("T,k,E,mode", [(1, 4, 128, "rand"), (56, 4, 128, "rand"), (2096, 4, 128, "rand"),
                                         (4096, 4, 256, "skew"), (64, 4, 8, "one"), (16384, 4, 128, "rand")])
 def test_permute_bit_exact(T, k, E, mode):

@@ -65,7 +65,7 @@ class RaggedStage:
     """One pipeline stage of GPT-OSS decoder layers on libflyai_stage."""
 
     def __init__(self, shape: GptOssShape, layers, rotary, kv: KVWorkspace, max_tokens, max_seqs,
-                 max_attn_items=None, split_keys=512, device="cuda"):
+                 max_attn_items=None, split_keys=1024, device="cuda"):
         self.shape, self.layers, self.rotary, self.kv = shape, layers, rotary, kv
         self.device = torch.device(device)
         self.max_tokens, self.max_seqs = max_tokens, max_seqs

@@ -78,11 +78,25 @@ __global__ __launch_bounds__(256) void gemm_splitk_bf16_kernel(
   for (int m0 = 0; m0 < M; m0 += kGemmRows) {
     const int rows = min(kGemmRows, M - m0);
     __syncthreads();
-    for (int i = threadIdx.x; i < kGemmRows * kKQW * 16; i += 256) {
-      const int row = i / (kKQW * 16), v = i % (kKQW * 16);
-      const int k = 128 * kq0 + 8 * v;
-      as[row][v] = (row < rows && k < K) ? *reinterpret_cast<const uint4*>(x + (size_t)(m0 + row) * K + k)
-                                         : make_uint4(0, 0, 0, 0);
+    // the slice of A goes to LDS with loads batched 8 per thread (one round trip per batch);
+    // rows past the pass and K past the row end are stored as zero
+    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+    for (int b0 = 0; b0 < kGemmRows * kKQW * 16; b0 += 8 * 256) {
+      u32x4 v8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = b0 + j * 256 + (int)threadIdx.x;
+        const int row = i / (kKQW * 16), v = i % (kKQW * 16);
+        const int k = 128 * kq0 + 8 * v;
+        const bool ok = row < rows && k < K;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(x + (ok ? (size_t)(m0 + row) * K + k : 0));
+        v8[j] = ok ? val : u32x4{0u, 0u, 0u, 0u};
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = b0 + j * 256 + (int)threadIdx.x;
+        *reinterpret_cast<u32x4*>(&as[i / (kKQW * 16)][i % (kKQW * 16)]) = v8[j];
+      }
     }
     __syncthreads();
     if (!nval) continue;

@@ -125,12 +125,25 @@ __global__ __launch_bounds__(256) void moe_mxfp4_kernel(
   for (int m0 = 0; m0 < n_e; m0 += kRowsPerPass) {
     const int rows = min(kRowsPerPass, n_e - m0);
     __syncthreads();  // the previous pass is done with the LDS rows
-    for (int i = threadIdx.x; i < rows * row_vecs; i += 256) {
-      const int rr = i / row_vecs, v = i % row_vecs;
-      const int p = row_lo + m0 + rr;
-      const int src = GATE_UP ? perm[p] / k_top : p;
-      *reinterpret_cast<uint4*>(const_cast<char*>(lds) + rr * row_bytes + v * 16) =
-          reinterpret_cast<const uint4*>(act + (size_t)src * K)[v];
+    // staging loads go out in batches of 4 per thread (one round trip per batch, not per vector);
+    // indices past the end are clamped for the load and not stored
+    const int total = rows * row_vecs;
+    for (int b0 = 0; b0 < total; b0 += 4 * 256) {
+      u32x4_t v4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = min(b0 + j * 256 + (int)threadIdx.x, total - 1);
+        const int rr = i / row_vecs, v = i % row_vecs;
+        const int p = row_lo + m0 + rr;
+        const int src = GATE_UP ? perm[p] / k_top : p;
+        v4[j] = reinterpret_cast<const u32x4_t*>(act + (size_t)src * K)[v];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int i = b0 + j * 256 + (int)threadIdx.x;
+        if (i < total)
+          *reinterpret_cast<u32x4_t*>(const_cast<char*>(lds) + (i / row_vecs) * row_bytes + (i % row_vecs) * 16) = v4[j];
+      }
     }
     __syncthreads();
     if (ntw == 0) continue;

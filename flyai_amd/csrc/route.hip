@@ -30,10 +30,22 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
                                         : make_uint4(0, 0, 0, 0);
     }
   const int vecs = H / 8;
-  for (int i = tid; i < TT * vecs; i += 256) {
-    const int t = i / vecs, v = i % vecs;
-    reinterpret_cast<uint4*>(xs + t * H)[v] =
-        t < nt ? reinterpret_cast<const uint4*>(x + (size_t)(t0 + t) * H)[v] : make_uint4(0, 0, 0, 0);
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  for (int b0 = 0; b0 < TT * vecs; b0 += 4 * 256) {  // loads batched 4 per thread
+    u32x4 v4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = b0 + j * 256 + tid;
+      const int t = i / vecs, v = i % vecs;
+      const bool ok = i < TT * vecs && t < nt;
+      const u32x4 val = reinterpret_cast<const u32x4*>(x + (ok ? (size_t)(t0 + t) * H : 0))[ok ? v : 0];
+      v4[j] = ok ? val : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = b0 + j * 256 + tid;
+      if (i < TT * vecs) reinterpret_cast<u32x4*>(xs + (i / vecs) * H)[i % vecs] = v4[j];
+    }
   }
   __syncthreads();
   float acc[EPW][TT];

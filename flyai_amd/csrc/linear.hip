@@ -378,6 +378,74 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(
   }
 }
 
+// The stage's QKV finalize + RoPE + K/V append from the split-K partials, vectorised: each thread
+// takes four rotary pairs of one head (features d0..d0+3 and d0+D/2..+3) or four V dims, sums the
+// NS-bounded slices with float4 loads all issued before the first add (same slice order and
+// per-op bf16 rounding as rope_kv_append_kernel<true>), and writes its q, K or transposed V values.
+template <int NS>
+__global__ __launch_bounds__(256) void qkv_rope_kv_vec_kernel(
+    const float* __restrict__ part, int slices, int M, const uint16_t* __restrict__ bias,
+    const int32_t* __restrict__ positions, const int32_t* __restrict__ seq_id,
+    const uint16_t* __restrict__ cos_tab, const uint16_t* __restrict__ sin_tab, int rope_positions,
+    int Hq, int Hkv, int D, const int64_t* __restrict__ kv_base, const int32_t* __restrict__ kv_cap,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool) {
+  const int t = blockIdx.x;
+  const int u = blockIdx.y * blockDim.x + threadIdx.x;
+  const int D2 = D / 2, Q2 = D2 / 4, QV = D / 4;
+  const int rot_units = (Hq + Hkv) * Q2;
+  if (u >= rot_units + Hkv * QV) return;
+  const int pos = positions[t];
+  if (pos < 0 || pos >= rope_positions) return;  // outside the rotary table: no read, no write
+  const int b = seq_id[t];
+  const int cap = kv_cap[b];
+  const bool in_cap = pos < cap;
+  const int64_t base = kv_base[b];
+  const int width = (Hq + 2 * Hkv) * D;
+  const size_t stride = (size_t)M * width;
+  const float* row = part + (size_t)t * width;
+  auto sum4 = [&](int f, float (&o)[4]) __attribute__((always_inline)) {
+    float4 v[NS];
+#pragma unroll
+    for (int i = 0; i < NS; ++i)
+      v[i] = i < slices ? *reinterpret_cast<const float4*>(row + i * stride + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 a = v[0];
+#pragma unroll
+    for (int i = 1; i < NS; ++i)
+      if (i < slices) { a.x += v[i].x; a.y += v[i].y; a.z += v[i].z; a.w += v[i].w; }
+    const float av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = bf16_round(av[j] + (bias ? bf2f(bias[f + j]) : 0.f));
+  };
+  if (u < rot_units) {
+    const int h = u / Q2, d0 = (u % Q2) * 4;
+    if (h >= Hq && !in_cap) return;
+    float x1[4], x2[4];
+    sum4(h * D + d0, x1);
+    sum4(h * D + d0 + D2, x2);
+    const uint16_t* cr = cos_tab + (size_t)pos * D2 + d0;
+    const uint16_t* sr = sin_tab + (size_t)pos * D2 + d0;
+    uint16_t first[4], second[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float c = bf2f(cr[j]), sn = bf2f(sr[j]);
+      first[j] = f2bf(bf16_round(bf16_round(x1[j] * c) - bf16_round(x2[j] * sn)));
+      second[j] = f2bf(bf16_round(bf16_round(x2[j] * c) + bf16_round(x1[j] * sn)));
+    }
+    uint16_t* dst = h < Hq ? q_out + ((size_t)t * Hq + h) * D
+                           : k_pool + base + ((size_t)(h - Hq) * cap + pos) * D;
+    *reinterpret_cast<uint2*>(dst + d0) = make_uint2(first[0] | ((uint32_t)first[1] << 16),
+                                                     first[2] | ((uint32_t)first[3] << 16));
+    *reinterpret_cast<uint2*>(dst + d0 + D2) = make_uint2(second[0] | ((uint32_t)second[1] << 16),
+                                                          second[2] | ((uint32_t)second[3] << 16));
+  } else if (in_cap) {
+    const int v = u - rot_units, gv = v / QV, d0 = (v % QV) * 4;
+    float o[4];
+    sum4((Hq + Hkv) * D + gv * D + d0, o);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v_pool[base + ((size_t)gv * D + d0 + j) * cap + pos] = f2bf(o[j]);
+  }
+}
+
 int launch_rope_kv(const uint16_t* qkv, const int32_t* positions, const int32_t* seq_id,
                    const uint16_t* cos_tab, const uint16_t* sin_tab, int rope_positions, int T,
                    int Hq, int Hkv, int D, const int64_t* kv_base, const int32_t* kv_cap,
@@ -399,9 +467,23 @@ int launch_qkv_rope_kv(const uint16_t* x, const uint16_t* Wqkv, const uint16_t* 
   const int width = (Hq + 2 * Hkv) * D;
   int rc = launch_gemm_splitk(x, Wqkv, T, width, H, part, s);
   if (rc) return rc;
-  hipLaunchKernelGGL(rope_kv_append_kernel<true>, dim3(T, 4), dim3(256), 0, s, nullptr, part,
-                     gemm_slices(H), T, bqkv, positions, seq_id, cos_tab, sin_tab, rope_positions, Hq,
-                     Hkv, D, kv_base, kv_cap, q_out, k_pool, v_pool);
+  const int slices = gemm_slices(H);
+  if (D % 8 == 0 && slices <= 16) {
+    const int units = (Hq + Hkv) * (D / 8) + Hkv * (D / 4);
+    const dim3 grid(T, ceil_div(units, 256));
+    if (slices <= 8)
+      hipLaunchKernelGGL(qkv_rope_kv_vec_kernel<8>, grid, dim3(256), 0, s, part, slices, T, bqkv, positions,
+                         seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base, kv_cap, q_out,
+                         k_pool, v_pool);
+    else
+      hipLaunchKernelGGL(qkv_rope_kv_vec_kernel<16>, grid, dim3(256), 0, s, part, slices, T, bqkv, positions,
+                         seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base, kv_cap, q_out,
+                         k_pool, v_pool);
+  } else {
+    hipLaunchKernelGGL(rope_kv_append_kernel<true>, dim3(T, 4), dim3(256), 0, s, nullptr, part, slices, T,
+                       bqkv, positions, seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base,
+                       kv_cap, q_out, k_pool, v_pool);
+  }
   return check_launch("qkv_rope_kv_append");
 }
 

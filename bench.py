@@ -65,7 +65,7 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after timing, copy a buffer of this many MiB 3 times (a known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
-    ap.add_argument("--workload", choices=("c1", "c3"), default="c1")
+    ap.add_argument("--workload", choices=("c1", "c2", "c3"), default="c1")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -74,7 +74,7 @@ def main():
     if args.workload == "c3":
         run_c3(args)
     else:
-        run_c1(args)
+        run_gptoss(args, chunked_prefill=args.workload == "c2")
 
 
 def copy_probe(mib, dev):
@@ -87,7 +87,13 @@ def copy_probe(mib, dev):
         torch.cuda.synchronize()
 
 
-def run_c1(args):
+def c2_batch(seed=0):
+    """One 2048-token prefill chunk at prior KV 4096 plus 48 single-token decode rows."""
+    rng = np.random.default_rng(seed)
+    return [2048] + [1] * 48, [4096] + [int(v) for v in rng.integers(512, 8192 + 1, size=48)]
+
+
+def run_gptoss(args, chunked_prefill=False):
     import torch
     from flyai_amd import ops
     from flyai_amd.rope import YarnRotary
@@ -97,11 +103,12 @@ def run_c1(args):
     dev = "cuda"
     torch.cuda.set_device(0)
     shape = GptOssShape()
-    q_lens, starts = c1_batch(0)
+    q_lens, starts = c2_batch(0) if chunked_prefill else c1_batch(0)
     S, T = len(q_lens), sum(q_lens)
     maxlen = 8192 + 64
+    with_cpu = not args.no_cpu and not chunked_prefill
     print(f"[bench] building {args.layers}-layer stage ...", file=sys.stderr, flush=True)
-    layers = [synthetic_layer(shape, 1000 + i, dev, sliding=(i % 2 == 0), keep_hf=(i == 1 and not args.no_cpu))
+    layers = [synthetic_layer(shape, 1000 + i, dev, sliding=(i % 2 == 0), keep_hf=(i == 1 and with_cpu))
               for i in range(args.layers)]
     rot = YarnRotary(maxlen, device=dev)
     kv = KVWorkspace(args.layers, S, maxlen, shape.n_kv_heads, shape.head_dim, dev)
@@ -110,7 +117,7 @@ def run_c1(args):
     for t in kv.k + kv.v:
         t.copy_(torch.randn(t.shape, device=dev, generator=g).to(torch.bfloat16))
     hidden0 = torch.randn(T, shape.hidden, device=dev, generator=g).to(torch.bfloat16)
-    stage = RaggedStage(shape, layers, rot, kv, max_tokens=64, max_seqs=S)
+    stage = RaggedStage(shape, layers, rot, kv, max_tokens=max(64, T), max_seqs=S)
     slots = list(range(S))
     torch.cuda.synchronize()
     print("[bench] warmup", file=sys.stderr, flush=True)
@@ -163,8 +170,34 @@ def run_c1(args):
     copy_probe(args.copy_probe_mib, dev)
 
     cpu = None
-    if not args.no_cpu:
+    if with_cpu:
         cpu = cpu_baseline(layers[1], kv, 1, hidden0, q_lens, starts, slots, shape, maxlen, args.layers)
+
+    if chunked_prefill:
+        # dense groups (~65 rows per expert): the gate_up GEMM against the bf16 MFMA peak
+        P = T * shape.top_k
+        flops = 2.0 * P * shape.hidden * 2 * shape.intermediate
+        tflops = flops / (gu_us * 1e-6) / 1e12
+        line = {
+            "metric": "stage tokens/sec at a chunked-prefill mixed batch; MoE layer us; % MFMA roofline",
+            "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4-e2m1/bf16 (fp32 accumulate)",
+            "data": "synthetic (seeded random-init weights, N(0,1) KV and activations)",
+            "config": {"workload": "gpt-oss-120b-shaped 9-layer MXFP4 stage, one 2048-token prefill chunk "
+                                   "(prior KV 4096) + 48 decode rows (KV 512-8192)",
+                       "layers": args.layers, "tokens": T, "sequences": S, "experts": shape.n_experts,
+                       "top_k": shape.top_k, "hidden": shape.hidden, "parallelism": "single GPU"},
+            "moe_layer_us": round(gu_us + dn_us, 2),
+            "roofline": {"bound": "mfma", "kernel": "moe_mxfp4_dense_kernel<gate_up>", "achieved": round(tflops, 1),
+                         "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                         "algorithmic_flops": flops, "avg_us": round(gu_us, 2), "hbm_GB/s": round(gu_gbs, 1)},
+            "kernels": {"moe_down": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),
+                                     "TFLOP/s": round(flops / 2 / (dn_us * 1e-6) / 1e12, 1)}},
+            "cpu_baseline": None,
+        }
+        print(json.dumps(line))
+        return
 
     line = {
         "metric": "stage tokens/sec at ragged batch 32; MoE layer us; % HBM/MFMA roofline",

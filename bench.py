@@ -189,7 +189,7 @@ def run_gptoss(args, chunked_prefill=False):
                        "layers": args.layers, "tokens": T, "sequences": S, "experts": shape.n_experts,
                        "top_k": shape.top_k, "hidden": shape.hidden, "parallelism": "single GPU"},
             "moe_layer_us": round(gu_us + dn_us, 2),
-            "roofline": {"bound": "mfma", "kernel": "moe_mxfp4_dense_kernel<gate_up>", "achieved": round(tflops, 1),
+            "roofline": {"bound": "mfma", "kernel": "moe_mxfp4_gemm_kernel<gate_up>", "achieved": round(tflops, 1),
                          "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
                          "algorithmic_flops": flops, "avg_us": round(gu_us, 2), "hbm_GB/s": round(gu_gbs, 1)},
             "kernels": {"moe_down": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),

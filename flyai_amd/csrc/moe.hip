@@ -229,16 +229,7 @@ __global__ __launch_bounds__(256) void moe_mxfp4_kernel(
 
 constexpr int kNTW = 2;  // weight tiles per wave
 
-// ---- dense groups ------------------------------------------------------------------------------
-// Groups of many rows (chunked prefill, skewed routing) take MT row tiles per pass so the expert's
-// weights stream once per MT*16 rows: one weight tile per wave, the same 4-deep non-temporal ring
-// and scale prefetch as above, and the bf16 activation rows staged in LDS one 128-K group at a
-// time.  The staging loads of group c+1 are issued into registers before group c's ring loads
-// (vector-memory waits complete in issue order, so a later wait on them never drains the ring) and
-// stored at the next group boundary.  Loads are unconditional with clamped addresses: weight lanes
-// past the last block of a row are zeroed by select, activation loads past the row end read a
-// valid element of the row (multiplied by those zero weights); rows past the pass read row 0 and
-// are never stored.
+// compile-time loop: f(integral_constant<int, B>) ... f(integral_constant<int, N-1>)
 template <int B, int N, class F>
 __device__ __forceinline__ void mx_static_for(F&& f) {
   if constexpr (B < N) {
@@ -247,150 +238,364 @@ __device__ __forceinline__ void mx_static_for(F&& f) {
   }
 }
 
-template <bool GATE_UP, int MT>
-__global__ __launch_bounds__(256) void moe_mxfp4_dense_kernel(
-    const uint16_t* __restrict__ act, const int32_t* __restrict__ perm,
-    const int32_t* __restrict__ offsets, int k_top, const uint8_t* __restrict__ packed,
-    const float* __restrict__ bias, int E, int N, int K, int min_rows, void* __restrict__ out) {
-  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  extern __shared__ uint4 xd_lds[];
-  constexpr int KC = 256;                    // bytes of a bf16 row per chunk: one group of 128 K
-  constexpr int ROWB = KC + 16;              // padded LDS row
-  constexpr int VPR = KC / 16;               // 16-byte vectors per row chunk
-  constexpr int SREG = MT * 16 * VPR / 256;  // staging vectors per thread
-  const MxGeom gm = mx_geom(E, N, K);
-  const int wg_per_e = (gm.NT + 3) / 4;
-  const int e = blockIdx.x / wg_per_e;
-  const int wgi = blockIdx.x % wg_per_e;
-  const int row_lo = offsets[e];
-  const int n_e = offsets[e + 1] - row_lo;
-  if (n_e <= 0 || n_e < min_rows) return;  // uniform over the workgroup
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nt = wgi * 4 + wave;
-  const bool has_tile = nt < gm.NT;         // waves past the last tile still join the barriers
-  const int ntc = min(nt, gm.NT - 1);
-  const int r = lane & 15, g = lane >> 4;
-  char* lds = reinterpret_cast<char*>(xd_lds);
-  const uint8_t* data = packed + ((size_t)e * gm.NT + ntc) * gm.G * 256 + lane * 16;
-  const uint32_t* scl = reinterpret_cast<const uint32_t*>(packed + gm.data_bytes + ((size_t)e * gm.NT + ntc) * gm.KG4 * 256) + lane;
+// ---- dense groups as a tiled GEMM ----------------------------------------------------------------
+// For groups of many rows the weights are still read once from HBM, but each weight byte now feeds
+// up to 96 rows, so the kernel must keep HBM busy and the MFMA pipes busy at the same time.
+// A workgroup of 8 waves (2 per SIMD, the CU's whole LDS) computes, for one expert and 96 of its
+// rows, a chunk of consecutive 256-row weight blocks (16 packed tiles each); wave w owns tiles
+// 2w, 2w+1 of the block and all 6 row tiles (12 accumulators; every A fragment feeds 2 MFMAs,
+// every B fragment 6).  The blocks of a chunk share the activation rows, so the load pipeline runs
+// on across block boundaries and a workgroup's start-up latency (index loads, pipeline fill) is
+// paid once per chunk, not once per block.  K advances one 128-K group at a time:
+//  * the weights (1 KiB per tile and group) go global -> registers through a 4-deep ring, each wave
+//    loading only its own tiles, as the memory-bound kernels do: registers hold far more bytes in
+//    flight than LDS could;
+//  * the activation rows (shared by all 8 waves) and the weight scales go global -> LDS directly
+//    (global_load_lds) through 4 stages of 28 KiB; a group's loads are issued 3 groups ahead;
+//  * activations sit in LDS in MFMA-fragment order: the 1 KiB block (m, j) holds, at 16*lane, the
+//    8 values lane (g, r) = (lane / 16, lane % 16) feeds to step j of row tile m (row 16m + r,
+//    K = 32g + 8j of the group).  The direct-to-LDS loads gather each lane's 16 bytes from its row,
+//    and every fragment read is one contiguous 1 KiB: ds_read_b128 runs conflict-free only for
+//    lane-contiguous addresses (16 rows at any stride, padded or XOR-swizzled, cost 2x);
+//  * the stages are separate LDS arrays with compile-time stage numbers, so the compiler can tell
+//    a stage's reads from the asynchronous writes into the other stages; each stage is waited for
+//    with an explicit vmcnt that leaves the 2 younger groups' loads in flight (vector-memory loads
+//    complete in issue order, so within a group the register loads go out before the LDS ones),
+//    and the barrier is a bare s_barrier after the wave's own LDS reads (__syncthreads() would
+//    also wait for every outstanding global load);
+//  * a group is 4 MFMA steps of 32 K; the LDS reads and fp4 conversions of step j+1 are issued
+//    under the 12 MFMAs of step j (operands are double-buffered in registers, never copied), and
+//    the barrier that hands over the next stage sits before the last step, so the next group's
+//    first reads hide under that step's MFMAs;
+//  * packed MXFP4 is dequantised per wave (v_cvt_scalef32_pk_bf16_fp4) right before its MFMAs.
+// Each block runs its K groups padded to a multiple of 4, so blocks start on stage 0 and the
+// 4-way unrolled group loop is straight-line; a block's outputs are written after its last group.
+// Loads are unconditional with clamped addresses: rows past the group read row 0 and are never
+// stored; weight lanes past a row's last block (and the padding groups) are zeroed before
+// conversion, their activation slots read the row's first group (finite values); tiles past N
+// compute on a clamped tile and are never stored; the 3 groups issued past the chunk's end read
+// clamped addresses and are never computed on.
+constexpr int kGemmTiles = 16;                       // packed 16-row weight tiles per block
+constexpr int kGemmRows = 96;                        // group rows per pass
+constexpr int kGemmStage = kGemmRows * 256 + kGemmTiles * 256;  // activations + scale dwords
+constexpr int kGemmStages = 4;
 
-  for (int m0 = 0; m0 < n_e; m0 += MT * 16) {
-    const int rows = min(MT * 16, n_e - m0);
-    const uint16_t* asrc[SREG];
-    int acol[SREG];
-    mx_static_for<0, SREG>([&](auto J) {
-      const int i = J * 256 + tid;
-      const int rr = i / VPR;
-      const int p = row_lo + m0 + (rr < rows ? rr : 0);
-      asrc[J] = act + (size_t)(GATE_UP ? perm[p] / k_top : p) * K;
-      acol[J] = (i % VPR) * 8;   // element offset within the chunk
+// s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);
+
+// workgroup barrier that waits only for the wave's own LDS operations (global loads stay in flight)
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// instruction classes for __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedValu = 0x2, kSchedMfma = 0x8, kSchedVmem = 0x10, kSchedDsRead = 0x100;
+
+// value of lane ^ 1 (DPP quad permutation [1, 0, 3, 2]; no LDS traffic)
+__device__ __forceinline__ float lane_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+
+// what one workgroup of the tiled GEMM works on: an expert, its rows, a chunk of weight blocks
+struct GemmCtx {
+  const uint16_t* act;
+  const int32_t* perm;
+  const float* bias;
+  void* out;
+  const uint8_t* wbase;  // the expert's packed tiles, + lane * 16
+  const uint8_t* sbase;  // the expert's scale rows, + lane * 4
+  MxGeom gm;
+  size_t tile_bytes;
+  int k_top, N, K, e, nb0, nbn, row_lo, lane, wave, r, g;
+};
+
+// One pass over MT row tiles (16*MT rows from m0) and every block of the chunk.
+template <bool GATE_UP, int MT>
+__device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmStage], char (&st1)[kGemmStage],
+                                          char (&st2)[kGemmStage], char (&st3)[kGemmStage], int m0, int rows) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  static_assert(MT % 2 == 0 && MT <= 6, "row tiles per pass");
+  constexpr int ABYTES = MT * 4096;                   // activation part of a stage
+  constexpr int LOADS = 2 + 2 + MT / 2;               // weight tiles, scale rows, activation blocks
+  constexpr int WAIT = (kGemmStages - 2) * LOADS;     // loads younger than the stage waited for
+  const MxGeom& gm = c.gm;
+  const int lane = c.lane, wave = c.wave, r = c.r, g = c.g;
+  const int sfrag_off = ABYTES + 2 * wave * 256 + lane * 4;
+  // this wave's tile n of chunk block nb (clamped into the expert)
+  auto tile_of = [&](int nb, int n) __attribute__((always_inline)) {
+    return min((c.nb0 + nb) * kGemmTiles + 2 * wave + n, gm.NT - 1);
+  };
+  const int KGP = (gm.KG + kGemmStages - 1) / kGemmStages * kGemmStages;  // groups per block, padded
+
+  // activation DMA: instruction J fills fragment block b = J*8 + wave, i.e. row tile b / 4, step
+  // b % 4: the lane fetches row 16*(b/4) + r, elements 8*(4g + b%4) .. +7 of the group
+  const uint16_t* arow[MT / 2];
+#pragma unroll
+  for (int J = 0; J < MT / 2; ++J) {
+    const int b = J * 8 + wave;
+    const int row = (b >> 2) * 16 + r;
+    const int p = c.row_lo + m0 + (row < rows ? row : 0);
+    arow[J] = c.act + (size_t)(GATE_UP ? c.perm[p] / c.k_top : p) * c.K + (4 * g + (b & 3)) * 8;
+  }
+  // the next group to load: block i_nb of the chunk (past the end: the last block), group i_kg
+  int i_nb = 0, i_kg = 0;
+  // the loads of that group: weights into the ring slot, then scales and activations into the
+  // stage; advances the position
+  auto issue = [&](u32x4 (&bq)[2], char* stage) __attribute__((always_inline)) {
+    const int nb = min(i_nb, c.nbn - 1), kg = i_kg;
+    const bool blk = 4 * kg + g < gm.G;  // the lane's block of the group exists
+    const size_t woff = blk ? (size_t)kg * 1024 : 0;
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+      bq[n] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(c.wbase + (size_t)tile_of(nb, n) * c.tile_bytes + woff));
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+      __builtin_amdgcn_global_load_lds((const void*)(c.sbase + ((size_t)tile_of(nb, n) * gm.KG4 + min(kg / 4, gm.KG4 - 1)) * 256),
+                                       (lds_ptr)(stage + ABYTES + (2 * wave + n) * 256), 4, 0, 0);
+    const int col = blk ? kg * 128 : 0;
+#pragma unroll
+    for (int J = 0; J < MT / 2; ++J)
+      __builtin_amdgcn_global_load_lds((const void*)(arow[J] + col), (lds_ptr)(stage + (J * 8 + wave) * 1024), 16, 0, 0);
+    if (++i_kg == KGP) {
+      i_kg = 0;
+      ++i_nb;
+    }
+  };
+  f32x4_t acc[MT][2];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) acc[m][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  zero_acc();
+
+  // double-buffered step operands (x0 / x1), the weight ring, the current group's scales
+  bf16x8_t a0[MT], a1[MT], b0[2], b1[2];
+  u32x4 w0[2], w1[2], w2[2], w3[2];
+  float scale[2];
+  bool bok = false;
+  auto read_scales = [&](const char* stage, int kg) __attribute__((always_inline)) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const uint32_t sw = *reinterpret_cast<const uint32_t*>(stage + sfrag_off + n * 256);
+      scale[n] = e8m0_operand((sw >> (8 * (kg & 3))) & 0xffu);
+    }
+    bok = 4 * kg + g < gm.G;  // the lane's weight block exists
+  };
+  auto read_a = [&](bf16x8_t (&a)[MT], const char* stage, auto j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m) a[m] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + (4 * m + j) * 1024 + lane * 16));
+  };
+  auto cvt = [&](bf16x8_t (&b)[2], const u32x4 (&bq)[2], auto j) __attribute__((always_inline)) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) b[n] = fp4x8_to_bf16x8(bok ? bq[n][int(j)] : 0u, scale[n]);
+  };
+  auto mfma_step = [&](const bf16x8_t (&a)[MT], const bf16x8_t (&b)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) acc[m][n] = mfma16x16x32(a[m], b[n], acc[m][n]);
+  };
+  // 2*MT MFMAs with the next step's MT reads going out early and its 8 conversions spread after
+  auto sched_step = [&]() __attribute__((always_inline)) {
+    mx_static_for<0, MT>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
     });
-    auto stage_load = [&](u32x4 (&st)[SREG], int c) __attribute__((always_inline)) {
-      mx_static_for<0, SREG>([&](auto J) {
-        const int col = c * 128 + acol[J];
-        st[J] = *reinterpret_cast<const u32x4*>(asrc[J] + (col < K ? col : acol[J]));
-      });
-    };
-    u32x4 stg[SREG];
-    stage_load(stg, 0);
-    auto next_chunk = [&](int c) __attribute__((always_inline)) {
-      __syncthreads();  // every wave is done with the previous chunk
-      mx_static_for<0, SREG>([&](auto J) {
-        const int i = J * 256 + tid;
-        *reinterpret_cast<u32x4*>(lds + (i / VPR) * ROWB + (i % VPR) * 16) = stg[J];
-      });
-      __syncthreads();
-      if (c + 1 < gm.KG) stage_load(stg, c + 1);
-    };
-    auto load_w = [&](int kg) __attribute__((always_inline)) -> uint4 {
-      // lanes past the row's last block (and look-ahead past K) load group 0 and are zeroed
-      const bool ok = kg < gm.KG && 4 * kg + g < gm.G;
-      const uint4 v = ld_nt(data + (ok ? (size_t)kg * 1024 : 0));
-      return ok ? v : make_uint4(0, 0, 0, 0);
-    };
-    auto load_sc = [&](int kg4) __attribute__((always_inline)) -> uint32_t {
-      return scl[min(kg4, gm.KG4 - 1) * 64];
-    };
-    f32x4_t acc[MT];
+    mx_static_for<0, MT>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // bias of this wave's two columns of chunk block nb
+  float bsum[2];
+  auto load_bias = [&](int nb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    auto compute = [&](uint4 w, uint32_t sc, int b) __attribute__((always_inline)) {
-      const float scale = e8m0_operand((sc >> (8 * b)) & 0xffu);
-      const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-      bf16x8_t bw[4];
+    for (int n = 0; n < 2; ++n) bsum[n] = c.bias[(size_t)c.e * c.N + tile_of(min(nb, c.nbn - 1), n) * 16 + r];
+  };
+  // acc[m][n][v] = D[group row 16m + 4g + v][feature (block tile 2*wave + n) * 16 + r]
+  auto epilogue = [&](int nb) __attribute__((always_inline)) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bw[j] = fp4x8_to_bf16x8(wd[j], scale);
+    for (int n = 0; n < 2; ++n) {
+      const int tile = (c.nb0 + nb) * kGemmTiles + 2 * wave + n;
+      const bool nval = tile < gm.NT;
+      const int feat = tile * 16 + r;
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-        const char* ap = lds + (m * 16 + r) * ROWB + 64 * g;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[m] = mfma16x16x32(as_bf16x8(*reinterpret_cast<const uint4*>(ap + 16 * j)), bw[j], acc[m]);
-      }
-    };
-
-    uint4 w0, w1, w2, w3;
-    uint32_t sc_cur = 0, sc_nxt = 0;
-    if (has_tile) {
-      sc_cur = load_sc(0);
-      w0 = load_w(0);
-      w1 = load_w(1);
-      w2 = load_w(2);
-    }
-    for (int kg = 0; kg < gm.KG4 * 4; kg += 4) {
-      // chunk switches happen for every existing group; groups past KG (the last body's tail) skip
-      if (kg < gm.KG) next_chunk(kg);
-      if (has_tile) {
-        sc_nxt = load_sc(kg / 4 + 1);
-        w3 = load_w(kg + 3);
-        if (kg < gm.KG) compute(w0, sc_cur, 0);
-        w0 = load_w(kg + 4);
-      }
-      if (kg + 1 < gm.KG) next_chunk(kg + 1);
-      if (has_tile) {
-        if (kg + 1 < gm.KG) compute(w1, sc_cur, 1);
-        w1 = load_w(kg + 5);
-      }
-      if (kg + 2 < gm.KG) next_chunk(kg + 2);
-      if (has_tile) {
-        if (kg + 2 < gm.KG) compute(w2, sc_cur, 2);
-        w2 = load_w(kg + 6);
-      }
-      if (kg + 3 < gm.KG) next_chunk(kg + 3);
-      if (has_tile) {
-        if (kg + 3 < gm.KG) compute(w3, sc_cur, 3);
-        sc_cur = sc_nxt;
-      }
-    }
-
-    // epilogue: acc[m][v] = D[act row m*16 + 4g + v][feature nt*16 + r]
-    const int feat = ntc * 16 + r;
-    const float bsum = bias[(size_t)e * N + feat];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int orow = m * 16 + 4 * g + v;
-        const float val = acc[m][v] + bsum;
-        if (GATE_UP) {
-          const float partner = __shfl_xor(val, 1, 64);
-          if (has_tile && (r & 1) == 0 && orow < rows)
-            reinterpret_cast<uint16_t*>(out)[(size_t)(row_lo + m0 + orow) * (N / 2) + feat / 2] =
-                f2bf(swiglu_gptoss(val, partner));
-        } else {
-          if (has_tile && orow < rows)
-            reinterpret_cast<float*>(out)[(size_t)(row_lo + m0 + orow) * N + feat] = val;
+        for (int v = 0; v < 4; ++v) {
+          const int orow = 16 * m + 4 * g + v;
+          const float val = acc[m][n][v] + bsum[n];
+          if (GATE_UP) {
+            const float partner = lane_xor1(val);
+            if (nval && (r & 1) == 0 && orow < rows)
+              reinterpret_cast<uint16_t*>(c.out)[(size_t)(c.row_lo + m0 + orow) * (c.N / 2) + feat / 2] =
+                  f2bf(swiglu_gptoss(val, partner));
+          } else {
+            if (nval && orow < rows)
+              reinterpret_cast<float*>(c.out)[(size_t)(c.row_lo + m0 + orow) * c.N + feat] = val;
+          }
         }
       }
     }
+  };
+
+  // group kg of a block from stage `cur` and weight slot `wc` (steps 0, 1, 2 from x0, x1, x0;
+  // step 3 from x1); hands over to the next group (`nxt`, `wn`, into x0) and refills `cur` and
+  // `wc` 4 groups ahead
+  auto group = [&](char* cur, u32x4 (&wc)[2], const char* nxt, const u32x4 (&wn)[2], int kg)
+                   __attribute__((always_inline)) {
+    read_a(a1, cur, std::integral_constant<int, 1>{});
+    cvt(b1, wc, std::integral_constant<int, 1>{});
+    mfma_step(a0, b0);
+    sched_step();
+    read_a(a0, cur, std::integral_constant<int, 2>{});
+    cvt(b0, wc, std::integral_constant<int, 2>{});
+    mfma_step(a1, b1);
+    sched_step();
+    read_a(a1, cur, std::integral_constant<int, 3>{});
+    cvt(b1, wc, std::integral_constant<int, 3>{});
+    mfma_step(a0, b0);
+    sched_step();
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(WAIT));  // this wave's loads of the next group are done
+    lds_barrier();  // every wave's part of the next stage is in LDS; every wave is done with `cur`
+    // step 3 under the next group's first reads and conversions and the refill
+    read_scales(nxt, kg + 1 == KGP ? 0 : kg + 1);
+    read_a(a0, nxt, std::integral_constant<int, 0>{});
+    mfma_step(a1, b1);
+    cvt(b0, wn, std::integral_constant<int, 0>{});
+    issue(wc, cur);
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+    mx_static_for<0, MT>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+    });
+    mx_static_for<0, MT - 1>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmem, 2, 0);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  lds_barrier();  // every wave is done with the previous pass's stages
+  load_bias(0);
+  // the stage waits count loads per group in issue order: no load may move across a group
+  asm volatile("" ::: "memory");
+  issue(w0, st0);
+  asm volatile("" ::: "memory");
+  issue(w1, st1);
+  asm volatile("" ::: "memory");
+  issue(w2, st2);
+  asm volatile("" ::: "memory");
+  issue(w3, st3);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm((kGemmStages - 1) * LOADS));
+  lds_barrier();  // stage 0 is in LDS
+  for (int nb = 0; nb < c.nbn; ++nb) {
+    // the block's first operands (stage 0 stays valid until the first group's barrier); taken here
+    // rather than carried through the previous block's epilogue, to keep that epilogue's register
+    // pressure low: a spill would add vector-memory operations the stage waits do not count
+    read_scales(st0, 0);
+    read_a(a0, st0, std::integral_constant<int, 0>{});
+    cvt(b0, w0, std::integral_constant<int, 0>{});
+    for (int kg = 0; kg < KGP; kg += kGemmStages) {
+      group(st0, w0, st1, w1, kg);
+      group(st1, w1, st2, w2, kg + 1);
+      group(st2, w2, st3, w3, kg + 2);
+      group(st3, w3, st0, w0, kg + 3);
+    }
+    epilogue(nb);
+    load_bias(nb + 1);
+    zero_acc();
   }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the loads past the chunk's end have landed
+}
+
+template <bool GATE_UP>
+__global__ __launch_bounds__(512) void moe_mxfp4_gemm_kernel(
+    const uint16_t* __restrict__ act, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ offsets, int k_top, const uint8_t* __restrict__ packed,
+    const float* __restrict__ bias, int E, int N, int K, int min_rows, int chunk, void* __restrict__ out) {
+  __shared__ __align__(16) char st0[kGemmStage];
+  __shared__ __align__(16) char st1[kGemmStage];
+  __shared__ __align__(16) char st2[kGemmStage];
+  __shared__ __align__(16) char st3[kGemmStage];
+  GemmCtx c;
+  c.gm = mx_geom(E, N, K);
+  const int blocks_per_e = (c.gm.NT + kGemmTiles - 1) / kGemmTiles;
+  const int chunks_per_e = (blocks_per_e + chunk - 1) / chunk;
+  // work units (expert, chunk of weight blocks) are spread so that consecutive ones run on one XCD
+  // (workgroups are dealt to the 8 XCDs round-robin): its L2 then serves an expert's rows to all.
+  const int per_xcd = (int)(gridDim.x / 8);
+  const int unit = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (unit >= E * chunks_per_e) return;
+  c.e = unit / chunks_per_e;
+  c.nb0 = (unit % chunks_per_e) * chunk;
+  c.nbn = min(chunk, blocks_per_e - c.nb0);  // weight blocks in this chunk
+  c.row_lo = offsets[c.e];
+  const int n_e = offsets[c.e + 1] - c.row_lo;
+  if (n_e <= 0 || n_e < min_rows) return;  // uniform over the workgroup
+  c.act = act;
+  c.perm = perm;
+  c.bias = bias;
+  c.out = out;
+  c.k_top = k_top;
+  c.N = N;
+  c.K = K;
+  const int tid = threadIdx.x;
+  c.lane = tid & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  c.r = c.lane & 15;
+  c.g = c.lane >> 4;
+  c.tile_bytes = (size_t)c.gm.G * 256;
+  c.wbase = packed + (size_t)c.e * c.gm.NT * c.tile_bytes + c.lane * 16;
+  c.sbase = packed + c.gm.data_bytes + (size_t)c.e * c.gm.NT * c.gm.KG4 * 256 + c.lane * 4;
+  // passes of 96 rows; the last one takes the fewest 32-row multiples that hold its rows
+  for (int m0 = 0; m0 < n_e; m0 += kGemmRows) {
+    const int rows = min(kGemmRows, n_e - m0);
+    if (rows > 64) gemm_pass<GATE_UP, 6>(c, st0, st1, st2, st3, m0, rows);
+    else if (rows > 32) gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, m0, rows);
+    else gemm_pass<GATE_UP, 2>(c, st0, st1, st2, st3, m0, rows);
+  }
+}
+
+// Chunk of weight blocks per workgroup: the largest chunk that still gives at least 3 rounds of
+// workgroups over the CUs, so that workgroups of unequal length (experts with different row
+// counts take different row tiles) balance, while each start-up is shared by several blocks.
+inline int gemm_chunk(const MxGeom& gm, int E) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, v = 0;
+    cus = (hipGetDevice(&dev) == hipSuccess &&
+           hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
+  }
+  const int W = (gm.NT + kGemmTiles - 1) / kGemmTiles;
+  int best = 1;
+  for (int c = 1; c <= W; ++c)
+    if ((int64_t)E * ((W + c - 1) / c) >= 3LL * cus) best = c;
+  return best;
+}
+
+// grid of the tiled GEMM: the work units (expert, chunk of weight blocks) rounded up to 8 XCDs
+inline int gemm_grid(const MxGeom& gm, int E, int chunk) {
+  const int W = (gm.NT + kGemmTiles - 1) / kGemmTiles;
+  const int units = E * ((W + chunk - 1) / chunk);
+  return ((units + 7) / 8) * 8;
 }
 
 // Groups of more than kDenseFrom rows take the dense kernel when the batch averages at least that
 // many rows per expert (otherwise the row-pass kernel serves every group: a rare large group costs
 // extra passes, not a launch of mostly idle workgroups).  Both kernels are correct for any count.
 constexpr int kDenseFrom = 8;
-constexpr int kDenseMT = 6;  // 96 rows per pass
 
 inline bool use_dense(int rows_total, int E) { return (int64_t)rows_total >= (int64_t)kDenseFrom * E; }
 
@@ -398,7 +603,7 @@ int launch_moe_gate_up(const uint16_t* x, const int32_t* perm, const int32_t* of
                        const uint8_t* w13, const float* b13, int T, int E, int H, int I, uint16_t* h,
                        hipStream_t s) {
   const MxGeom gm = mx_geom(E, 2 * I, H);
-  const bool dense = use_dense(T * k_top, E);
+  const bool dense = use_dense(T * k_top, E) && H >= 128;  // the tiled kernel reads 128-K groups
   if (H <= 4064) {
     const int wg_per_e = ceil_div(gm.NT, 4 * kNTW);
     hipLaunchKernelGGL((moe_mxfp4_kernel<true, kNTW>), dim3(E * wg_per_e), dim3(256),
@@ -408,9 +613,10 @@ int launch_moe_gate_up(const uint16_t* x, const int32_t* perm, const int32_t* of
     if (rc) return rc;
   }
   if (dense || H > 4064) {
-    hipLaunchKernelGGL((moe_mxfp4_dense_kernel<true, kDenseMT>), dim3(E * ceil_div(gm.NT, 4)), dim3(256),
-                       kDenseMT * 16 * 272, s, x, perm, offsets, k_top, w13, b13, E, 2 * I, H,
-                       H > 4064 ? 1 : kDenseFrom + 1, (void*)h);
+    const int chunk = gemm_chunk(gm, E);
+    hipLaunchKernelGGL((moe_mxfp4_gemm_kernel<true>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s,
+                       x, perm, offsets, k_top, w13, b13, E, 2 * I, H, H > 4064 ? 1 : kDenseFrom + 1, chunk,
+                       (void*)h);
     return check_launch("moe_gate_up_mxfp4(dense)");
   }
   return FLYAI_OK;
@@ -419,7 +625,7 @@ int launch_moe_gate_up(const uint16_t* x, const int32_t* perm, const int32_t* of
 int launch_moe_down(const uint16_t* h, const int32_t* offsets, const uint8_t* w2, const float* b2,
                     int rows_total, int E, int H, int I, float* y, hipStream_t s) {
   const MxGeom gm = mx_geom(E, H, I);
-  const bool dense = use_dense(rows_total, E);
+  const bool dense = use_dense(rows_total, E) && I >= 128;  // the tiled kernel reads 128-K groups
   if (I <= 4064) {
     const int wg_per_e = ceil_div(gm.NT, 4 * kNTW);
     hipLaunchKernelGGL((moe_mxfp4_kernel<false, kNTW>), dim3(E * wg_per_e), dim3(256),
@@ -429,9 +635,9 @@ int launch_moe_down(const uint16_t* h, const int32_t* offsets, const uint8_t* w2
     if (rc) return rc;
   }
   if (dense || I > 4064) {
-    hipLaunchKernelGGL((moe_mxfp4_dense_kernel<false, kDenseMT>), dim3(E * ceil_div(gm.NT, 4)), dim3(256),
-                       kDenseMT * 16 * 272, s, h, nullptr, offsets, 1, w2, b2, E, H, I,
-                       I > 4064 ? 1 : kDenseFrom + 1, (void*)y);
+    const int chunk = gemm_chunk(gm, E);
+    hipLaunchKernelGGL((moe_mxfp4_gemm_kernel<false>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s,
+                       h, nullptr, offsets, 1, w2, b2, E, H, I, I > 4064 ? 1 : kDenseFrom + 1, chunk, (void*)y);
     return check_launch("moe_down_mxfp4(dense)");
   }
   return FLYAI_OK;

@@ -208,7 +208,7 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
       const int rr = i / VPR;
       asrc[J] = aq + (size_t)src_row(row_lo + m0 + (rr < rows ? rr : 0)) * K + (i % VPR) * 16;
     });
-    __syncthreads();  // the previous pass is done with LDS
+    lds_barrier();  // the previous pass is done with LDS (the weight ring stays in flight)
     for (int i = tid; i < MT * 16 * KB; i += 256) {
       const int rr = i / KB, kb = i % KB;
       lds_s[i] = rr < rows ? as[(size_t)src_row(row_lo + m0 + rr) * KB + kb] : (uint8_t)127;
@@ -255,12 +255,12 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
     // first switches chunks (every wave takes part, so waves without tiles still meet the barriers).
     const int nchunks = K / KC;
     auto next_chunk = [&](int c) __attribute__((always_inline)) {
-      __syncthreads();  // every wave is done with the previous chunk
+      lds_barrier();  // every wave is done with the previous chunk (the weight ring stays in flight)
       static_for<0, SREG>([&](auto J) {
         const int i = J * 256 + tid;
         *reinterpret_cast<u32x4*>(lds_a + (i / VPR) * ROWB + (i % VPR) * 16) = stg[J];
       });
-      __syncthreads();
+      lds_barrier();
       if (c + 1 < nchunks)
         static_for<0, SREG>([&](auto J) { stg[J] = *reinterpret_cast<const u32x4*>(asrc[J] + (size_t)(c + 1) * KC); });
     };

@@ -280,18 +280,6 @@ constexpr int kGemmRows = 96;                        // group rows per pass
 constexpr int kGemmStage = kGemmRows * 256 + kGemmTiles * 256;  // activations + scale dwords
 constexpr int kGemmStages = 4;
 
-// s_waitcnt immediates (vmcnt in bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8)
-constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
-constexpr int kWaitLgkm0 = 15 | (3 << 14) | (7 << 4);
-
-// workgroup barrier that waits only for the wave's own LDS operations (global loads stay in flight)
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(kWaitLgkm0);
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // instruction classes for __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedValu = 0x2, kSchedMfma = 0x8, kSchedVmem = 0x10, kSchedDsRead = 0x100;
 

@@ -66,6 +66,9 @@ def main():
                     help="after timing, copy a buffer of this many MiB 3 times (a known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     ap.add_argument("--workload", choices=("c1", "c2", "c3"), default="c1")
+    ap.add_argument("--graphs", action="store_true",
+                    help="replay the stage step as a HIP graph (measured slower than direct launches "
+                         "on this stack, so off by default)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -117,7 +120,7 @@ def run_gptoss(args, chunked_prefill=False):
     for t in kv.k + kv.v:
         t.copy_(torch.randn(t.shape, device=dev, generator=g).to(torch.bfloat16))
     hidden0 = torch.randn(T, shape.hidden, device=dev, generator=g).to(torch.bfloat16)
-    stage = RaggedStage(shape, layers, rot, kv, max_tokens=max(64, T), max_seqs=S)
+    stage = RaggedStage(shape, layers, rot, kv, max_tokens=max(64, T), max_seqs=S, use_graphs=args.graphs)
     slots = list(range(S))
     torch.cuda.synchronize()
     print("[bench] warmup", file=sys.stderr, flush=True)
@@ -187,7 +190,8 @@ def run_gptoss(args, chunked_prefill=False):
             "config": {"workload": "gpt-oss-120b-shaped 9-layer MXFP4 stage, one 2048-token prefill chunk "
                                    "(prior KV 4096) + 48 decode rows (KV 512-8192)",
                        "layers": args.layers, "tokens": T, "sequences": S, "experts": shape.n_experts,
-                       "top_k": shape.top_k, "hidden": shape.hidden, "parallelism": "single GPU"},
+                       "top_k": shape.top_k, "hidden": shape.hidden, "parallelism": "single GPU",
+                       "step_launch": "hip graph replay" if args.graphs else "direct launches"},
             "moe_layer_us": round(gu_us + dn_us, 2),
             "roofline": {"bound": "mfma", "kernel": "moe_mxfp4_gemm_kernel<gate_up>", "achieved": round(tflops, 1),
                          "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
@@ -208,7 +212,8 @@ def run_gptoss(args, chunked_prefill=False):
         "config": {"workload": "gpt-oss-120b-shaped 9-layer MXFP4 stage, ragged batch of 32 sequences "
                                "(24 decode + 8 four-token verify = 56 tokens), KV 512-8192",
                    "layers": args.layers, "tokens": T, "sequences": S, "experts": shape.n_experts,
-                   "top_k": shape.top_k, "hidden": shape.hidden, "parallelism": "single GPU"},
+                   "top_k": shape.top_k, "hidden": shape.hidden, "parallelism": "single GPU",
+                   "step_launch": "hip graph replay" if args.graphs else "direct launches"},
         "moe_layer_us": round(gu_us + dn_us, 2),
         "roofline": {"bound": "hbm", "kernel": "moe_mxfp4_kernel<gate_up>", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),

@@ -82,6 +82,8 @@ _PROTOS = {
     "flyai_stage_set_workspace": (C.c_int, [P, P, SZ, P, SZ]),
     "flyai_stage_forward": (C.c_int, [P, P, P, P, P, I32, P, P]),
     "flyai_stage_debug_buffer": (P, [P, I32]),
+    "flyai_stage_set_graphs": (C.c_int, [P, I32]),
+    "flyai_stage_graphs_captured": (I32, [P]),
 }
 
 _lib = None

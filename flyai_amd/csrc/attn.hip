@@ -218,7 +218,10 @@ __global__ __launch_bounds__(64, 2) void attn_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
     const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
     const int32_t* __restrict__ kv_cap, int window, int Hq,
-    const flyai_attn_item* __restrict__ items, float* __restrict__ partials) {
+    const flyai_attn_item* __restrict__ items, const int32_t* __restrict__ n_live,
+    float* __restrict__ partials) {
+  // a graph-replayed step launches the plan's capacity; items past this step's count exit
+  if (n_live && (int)blockIdx.x >= *n_live) return;
   const flyai_attn_item it = items[blockIdx.x];
   if (it.ntok <= 2)
     attn_item<1>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials);
@@ -231,7 +234,9 @@ __global__ __launch_bounds__(64, 2) void attn_partial_kernel(
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ partials,
                                                          const flyai_attn_group* __restrict__ groups,
                                                          const float* __restrict__ sinks, int Hq,
+                                                         const int32_t* __restrict__ n_live,
                                                          uint16_t* __restrict__ out) {
+  if (n_live && (int)blockIdx.x >= *n_live) return;  // as in attn_partial_kernel
   const flyai_attn_group gr = groups[blockIdx.x];
   const int rq = threadIdx.x >> 3, part = threadIdx.x & 7;
   const int ti = rq >> 3;
@@ -259,19 +264,21 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   *reinterpret_cast<uint4*>(o) = make_uint4(wv[0], wv[1], wv[2], wv[3]);
 }
 
+// n_items / n_groups size the grids; counts (nullable) holds this step's live item and group
+// counts on the device, for launches sized by a plan capacity (graph replay)
 int launch_attn(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
                 const int64_t* kv_base, const int32_t* kv_cap, const float* sinks, int window,
                 int Hq, const flyai_attn_item* items, int n_items, int n_small,
-                const flyai_attn_group* groups, int n_groups, float* partials, uint16_t* out,
-                hipStream_t s) {
+                const flyai_attn_group* groups, int n_groups, const int32_t* counts, float* partials,
+                uint16_t* out, hipStream_t s) {
   if (n_items == 0) return FLYAI_OK;
   (void)n_small;  // the plan's two ranges share one launch
   hipLaunchKernelGGL(attn_partial_kernel, dim3(n_items), dim3(64), 0, s, q, k_pool, v_pool, kv_base,
-                     kv_cap, window, Hq, items, partials);
+                     kv_cap, window, Hq, items, counts, partials);
   int rc = check_launch("attn_partial");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_merge_kernel, dim3(n_groups), dim3(256), 0, s, partials, groups, sinks,
-                     Hq, out);
+                     Hq, counts ? counts + 1 : nullptr, out);
   return check_launch("attn_merge");
 }
 
@@ -368,5 +375,5 @@ extern "C" int flyai_attn_ragged(const uint16_t* q, const uint16_t* k_pool, cons
                     (n_items == 0 || (items_dev && groups_dev && partials)),
                 "attn: null pointer");
   return launch_attn(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, items_dev, n_items,
-                     n_items_small, groups_dev, n_groups, partials, out, as_stream(stream));
+                     n_items_small, groups_dev, n_groups, nullptr, partials, out, as_stream(stream));
 }

@@ -53,7 +53,7 @@ int launch_qkv_rope_kv(const uint16_t*, const uint16_t*, const uint16_t*, float*
 size_t linear_partials_bytes(int M, int N, int K);
 int launch_attn(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
                 const float*, int, int, const flyai_attn_item*, int, int, const flyai_attn_group*, int,
-                float*, uint16_t*, hipStream_t);
+                const int32_t*, float*, uint16_t*, hipStream_t);
 int attn_plan(const int32_t*, const int32_t*, int, int, int, int, flyai_attn_item*, int,
               flyai_attn_group*, int, int*, int*, int*);
 
@@ -87,6 +87,7 @@ struct flyai_stage {
   size_t o_xn, o_gemm, o_qrot, o_attn, o_parts;
   size_t o_ids, o_w, o_logits, o_hist, o_off, o_perm, o_inv, o_hmoe, o_y;
   size_t o_h2;  // the post-attention residual stream of the decode-sized path
+  size_t o_hidden;  // stage-owned hidden rows the replayed graphs read and update
   size_t dev_bytes = 0;
   size_t host_half = 0;  // bytes of one pinned staging half (== blob_max)
   std::vector<flyai_attn_item> plan_items[2];
@@ -96,10 +97,25 @@ struct flyai_stage {
   hipEvent_t staged[2] = {nullptr, nullptr};
   int half = 0;
   bool events_ready = false;
+  // HIP-graph replay of the step (off by default).  One executable graph per key (tokens,
+  // sequences, attention plan capacities), captured on first use on a stream of the stage's own
+  // (the null stream cannot be captured) and replayed on the caller's stream.
+  bool graphs = false;
+  hipStream_t capture_stream = nullptr;
+  struct Graph {
+    int64_t key[6];
+    hipGraphExec_t exec;
+    uint64_t last_use;
+  };
+  std::vector<Graph> graph_cache;
+  uint64_t use_clock = 0;
+  int graphs_captured = 0;
 };
+static constexpr int kGraphCacheMax = 16;
+static constexpr int kPlanBucket = 64;  // attention plan capacities round up to this
 
 static size_t blob_bytes(int S, int n_items0, int n_items1, int n_groups0, int n_groups1) {
-  return align256((size_t)S * 4) * 3 + align256((size_t)S * 8) +
+  return align256(4 * sizeof(int32_t)) + align256((size_t)S * 4) * 3 + align256((size_t)S * 8) +
          align256((size_t)n_items0 * sizeof(flyai_attn_item)) + align256((size_t)n_items1 * sizeof(flyai_attn_item)) +
          align256((size_t)n_groups0 * sizeof(flyai_attn_group)) + align256((size_t)n_groups1 * sizeof(flyai_attn_group));
 }
@@ -135,6 +151,7 @@ static void layout(flyai_stage* st) {
   st->o_hmoe = d.take(P * c.intermediate * 2);
   st->o_y = d.take(P * c.hidden * 4);
   st->o_h2 = d.take(T * c.hidden * 2);
+  st->o_hidden = d.take(T * c.hidden * 2);
   st->dev_bytes = d.off;
   st->host_half = st->blob_max;
 }
@@ -182,6 +199,8 @@ extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** o
 
 extern "C" void flyai_stage_destroy(flyai_stage* st) {
   if (!st) return;
+  for (auto& g : st->graph_cache) hipGraphExecDestroy(g.exec);
+  if (st->capture_stream) hipStreamDestroy(st->capture_stream);
   for (int i = 0; i < 2; ++i)
     if (st->staged[i]) hipEventDestroy(st->staged[i]);
   delete[] st->layers;
@@ -251,6 +270,140 @@ static int copy_h2d(char* dst, const char* src, size_t bytes, hipStream_t s) {
   return FLYAI_OK;
 }
 
+// Where this step's batch sits in the device blob, and how the kernels are sized.
+namespace {
+struct StepPlan {
+  int Tn, S;
+  int grid_items[2], grid_groups[2];  // launch sizes: exact counts, or the plan capacities (graphs)
+  int n_small[2];
+  size_t off_counts, off_q, off_st, off_cap, off_base, off_items[2], off_groups[2];
+};
+}  // namespace
+
+// The step's kernel sequence: ragged packing, then every layer.  Runs eagerly or under capture.
+// counts != nullptr: the attention grids are capacities and the kernels read the live counts there.
+static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* counts, uint16_t* hidden,
+                       hipStream_t s) {
+  const flyai_stage_config& c = st->cfg;
+  char* d = st->dev;
+  char* blob = d + st->o_blob;
+  auto I32 = [&](size_t o) { return reinterpret_cast<int32_t*>(d + o); };
+  auto F32 = [&](size_t o) { return reinterpret_cast<float*>(d + o); };
+  auto B16 = [&](size_t o) { return reinterpret_cast<uint16_t*>(d + o); };
+  const int64_t* base_d = reinterpret_cast<const int64_t*>(blob + sp.off_base);
+  const int32_t* cap_d = reinterpret_cast<const int32_t*>(blob + sp.off_cap);
+  flyai_stream_t stream = reinterpret_cast<flyai_stream_t>(s);
+
+  RUN(flyai_pack_ragged(reinterpret_cast<const int32_t*>(blob + sp.off_q),
+                        reinterpret_cast<const int32_t*>(blob + sp.off_st), base_d, cap_d, sp.S, c.head_dim,
+                        c.max_tokens, I32(st->o_cu), I32(st->o_pos), I32(st->o_sid),
+                        I32(st->o_kvlen), reinterpret_cast<int64_t*>(d + st->o_slot),
+                        I32(st->o_status), stream));
+  const int Tn = sp.Tn;
+  const int H = c.hidden, E = c.n_experts, k = c.top_k, I = c.intermediate;
+  const bool fused_route = Tn <= 256 && Tn * k <= 4096;
+  RUN(launch_rmsnorm(hidden, st->layers[0].ln1, Tn, H, c.rms_eps, B16(st->o_xn), s));
+  for (int l = 0; l < c.n_layers; ++l) {
+    const flyai_layer_desc& L = st->layers[l];
+    const int p = L.sliding ? 1 : 0;
+    // xn holds this layer's input RMSNorm (written by the previous layer's combine)
+    RUN(launch_qkv_rope_kv(B16(st->o_xn), L.wqkv, L.bqkv, F32(st->o_gemm), I32(st->o_pos),
+                           I32(st->o_sid), st->cos_tab, st->sin_tab, c.rope_positions, Tn, H,
+                           c.n_q_heads, c.n_kv_heads, c.head_dim, base_d, cap_d, B16(st->o_qrot),
+                           L.k_pool, L.v_pool, s));
+    RUN(launch_attn(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks,
+                    L.sliding ? c.window : 0, c.n_q_heads,
+                    reinterpret_cast<const flyai_attn_item*>(blob + sp.off_items[p]), sp.grid_items[p],
+                    sp.n_small[p], reinterpret_cast<const flyai_attn_group*>(blob + sp.off_groups[p]),
+                    sp.grid_groups[p], counts ? counts + 2 * p : nullptr, F32(st->o_parts),
+                    B16(st->o_attn), s));
+    if (fused_route) {
+      // decode-sized: o-proj finalize + residual + RMSNorm + router logits, then top-k + permute
+      RUN(launch_linear_residual_rmsnorm_logits(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
+                                                hidden, B16(st->o_h2), L.ln2, c.rms_eps, B16(st->o_xn),
+                                                F32(st->o_gemm), L.router_w, L.router_b, E,
+                                                F32(st->o_logits), s));
+      RUN(launch_topk_permute(F32(st->o_logits), Tn, E, k, I32(st->o_ids), F32(st->o_w), I32(st->o_hist),
+                              I32(st->o_off), I32(st->o_perm), I32(st->o_inv), s));
+    } else {
+      RUN(launch_linear_residual_rmsnorm(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
+                                         hidden, L.ln2, c.rms_eps, B16(st->o_xn), F32(st->o_gemm), s));
+      RUN(launch_route_permute(B16(st->o_xn), L.router_w, L.router_b, Tn, H, E, k, I32(st->o_ids),
+                               F32(st->o_w), F32(st->o_logits), I32(st->o_hist), I32(st->o_off),
+                               I32(st->o_perm), I32(st->o_inv), s));
+    }
+    RUN(launch_moe_gate_up(B16(st->o_xn), I32(st->o_perm), I32(st->o_off), k, L.w13_packed, L.b13,
+                           Tn, E, H, I, B16(st->o_hmoe), s));
+    RUN(launch_moe_down(B16(st->o_hmoe), I32(st->o_off), L.w2_packed, L.b2, Tn * k, E, H, I,
+                        F32(st->o_y), s));
+    const float* next_ln1 = (l + 1 < c.n_layers) ? st->layers[l + 1].ln1 : nullptr;
+    // the fused path left the post-attention residual in o_h2; the other path updated hidden in place
+    const uint16_t* resid = fused_route ? B16(st->o_h2) : hidden;
+    RUN(launch_combine(F32(st->o_y), I32(st->o_inv), F32(st->o_w), Tn, k, H, resid, hidden, next_ln1,
+                       c.rms_eps, B16(st->o_xn), s));
+  }
+  return FLYAI_OK;
+}
+
+static int hip_fail(const char* what, hipError_t e) {
+  return set_error(FLYAI_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// The executable graph for this step's key, captured on first use (least recently used evicted).
+static int step_graph(flyai_stage* st, const StepPlan& sp, hipGraphExec_t* out) {
+  const int64_t key[6] = {sp.Tn, sp.S, sp.grid_items[0], sp.grid_items[1], sp.grid_groups[0], sp.grid_groups[1]};
+  ++st->use_clock;
+  for (auto& g : st->graph_cache)
+    if (memcmp(g.key, key, sizeof(key)) == 0) {
+      g.last_use = st->use_clock;
+      *out = g.exec;
+      return FLYAI_OK;
+    }
+  if (!st->capture_stream) {
+    const hipError_t e = hipStreamCreateWithFlags(&st->capture_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) return hip_fail("hipStreamCreate", e);
+  }
+  hipStream_t cs = st->capture_stream;
+  hipError_t e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+  if (e != hipSuccess) return hip_fail("hipStreamBeginCapture", e);
+  const int rc = record_step(st, sp, reinterpret_cast<const int32_t*>(st->dev + st->o_blob + sp.off_counts),
+                             reinterpret_cast<uint16_t*>(st->dev + st->o_hidden), cs);
+  hipGraph_t graph = nullptr;
+  e = hipStreamEndCapture(cs, &graph);
+  if (rc) {
+    if (graph) hipGraphDestroy(graph);
+    return rc;
+  }
+  if (e != hipSuccess) return hip_fail("hipStreamEndCapture", e);
+  hipGraphExec_t exec = nullptr;
+  e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+  hipGraphDestroy(graph);
+  if (e != hipSuccess) return hip_fail("hipGraphInstantiate", e);
+  if ((int)st->graph_cache.size() >= kGraphCacheMax) {
+    size_t lru = 0;
+    for (size_t i = 1; i < st->graph_cache.size(); ++i)
+      if (st->graph_cache[i].last_use < st->graph_cache[lru].last_use) lru = i;
+    hipGraphExecDestroy(st->graph_cache[lru].exec);
+    st->graph_cache.erase(st->graph_cache.begin() + lru);
+  }
+  flyai_stage::Graph g;
+  memcpy(g.key, key, sizeof(key));
+  g.exec = exec;
+  g.last_use = st->use_clock;
+  st->graph_cache.push_back(g);
+  ++st->graphs_captured;
+  *out = exec;
+  return FLYAI_OK;
+}
+
+extern "C" int flyai_stage_set_graphs(flyai_stage* st, int32_t enable) {
+  FLYAI_REQUIRE(st, "set_graphs: null stage");
+  st->graphs = enable != 0;
+  return FLYAI_OK;
+}
+
+extern "C" int32_t flyai_stage_graphs_captured(const flyai_stage* st) { return st ? st->graphs_captured : 0; }
+
 extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const int32_t* starts,
                                    const int64_t* kv_base, const int32_t* kv_cap, int32_t S,
                                    uint16_t* hidden, flyai_stream_t stream) {
@@ -280,94 +433,63 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
     FLYAI_REQUIRE(st->layers[l].wqkv, "forward: layer %d not bound", l);
   hipStream_t s = as_stream(stream);
 
-  int n_items[2], n_groups[2], n_small[2];
+  StepPlan sp;
+  sp.Tn = (int)T;
+  sp.S = S;
+  int n_items[2], n_groups[2];
   for (int p = 0; p < 2; ++p) {
     RUN(attn_plan(q_lens, starts, S, c.n_kv_heads, p == 0 ? 0 : c.window, c.attn_split_keys,
                   st->plan_items[p].data(), c.max_attn_items, st->plan_groups[p].data(), st->max_groups,
-                  &n_items[p], &n_groups[p], &n_small[p]));
+                  &n_items[p], &n_groups[p], &sp.n_small[p]));
+    // replayed graphs are sized by capacities, so that a step with a few more items (longer KV)
+    // reuses the graph; the kernels read the live counts from the blob
+    auto bucket = [](int n, int cap) { const int b = (n + kPlanBucket - 1) / kPlanBucket * kPlanBucket; return b < cap ? b : cap; };
+    sp.grid_items[p] = st->graphs ? bucket(n_items[p], c.max_attn_items) : n_items[p];
+    sp.grid_groups[p] = st->graphs ? bucket(n_groups[p], st->max_groups) : n_groups[p];
   }
-  // one compact blob per step: q_lens | starts | kv_cap | kv_base | items x2 | groups x2
-  size_t off_q, off_st, off_cap, off_base, off_items[2], off_groups[2];
+  // one compact blob per step: live counts | q_lens | starts | kv_cap | kv_base | items x2 | groups x2
   {
     Carve b;
-    off_q = b.take((size_t)S * 4);
-    off_st = b.take((size_t)S * 4);
-    off_cap = b.take((size_t)S * 4);
-    off_base = b.take((size_t)S * 8);
-    for (int p = 0; p < 2; ++p) off_items[p] = b.take((size_t)n_items[p] * sizeof(flyai_attn_item));
-    for (int p = 0; p < 2; ++p) off_groups[p] = b.take((size_t)n_groups[p] * sizeof(flyai_attn_group));
+    sp.off_counts = b.take(4 * sizeof(int32_t));
+    sp.off_q = b.take((size_t)S * 4);
+    sp.off_st = b.take((size_t)S * 4);
+    sp.off_cap = b.take((size_t)S * 4);
+    sp.off_base = b.take((size_t)S * 8);
+    for (int p = 0; p < 2; ++p) sp.off_items[p] = b.take((size_t)sp.grid_items[p] * sizeof(flyai_attn_item));
+    for (int p = 0; p < 2; ++p) sp.off_groups[p] = b.take((size_t)sp.grid_groups[p] * sizeof(flyai_attn_group));
     if (b.off > st->blob_max) return set_error(FLYAI_ERANGE, "batch blob exceeds its reservation");
     // wait until the GPU consumed this staging half's previous contents, then fill it
     const int h = st->half;
     st->half ^= 1;
     const hipError_t ew = hipEventSynchronize(st->staged[h]);
-    if (ew != hipSuccess) return set_error(FLYAI_EHIP, "hipEventSynchronize: %s", hipGetErrorString(ew));
+    if (ew != hipSuccess) return hip_fail("hipEventSynchronize", ew);
     char* hb = st->host + h * st->host_half;
-    memcpy(hb + off_q, q_lens, S * 4);
-    memcpy(hb + off_st, starts, S * 4);
-    memcpy(hb + off_cap, kv_cap, S * 4);
-    memcpy(hb + off_base, kv_base, S * 8);
+    const int32_t counts[4] = {n_items[0], n_groups[0], n_items[1], n_groups[1]};
+    memcpy(hb + sp.off_counts, counts, sizeof(counts));
+    memcpy(hb + sp.off_q, q_lens, S * 4);
+    memcpy(hb + sp.off_st, starts, S * 4);
+    memcpy(hb + sp.off_cap, kv_cap, S * 4);
+    memcpy(hb + sp.off_base, kv_base, S * 8);
     for (int p = 0; p < 2; ++p) {
-      memcpy(hb + off_items[p], st->plan_items[p].data(), n_items[p] * sizeof(flyai_attn_item));
-      memcpy(hb + off_groups[p], st->plan_groups[p].data(), n_groups[p] * sizeof(flyai_attn_group));
+      memcpy(hb + sp.off_items[p], st->plan_items[p].data(), n_items[p] * sizeof(flyai_attn_item));
+      memcpy(hb + sp.off_groups[p], st->plan_groups[p].data(), n_groups[p] * sizeof(flyai_attn_group));
     }
     RUN(copy_h2d(st->dev + st->o_blob, hb, b.off, s));
     const hipError_t er = hipEventRecord(st->staged[h], s);
-    if (er != hipSuccess) return set_error(FLYAI_EHIP, "hipEventRecord: %s", hipGetErrorString(er));
+    if (er != hipSuccess) return hip_fail("hipEventRecord", er);
   }
-  char* d = st->dev;
-  char* blob = d + st->o_blob;
-  auto I32 = [&](size_t o) { return reinterpret_cast<int32_t*>(d + o); };
-  auto F32 = [&](size_t o) { return reinterpret_cast<float*>(d + o); };
-  auto B16 = [&](size_t o) { return reinterpret_cast<uint16_t*>(d + o); };
-  const int64_t* base_d = reinterpret_cast<const int64_t*>(blob + off_base);
-  const int32_t* cap_d = reinterpret_cast<const int32_t*>(blob + off_cap);
+  if (!st->graphs) return record_step(st, sp, nullptr, hidden, s);
 
-  RUN(flyai_pack_ragged(reinterpret_cast<const int32_t*>(blob + off_q),
-                        reinterpret_cast<const int32_t*>(blob + off_st), base_d, cap_d, S, c.head_dim,
-                        c.max_tokens, I32(st->o_cu), I32(st->o_pos), I32(st->o_sid),
-                        I32(st->o_kvlen), reinterpret_cast<int64_t*>(d + st->o_slot),
-                        I32(st->o_status), stream));
-  const int Tn = (int)T;
-  const int H = c.hidden, E = c.n_experts, k = c.top_k, I = c.intermediate;
-  RUN(launch_rmsnorm(hidden, st->layers[0].ln1, Tn, H, c.rms_eps, B16(st->o_xn), s));
-  for (int l = 0; l < c.n_layers; ++l) {
-    const flyai_layer_desc& L = st->layers[l];
-    const int p = L.sliding ? 1 : 0;
-    // xn holds this layer's input RMSNorm (written by the previous layer's combine)
-    RUN(launch_qkv_rope_kv(B16(st->o_xn), L.wqkv, L.bqkv, F32(st->o_gemm), I32(st->o_pos),
-                           I32(st->o_sid), st->cos_tab, st->sin_tab, c.rope_positions, Tn, H,
-                           c.n_q_heads, c.n_kv_heads, c.head_dim, base_d, cap_d, B16(st->o_qrot),
-                           L.k_pool, L.v_pool, s));
-    RUN(launch_attn(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks,
-                    L.sliding ? c.window : 0, c.n_q_heads,
-                    reinterpret_cast<const flyai_attn_item*>(blob + off_items[p]), n_items[p], n_small[p],
-                    reinterpret_cast<const flyai_attn_group*>(blob + off_groups[p]), n_groups[p],
-                    F32(st->o_parts), B16(st->o_attn), s));
-    if (Tn <= 256 && Tn * k <= 4096) {
-      // decode-sized: o-proj finalize + residual + RMSNorm + router logits, then top-k + permute
-      RUN(launch_linear_residual_rmsnorm_logits(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
-                                                hidden, B16(st->o_h2), L.ln2, c.rms_eps, B16(st->o_xn),
-                                                F32(st->o_gemm), L.router_w, L.router_b, E,
-                                                F32(st->o_logits), s));
-      RUN(launch_topk_permute(F32(st->o_logits), Tn, E, k, I32(st->o_ids), F32(st->o_w), I32(st->o_hist),
-                              I32(st->o_off), I32(st->o_perm), I32(st->o_inv), s));
-    } else {
-      RUN(launch_linear_residual_rmsnorm(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
-                                         hidden, L.ln2, c.rms_eps, B16(st->o_xn), F32(st->o_gemm), s));
-      RUN(launch_route_permute(B16(st->o_xn), L.router_w, L.router_b, Tn, H, E, k, I32(st->o_ids),
-                               F32(st->o_w), F32(st->o_logits), I32(st->o_hist), I32(st->o_off),
-                               I32(st->o_perm), I32(st->o_inv), s));
-    }
-    RUN(launch_moe_gate_up(B16(st->o_xn), I32(st->o_perm), I32(st->o_off), k, L.w13_packed, L.b13,
-                           Tn, E, H, I, B16(st->o_hmoe), s));
-    RUN(launch_moe_down(B16(st->o_hmoe), I32(st->o_off), L.w2_packed, L.b2, Tn * k, E, H, I,
-                        F32(st->o_y), s));
-    const float* next_ln1 = (l + 1 < c.n_layers) ? st->layers[l + 1].ln1 : nullptr;
-    // the fused path left the post-attention residual in o_h2; the other path updated hidden in place
-    const uint16_t* resid = (Tn <= 256 && Tn * k <= 4096) ? B16(st->o_h2) : hidden;
-    RUN(launch_combine(F32(st->o_y), I32(st->o_inv), F32(st->o_w), Tn, k, H, resid, hidden, next_ln1,
-                       c.rms_eps, B16(st->o_xn), s));
-  }
+  hipGraphExec_t exec = nullptr;
+  RUN(step_graph(st, sp, &exec));
+  // the graph reads and updates the stage-owned rows; the caller's rows are copied in and out
+  uint16_t* hs = reinterpret_cast<uint16_t*>(st->dev + st->o_hidden);
+  const size_t hb = (size_t)sp.Tn * c.hidden * 2;
+  hipError_t e = hipMemcpyAsync(hs, hidden, hb, hipMemcpyDeviceToDevice, s);
+  if (e != hipSuccess) return hip_fail("hipMemcpyAsync", e);
+  e = hipGraphLaunch(exec, s);
+  if (e != hipSuccess) return hip_fail("hipGraphLaunch", e);
+  e = hipMemcpyAsync(hidden, hs, hb, hipMemcpyDeviceToDevice, s);
+  if (e != hipSuccess) return hip_fail("hipMemcpyAsync", e);
   return FLYAI_OK;
 }

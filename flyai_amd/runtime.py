@@ -65,7 +65,7 @@ class RaggedStage:
     """One pipeline stage of GPT-OSS decoder layers on libflyai_stage."""
 
     def __init__(self, shape: GptOssShape, layers, rotary, kv: KVWorkspace, max_tokens, max_seqs,
-                 max_attn_items=None, split_keys=1024, device="cuda"):
+                 max_attn_items=None, split_keys=1024, device="cuda", use_graphs=False):
         self.shape, self.layers, self.rotary, self.kv = shape, layers, rotary, kv
         self.device = torch.device(device)
         self.max_tokens, self.max_seqs = max_tokens, max_seqs
@@ -101,6 +101,19 @@ class RaggedStage:
         self.staging = torch.empty(host_bytes, dtype=torch.uint8, pin_memory=True)
         check(lib().flyai_stage_set_workspace(self._h, C.c_void_p(self._ws_ptr), dev_bytes,
                                               C.c_void_p(self.staging.data_ptr()), host_bytes))
+        self.use_graphs = False
+        self.set_graphs(use_graphs)
+
+    def set_graphs(self, enable):
+        """Replay each step as a HIP graph, one per (tokens, sequences, attention-plan bucket), captured
+        on first use (the CUDA-graph capture of FastVerify.decode, phase0/fastverify.py:221-231)."""
+        if bool(enable) != self.use_graphs:
+            check(lib().flyai_stage_set_graphs(self._h, int(bool(enable))))
+            self.use_graphs = bool(enable)
+
+    @property
+    def graphs_captured(self):
+        return int(lib().flyai_stage_graphs_captured(self._h))
 
     def __del__(self):
         h = getattr(self, "_h", None)
@@ -181,9 +194,11 @@ class FastVerifyStage:
         return flat.view(1, n, self.hidden)
 
     def prefill(self, h, start):
+        self.stage.set_graphs(False)  # prefill runs eager in the reference (fastverify.py:138-155)
         return self._run(h, start)
 
     def decode(self, h, start):
+        self.stage.set_graphs(True)  # one graph per (tokens, KV bucket), as fastverify.py:221-231
         self.out = self._run(h, start)
         return self.out
 
@@ -236,6 +251,7 @@ class BatchedFastVerifyStage:
         if need > self.maxlen:
             raise ContextOverflow(_lib.FLYAI_ERANGE, f"batched decode needs {need} positions > max_ctx {self.maxlen}")
         flat = h.reshape(B * kp1, H).to(torch.bfloat16).contiguous().clone()
+        self.stage.set_graphs(use_graph)
         self.stage.forward(flat, [kp1] * B, st, list(range(B)))
         self.out = flat.view(B, kp1, H)
         return self.out

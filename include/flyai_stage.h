@@ -287,6 +287,16 @@ int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t dev_bytes, v
 int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens_host, const int32_t* starts_host,
                         const int64_t* kv_base_host, const int32_t* kv_cap_host, int32_t n_seqs,
                         uint16_t* hidden, flyai_stream_t stream);
+/* HIP-graph replay of flyai_stage_forward (the CUDA-graph capture of FastVerify.decode /
+ * BatchedFastVerify.decode, phase0/fastverify.py:221-231, phase0/batchverify.py:180-190).  When
+ * enabled, each step's kernels are one graph per (tokens, sequences, attention-plan capacity) key:
+ * captured on first use, replayed after, least recently used evicted beyond 16.  The plan
+ * capacities round the step's attention item and group counts up to multiples of 64, so steps whose
+ * KV grows within that bucket replay the same graph (kernels past the live count exit).  The
+ * caller's hidden rows are copied into a stage-owned buffer around the replay.  Off by default. */
+int flyai_stage_set_graphs(flyai_stage* st, int32_t enable);
+/* Number of graphs captured so far (tests: rebuilt only on a key change). */
+int32_t flyai_stage_graphs_captured(const flyai_stage* st);
 /* Device pointer of an internal buffer of the last step (for tests): 0 xn, 1 gemm partials, 2 q_rot,
  * 3 attn_out, 4 topk_ids, 5 topk_w, 6 offsets, 7 perm, 8 inv, 9 h_moe, 10 y_perm, 11 positions,
  * 12 seq_id, 13 cu_seqlens. */

@@ -275,3 +275,91 @@ def test_bf16_bit_helpers_roundtrip():
     ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     assert (bits == ref).all()
     assert (bf16_bits_to_f32(bits) == torch.from_numpy(x).to(torch.bfloat16).float().numpy()).all()
+
+
+# ---- a7 composition: the DeepSeek expert and MoE block ----------------------------------------
+
+def _fp8_experts(rng, n, H, I):
+    """n experts with synthetic 128x128-block e4m3 weights (std 0.05) and their dequantised fp64
+    matrices."""
+    qs, deq = {"w1": [], "s1": [], "w3": [], "s3": [], "w2": [], "s2": []}, {"w1": [], "w3": [], "w2": []}
+    for _ in range(n):
+        for name, shape in (("w1", (I, H)), ("w3", (I, H)), ("w2", (H, I))):
+            q, s = experts.fp8_block_quant_weight(rng.standard_normal(shape).astype(np.float32) * 0.05)
+            qs[name].append(q)
+            qs["s" + name[1]].append(s)
+            deq[name].append(q.astype(np.float64) * np.repeat(np.repeat(s, 128, 0), 128, 1))
+    w = experts.Fp8ExpertWeights(*(np.stack(qs[k]) for k in ("w1", "s1", "w3", "s3", "w2", "s2")))
+    return w, {k: np.stack(v) for k, v in deq.items()}
+
+
+def _silu(v):
+    return v / (1.0 + np.exp(-v))
+
+
+def _textbook_expert(x, d, e, weight=None):
+    """Unquantised fp64 SwiGLU expert on the dequantised weights: w2 . (weight * silu(w1 x) * w3 x)."""
+    h = _silu(x @ d["w1"][e].T) * (x @ d["w3"][e].T)
+    if weight is not None:
+        h = np.asarray(weight, np.float64)[:, None] * h
+    return h @ d["w2"][e].T
+
+
+def test_deepseek_expert_matches_textbook_swiglu_within_fp8_error():
+    """model.py:601-611 against an unquantised fp64 SwiGLU: the only differences are the e4m3
+    activation quantisation and bf16 roundings (a few percent per element, averaged down by the
+    dot products).  Swapping gate and up, dropping the routing weight or the silu fails it."""
+    rng = np.random.default_rng(21)
+    H, I = 256, 256
+    w, d = _fp8_experts(rng, 1, H, I)
+    x = bf16(torch.from_numpy(rng.standard_normal((6, H)).astype(np.float32))).numpy()
+    wt = np.array([0.9, 0.5, 0.25, 1.0, 0.1, 0.7], np.float32)
+    got = w.expert(0, x, wt).numpy()
+    ref = _textbook_expert(x.astype(np.float64), d, 0, wt)
+    mar, cos = metrics(got, ref)
+    assert mar < 6e-2 and cos > 0.997
+    # planted mistakes in the reference side of the comparison must not pass the same bar
+    swapped = (_silu(x @ d["w3"][0].T) * (x @ d["w1"][0].T) * wt[:, None]) @ d["w2"][0].T
+    no_weight = _textbook_expert(x.astype(np.float64), d, 0)
+    no_silu = (((x @ d["w1"][0].T) * (x @ d["w3"][0].T)) * wt[:, None]) @ d["w2"][0].T
+    for bad in (swapped, no_weight, no_silu):
+        mar_b, cos_b = metrics(got, bad)
+        assert not (mar_b < 6e-2 and cos_b > 0.997)
+
+
+def test_deepseek_moe_equals_token_major_restatement():
+    """MoE.forward (model.py:634-650) sums per expert in ascending id with torch.where rows; the same
+    block restated token by token (each token's k selected experts, then the shared expert) must give
+    the same fp32 sum to rounding of the summation order, and the unquantised textbook block must
+    agree within the fp8 error.  Catches a wrong slot/weight pairing, a dropped shared expert or a
+    scatter to the wrong token."""
+    rng = np.random.default_rng(22)
+    H, I, E, k, T = 128, 128, 6, 2, 5
+    routed, d = _fp8_experts(rng, E, H, I)
+    shared, ds = _fp8_experts(rng, 1, H, I)
+    x = bf16(torch.from_numpy(rng.standard_normal((T, H)).astype(np.float32))).numpy()
+    ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)])
+    wts = rng.uniform(0.1, 1.0, size=(T, k)).astype(np.float32)
+    got = experts.deepseek_moe(x, ids, wts, routed, shared).float().numpy()
+
+    ref = np.zeros((T, H), np.float32)
+    text = np.zeros((T, H), np.float64)
+    for t in range(T):
+        acc = np.zeros(H, np.float32)
+        for s in range(k):
+            acc += routed.expert(int(ids[t, s]), x[t:t + 1], wts[t, s:s + 1]).numpy()[0]
+            text[t] += _textbook_expert(x[t:t + 1].astype(np.float64), d, int(ids[t, s]), wts[t, s:s + 1])[0]
+        acc += shared.expert(0, x[t:t + 1]).numpy()[0]
+        text[t] += _textbook_expert(x[t:t + 1].astype(np.float64), ds, 0)[0]
+        ref[t] = acc
+    mar, cos = metrics(got, bf16(torch.from_numpy(ref)).numpy())
+    assert mar < 1e-2 and cos > 0.99999
+    mar_t, cos_t = metrics(got, text)
+    assert mar_t < 6e-2 and cos_t > 0.997
+    # a dropped shared expert or routing weights paired with the wrong slot fail the token-major bar
+    no_shared = experts.deepseek_moe(x, ids, wts, routed, experts.Fp8ExpertWeights(
+        *(np.zeros_like(a) for a in (shared.w1, shared.s1, shared.w3, shared.s3, shared.w2, shared.s2))))
+    swapped = experts.deepseek_moe(x, ids, wts[:, ::-1].copy(), routed, shared)
+    for bad in (no_shared, swapped):
+        mar_b, cos_b = metrics(bad.float().numpy(), ref)
+        assert not (mar_b < 1e-2 and cos_b > 0.99999)

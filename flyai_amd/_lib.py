@@ -81,6 +81,7 @@ _PROTOS = {
     "flyai_stage_host_staging_bytes": (SZ, [P]),
     "flyai_stage_set_workspace": (C.c_int, [P, P, SZ, P, SZ]),
     "flyai_stage_forward": (C.c_int, [P, P, P, P, P, I32, P, P]),
+    "flyai_stage_forward_tree": (C.c_int, [P, I32, I32, P, P, I64, I32, P, P]),
     "flyai_stage_debug_buffer": (P, [P, I32]),
     "flyai_stage_set_graphs": (C.c_int, [P, I32]),
     "flyai_stage_graphs_captured": (I32, [P]),

@@ -64,14 +64,19 @@ __device__ __forceinline__ void load_v_tile(uint4 (&v)[4][2], const uint16_t* __
 }
 
 // QT query-row tiles of 16 (QT = 1: up to 2 tokens; QT = 2: up to 4 tokens).
-template <int QT>
+// TREE: the batch is one tree-verify sequence; token (= node) i sits at position
+// tree->start + depth[i] (dep_s: the depths, staged in LDS) and sees the committed keys below
+// tree->start plus the tree slots of its ancestor set (FastVerify._tset masks).
+template <int QT, bool TREE>
 __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_idx,
                                           const uint16_t* __restrict__ q,
                                           const uint16_t* __restrict__ k_pool,
                                           const uint16_t* __restrict__ v_pool,
                                           const int64_t* __restrict__ kv_base,
                                           const int32_t* __restrict__ kv_cap, int window, int Hq,
-                                          float* __restrict__ partials) {
+                                          float* __restrict__ partials,
+                                          const flyai_attn_tree* __restrict__ tree,
+                                          const int* __restrict__ dep_s) {
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
   const int cap = kv_cap[it.seq];
@@ -84,12 +89,24 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
   bf16x8_t qf[QT][2];
   int qpos[QT];
   bool qval[QT];
+  int qdep[QT];        // TREE: the row's node depth and ancestor set
+  uint64_t qanc[QT];
+  const int tstart = TREE ? tree->start : 0;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int rq = 16 * qt + n;
     const int ti = rq >> 3;
     qval[qt] = ti < it.ntok;
-    qpos[qt] = it.pos0 + ti;
+    if (TREE) {
+      const int node = (it.tok + ti) & 63;  // < n_nodes <= 64 for every valid row
+      qdep[qt] = qval[qt] ? dep_s[node] : 0;
+      qanc[qt] = qval[qt] ? tree->ancestors[node] : 0ull;
+      qpos[qt] = tstart + qdep[qt];
+    } else {
+      qdep[qt] = 0;
+      qanc[qt] = 0ull;
+      qpos[qt] = it.pos0 + ti;
+    }
     uint4 a = make_uint4(0, 0, 0, 0), b2 = make_uint4(0, 0, 0, 0);
     if (qval[qt]) {
       const uint16_t* qp = q + ((size_t)(it.tok + ti) * Hq + it.kv_head * 8 + (rq & 7)) * 64 + 8 * g;
@@ -111,9 +128,18 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
 
   const int kb_first = it.key_lo & ~63;
   // Blocks fully inside every valid query row's key range need no score mask (wave-uniform test).
-  const int pos_last = it.pos0 + it.ntok - 1;
+  // In a tree only committed keys (below tree->start) can be unmasked for every row.
+  int pos_last, int_hi;
+  if (TREE) {
+    int dmax = 0;
+    for (int i = 0; i < it.ntok; ++i) dmax = max(dmax, dep_s[(it.tok + i) & 63]);
+    pos_last = tstart + dmax;
+    int_hi = min(it.key_hi - 1, tstart - 1);
+  } else {
+    pos_last = it.pos0 + it.ntok - 1;
+    int_hi = min(it.key_hi - 1, it.pos0);
+  }
   const int int_lo = max(it.key_lo, window > 0 ? pos_last - window + 1 : 0);
-  const int int_hi = min(it.key_hi - 1, it.pos0);
   uint4 kc[4][2], kn[4][2], vv[4][2];
   load_k_tile(kc, K, kb_first, n, g);
   for (int kb = kb_first; kb < it.key_hi; kb += 64) {
@@ -148,7 +174,19 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
 #pragma unroll
           for (int v = 0; v < 4; ++v) {
             const int key = kb + tile_key(kt, 4 * g + v);
-            const bool ok = qval[qt] && key >= lo && key <= hi;
+            bool ok;
+            if (TREE) {
+              if (key < tstart) {
+                ok = key >= lo && key < it.key_hi;  // committed prefix (window on positions)
+              } else {
+                const int j = (key - tstart) & 63;  // in range whenever key < key_hi <= start + n
+                ok = key >= it.key_lo && key < it.key_hi && ((qanc[qt] >> j) & 1ull) &&
+                     (window == 0 || qdep[qt] - dep_s[j] < window);
+              }
+              ok = ok && qval[qt];
+            } else {
+              ok = qval[qt] && key >= lo && key <= hi;
+            }
             s[kt][v] = ok ? s[kt][v] * scale : -INFINITY;
             bmax = fmaxf(bmax, s[kt][v]);
           }
@@ -213,20 +251,31 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
   }
 }
 
-// One launch for every item; the body is chosen per item (uniform across the wave).
+// One launch for every item; the body is chosen per item (uniform across the wave).  tree != NULL:
+// the batch is one tree-verify sequence (flyai_stage_forward_tree).
 __global__ __launch_bounds__(64, 2) void attn_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
     const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
     const int32_t* __restrict__ kv_cap, int window, int Hq,
     const flyai_attn_item* __restrict__ items, const int32_t* __restrict__ n_live,
-    float* __restrict__ partials) {
+    float* __restrict__ partials, const flyai_attn_tree* __restrict__ tree) {
+  __shared__ int dep_s[64];
   // a graph-replayed step launches the plan's capacity; items past this step's count exit
   if (n_live && (int)blockIdx.x >= *n_live) return;
   const flyai_attn_item it = items[blockIdx.x];
+  if (tree) {
+    dep_s[threadIdx.x] = (int)threadIdx.x < tree->n_nodes ? tree->depth[threadIdx.x] : 0;
+    __syncthreads();
+    if (it.ntok <= 2)
+      attn_item<1, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, tree, dep_s);
+    else
+      attn_item<2, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, tree, dep_s);
+    return;
+  }
   if (it.ntok <= 2)
-    attn_item<1>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials);
+    attn_item<1, false>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, nullptr, nullptr);
   else
-    attn_item<2>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials);
+    attn_item<2, false>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, nullptr, nullptr);
 }
 
 // Merge: per query row, M = max(sink, max_s m_s), L = e^(sink-M) + sum_s l_s e^(m_s-M),
@@ -270,11 +319,11 @@ int launch_attn(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_poo
                 const int64_t* kv_base, const int32_t* kv_cap, const float* sinks, int window,
                 int Hq, const flyai_attn_item* items, int n_items, int n_small,
                 const flyai_attn_group* groups, int n_groups, const int32_t* counts, float* partials,
-                uint16_t* out, hipStream_t s) {
+                uint16_t* out, const flyai_attn_tree* tree, hipStream_t s) {
   if (n_items == 0) return FLYAI_OK;
   (void)n_small;  // the plan's two ranges share one launch
   hipLaunchKernelGGL(attn_partial_kernel, dim3(n_items), dim3(64), 0, s, q, k_pool, v_pool, kv_base,
-                     kv_cap, window, Hq, items, counts, partials);
+                     kv_cap, window, Hq, items, counts, partials, tree);
   int rc = check_launch("attn_partial");
   if (rc) return rc;
   hipLaunchKernelGGL(attn_merge_kernel, dim3(n_groups), dim3(256), 0, s, partials, groups, sinks,
@@ -336,6 +385,56 @@ int attn_plan(const int32_t* q_lens, const int32_t* starts, int S, int Hkv, int 
   return FLYAI_OK;
 }
 
+// Tree-verify plan: the n nodes of one sequence (seq 0, tokens 0..n-1) in groups of <= 4
+// consecutive nodes; every group's keys run to start + n (the ancestor mask picks the tree slots),
+// and from the window start of its shallowest node on sliding layers.
+int attn_plan_tree(const flyai_attn_tree& tr, int Hkv, int window, int split_keys,
+                   flyai_attn_item* items, int max_items, flyai_attn_group* groups, int max_groups,
+                   int* n_items, int* n_groups, int* n_small) {
+  int ni = 0, ng = 0;
+  const int n = tr.n_nodes, st = tr.start;
+  for (int i0 = 0; i0 < n; i0 += 4) {
+    const int nt = n - i0 < 4 ? n - i0 : 4;
+    int dmin = tr.depth[i0];
+    for (int i = 1; i < nt; ++i) dmin = tr.depth[i0 + i] < dmin ? tr.depth[i0 + i] : dmin;
+    const int p_first = st + dmin;
+    const int key_hi = st + n;
+    const int key_lo = window > 0 ? (p_first - window + 1 > 0 ? p_first - window + 1 : 0) : 0;
+    const int kb0 = key_lo & ~63;
+    const int nsplit = (key_hi - kb0 + split_keys - 1) / split_keys;
+    for (int g = 0; g < Hkv; ++g) {
+      if (ng >= max_groups || ni + nsplit > max_items)
+        return set_error(FLYAI_ERANGE, "tree attention plan exceeds capacity (%d items, %d groups)",
+                         max_items, max_groups);
+      flyai_attn_group& gr = groups[ng];
+      gr.first_item = ni;
+      gr.n_splits = nsplit;
+      gr.tok = i0;
+      gr.ntok = nt;
+      gr.kv_head = g;
+      gr.pad[0] = gr.pad[1] = gr.pad[2] = 0;
+      for (int sp = 0; sp < nsplit; ++sp) {
+        flyai_attn_item& it = items[ni++];
+        it.seq = 0;
+        it.kv_head = g;
+        it.tok = i0;
+        it.ntok = nt;
+        it.pos0 = p_first;
+        const int lo = kb0 + sp * split_keys;
+        it.key_lo = lo > key_lo ? lo : key_lo;
+        const int hi = kb0 + (sp + 1) * split_keys;
+        it.key_hi = hi < key_hi ? hi : key_hi;
+        it.group = ng;
+      }
+      ++ng;
+    }
+  }
+  *n_items = ni;
+  *n_groups = ng;
+  *n_small = 0;
+  return FLYAI_OK;
+}
+
 }  // namespace flyai
 
 using namespace flyai;
@@ -375,5 +474,6 @@ extern "C" int flyai_attn_ragged(const uint16_t* q, const uint16_t* k_pool, cons
                     (n_items == 0 || (items_dev && groups_dev && partials)),
                 "attn: null pointer");
   return launch_attn(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, items_dev, n_items,
-                     n_items_small, groups_dev, n_groups, nullptr, partials, out, as_stream(stream));
+                     n_items_small, groups_dev, n_groups, nullptr, partials, out, nullptr,
+                     as_stream(stream));
 }

@@ -49,13 +49,18 @@ int launch_topk_permute(const float*, int, int, int, int32_t*, float*, int32_t*,
                         int32_t*, hipStream_t);
 int launch_qkv_rope_kv(const uint16_t*, const uint16_t*, const uint16_t*, float*, const int32_t*,
                        const int32_t*, const uint16_t*, const uint16_t*, int, int, int, int, int, int,
-                       const int64_t*, const int32_t*, uint16_t*, uint16_t*, uint16_t*, hipStream_t);
+                       const int64_t*, const int32_t*, uint16_t*, uint16_t*, uint16_t*, const int32_t*,
+                       hipStream_t);
 size_t linear_partials_bytes(int M, int N, int K);
 int launch_attn(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
                 const float*, int, int, const flyai_attn_item*, int, int, const flyai_attn_group*, int,
-                const int32_t*, float*, uint16_t*, hipStream_t);
+                const int32_t*, float*, uint16_t*, const flyai_attn_tree*, hipStream_t);
 int attn_plan(const int32_t*, const int32_t*, int, int, int, int, flyai_attn_item*, int,
               flyai_attn_group*, int, int*, int*, int*);
+int attn_plan_tree(const flyai_attn_tree&, int, int, int, flyai_attn_item*, int, flyai_attn_group*, int,
+                   int*, int*, int*);
+int launch_pack(const int32_t*, const int32_t*, const int64_t*, const int32_t*, int, int, int, int32_t*,
+                int32_t*, int32_t*, int32_t*, int64_t*, int32_t*, const int32_t*, int32_t*, hipStream_t);
 
 }  // namespace flyai
 
@@ -83,7 +88,7 @@ struct flyai_stage {
   const uint16_t* cos_tab = nullptr;
   const uint16_t* sin_tab = nullptr;
   // device workspace offsets; o_blob holds the per-step batch blob copied from the host
-  size_t o_blob, blob_max, o_cu, o_pos, o_sid, o_kvlen, o_slot, o_status;
+  size_t o_blob, blob_max, o_cu, o_pos, o_sid, o_kvlen, o_slot, o_status, o_kvpos;
   size_t o_xn, o_gemm, o_qrot, o_attn, o_parts;
   size_t o_ids, o_w, o_logits, o_hist, o_off, o_perm, o_inv, o_hmoe, o_y;
   size_t o_h2;  // the post-attention residual stream of the decode-sized path
@@ -117,7 +122,8 @@ static constexpr int kPlanBucket = 64;  // attention plan capacities round up to
 static size_t blob_bytes(int S, int n_items0, int n_items1, int n_groups0, int n_groups1) {
   return align256(4 * sizeof(int32_t)) + align256((size_t)S * 4) * 3 + align256((size_t)S * 8) +
          align256((size_t)n_items0 * sizeof(flyai_attn_item)) + align256((size_t)n_items1 * sizeof(flyai_attn_item)) +
-         align256((size_t)n_groups0 * sizeof(flyai_attn_group)) + align256((size_t)n_groups1 * sizeof(flyai_attn_group));
+         align256((size_t)n_groups0 * sizeof(flyai_attn_group)) + align256((size_t)n_groups1 * sizeof(flyai_attn_group)) +
+         align256(sizeof(flyai_attn_tree));
 }
 
 static void layout(flyai_stage* st) {
@@ -132,6 +138,7 @@ static void layout(flyai_stage* st) {
   st->o_kvlen = d.take(S * 4);
   st->o_slot = d.take(T * 8);
   st->o_status = d.take(4);
+  st->o_kvpos = d.take(T * 4);
   st->o_xn = d.take(T * c.hidden * 2);
   {
     const size_t a = linear_partials_bytes(c.max_tokens, st->qkv_width, c.hidden);
@@ -277,6 +284,8 @@ struct StepPlan {
   int grid_items[2], grid_groups[2];  // launch sizes: exact counts, or the plan capacities (graphs)
   int n_small[2];
   size_t off_counts, off_q, off_st, off_cap, off_base, off_items[2], off_groups[2];
+  bool tree = false;  // a tree-verify step: the blob carries the flyai_attn_tree at off_tree
+  size_t off_tree = 0;
 };
 }  // namespace
 
@@ -292,13 +301,14 @@ static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* count
   auto B16 = [&](size_t o) { return reinterpret_cast<uint16_t*>(d + o); };
   const int64_t* base_d = reinterpret_cast<const int64_t*>(blob + sp.off_base);
   const int32_t* cap_d = reinterpret_cast<const int32_t*>(blob + sp.off_cap);
-  flyai_stream_t stream = reinterpret_cast<flyai_stream_t>(s);
+  const flyai_attn_tree* tree_d = sp.tree ? reinterpret_cast<const flyai_attn_tree*>(blob + sp.off_tree) : nullptr;
+  const int32_t* kv_pos = sp.tree ? I32(st->o_kvpos) : nullptr;
 
-  RUN(flyai_pack_ragged(reinterpret_cast<const int32_t*>(blob + sp.off_q),
-                        reinterpret_cast<const int32_t*>(blob + sp.off_st), base_d, cap_d, sp.S, c.head_dim,
-                        c.max_tokens, I32(st->o_cu), I32(st->o_pos), I32(st->o_sid),
-                        I32(st->o_kvlen), reinterpret_cast<int64_t*>(d + st->o_slot),
-                        I32(st->o_status), stream));
+  RUN(launch_pack(reinterpret_cast<const int32_t*>(blob + sp.off_q),
+                  reinterpret_cast<const int32_t*>(blob + sp.off_st), base_d, cap_d, sp.S, c.head_dim,
+                  c.max_tokens, I32(st->o_cu), I32(st->o_pos), I32(st->o_sid), I32(st->o_kvlen),
+                  reinterpret_cast<int64_t*>(d + st->o_slot), I32(st->o_status),
+                  tree_d ? tree_d->depth : nullptr, I32(st->o_kvpos), s));
   const int Tn = sp.Tn;
   const int H = c.hidden, E = c.n_experts, k = c.top_k, I = c.intermediate;
   const bool fused_route = Tn <= 256 && Tn * k <= 4096;
@@ -310,13 +320,13 @@ static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* count
     RUN(launch_qkv_rope_kv(B16(st->o_xn), L.wqkv, L.bqkv, F32(st->o_gemm), I32(st->o_pos),
                            I32(st->o_sid), st->cos_tab, st->sin_tab, c.rope_positions, Tn, H,
                            c.n_q_heads, c.n_kv_heads, c.head_dim, base_d, cap_d, B16(st->o_qrot),
-                           L.k_pool, L.v_pool, s));
+                           L.k_pool, L.v_pool, kv_pos, s));
     RUN(launch_attn(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks,
                     L.sliding ? c.window : 0, c.n_q_heads,
                     reinterpret_cast<const flyai_attn_item*>(blob + sp.off_items[p]), sp.grid_items[p],
                     sp.n_small[p], reinterpret_cast<const flyai_attn_group*>(blob + sp.off_groups[p]),
                     sp.grid_groups[p], counts ? counts + 2 * p : nullptr, F32(st->o_parts),
-                    B16(st->o_attn), s));
+                    B16(st->o_attn), tree_d, s));
     if (fused_route) {
       // decode-sized: o-proj finalize + residual + RMSNorm + router logits, then top-k + permute
       RUN(launch_linear_residual_rmsnorm_logits(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
@@ -404,6 +414,46 @@ extern "C" int flyai_stage_set_graphs(flyai_stage* st, int32_t enable) {
 
 extern "C" int32_t flyai_stage_graphs_captured(const flyai_stage* st) { return st ? st->graphs_captured : 0; }
 
+// One compact blob per step: live counts | q_lens | starts | kv_cap | kv_base | items x2 | groups x2
+// [| tree], staged through the double-buffered pinned halves and copied with one H2D copy.
+static int stage_blob(flyai_stage* st, StepPlan& sp, const int32_t* q_lens, const int32_t* starts,
+                      const int64_t* kv_base, const int32_t* kv_cap, const int* n_items,
+                      const int* n_groups, const flyai_attn_tree* tree, hipStream_t s) {
+  const int S = sp.S;
+  Carve b;
+  sp.off_counts = b.take(4 * sizeof(int32_t));
+  sp.off_q = b.take((size_t)S * 4);
+  sp.off_st = b.take((size_t)S * 4);
+  sp.off_cap = b.take((size_t)S * 4);
+  sp.off_base = b.take((size_t)S * 8);
+  for (int p = 0; p < 2; ++p) sp.off_items[p] = b.take((size_t)sp.grid_items[p] * sizeof(flyai_attn_item));
+  for (int p = 0; p < 2; ++p) sp.off_groups[p] = b.take((size_t)sp.grid_groups[p] * sizeof(flyai_attn_group));
+  sp.tree = tree != nullptr;
+  if (tree) sp.off_tree = b.take(sizeof(flyai_attn_tree));
+  if (b.off > st->blob_max) return set_error(FLYAI_ERANGE, "batch blob exceeds its reservation");
+  // wait until the GPU consumed this staging half's previous contents, then fill it
+  const int h = st->half;
+  st->half ^= 1;
+  const hipError_t ew = hipEventSynchronize(st->staged[h]);
+  if (ew != hipSuccess) return hip_fail("hipEventSynchronize", ew);
+  char* hb = st->host + h * st->host_half;
+  const int32_t counts[4] = {n_items[0], n_groups[0], n_items[1], n_groups[1]};
+  memcpy(hb + sp.off_counts, counts, sizeof(counts));
+  memcpy(hb + sp.off_q, q_lens, S * 4);
+  memcpy(hb + sp.off_st, starts, S * 4);
+  memcpy(hb + sp.off_cap, kv_cap, S * 4);
+  memcpy(hb + sp.off_base, kv_base, S * 8);
+  for (int p = 0; p < 2; ++p) {
+    memcpy(hb + sp.off_items[p], st->plan_items[p].data(), n_items[p] * sizeof(flyai_attn_item));
+    memcpy(hb + sp.off_groups[p], st->plan_groups[p].data(), n_groups[p] * sizeof(flyai_attn_group));
+  }
+  if (tree) memcpy(hb + sp.off_tree, tree, sizeof(flyai_attn_tree));
+  RUN(copy_h2d(st->dev + st->o_blob, hb, b.off, s));
+  const hipError_t er = hipEventRecord(st->staged[h], s);
+  if (er != hipSuccess) return hip_fail("hipEventRecord", er);
+  return FLYAI_OK;
+}
+
 extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const int32_t* starts,
                                    const int64_t* kv_base, const int32_t* kv_cap, int32_t S,
                                    uint16_t* hidden, flyai_stream_t stream) {
@@ -447,37 +497,7 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
     sp.grid_items[p] = st->graphs ? bucket(n_items[p], c.max_attn_items) : n_items[p];
     sp.grid_groups[p] = st->graphs ? bucket(n_groups[p], st->max_groups) : n_groups[p];
   }
-  // one compact blob per step: live counts | q_lens | starts | kv_cap | kv_base | items x2 | groups x2
-  {
-    Carve b;
-    sp.off_counts = b.take(4 * sizeof(int32_t));
-    sp.off_q = b.take((size_t)S * 4);
-    sp.off_st = b.take((size_t)S * 4);
-    sp.off_cap = b.take((size_t)S * 4);
-    sp.off_base = b.take((size_t)S * 8);
-    for (int p = 0; p < 2; ++p) sp.off_items[p] = b.take((size_t)sp.grid_items[p] * sizeof(flyai_attn_item));
-    for (int p = 0; p < 2; ++p) sp.off_groups[p] = b.take((size_t)sp.grid_groups[p] * sizeof(flyai_attn_group));
-    if (b.off > st->blob_max) return set_error(FLYAI_ERANGE, "batch blob exceeds its reservation");
-    // wait until the GPU consumed this staging half's previous contents, then fill it
-    const int h = st->half;
-    st->half ^= 1;
-    const hipError_t ew = hipEventSynchronize(st->staged[h]);
-    if (ew != hipSuccess) return hip_fail("hipEventSynchronize", ew);
-    char* hb = st->host + h * st->host_half;
-    const int32_t counts[4] = {n_items[0], n_groups[0], n_items[1], n_groups[1]};
-    memcpy(hb + sp.off_counts, counts, sizeof(counts));
-    memcpy(hb + sp.off_q, q_lens, S * 4);
-    memcpy(hb + sp.off_st, starts, S * 4);
-    memcpy(hb + sp.off_cap, kv_cap, S * 4);
-    memcpy(hb + sp.off_base, kv_base, S * 8);
-    for (int p = 0; p < 2; ++p) {
-      memcpy(hb + sp.off_items[p], st->plan_items[p].data(), n_items[p] * sizeof(flyai_attn_item));
-      memcpy(hb + sp.off_groups[p], st->plan_groups[p].data(), n_groups[p] * sizeof(flyai_attn_group));
-    }
-    RUN(copy_h2d(st->dev + st->o_blob, hb, b.off, s));
-    const hipError_t er = hipEventRecord(st->staged[h], s);
-    if (er != hipSuccess) return hip_fail("hipEventRecord", er);
-  }
+  RUN(stage_blob(st, sp, q_lens, starts, kv_base, kv_cap, n_items, n_groups, nullptr, s));
   if (!st->graphs) return record_step(st, sp, nullptr, hidden, s);
 
   hipGraphExec_t exec = nullptr;
@@ -492,4 +512,63 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
   e = hipMemcpyAsync(hidden, hs, hb, hipMemcpyDeviceToDevice, s);
   if (e != hipSuccess) return hip_fail("hipMemcpyAsync", e);
   return FLYAI_OK;
+}
+
+
+extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t n, const int32_t* parent,
+                                        const int32_t* depth, int64_t kv_base, int32_t kv_cap,
+                                        uint16_t* hidden, flyai_stream_t stream) {
+  FLYAI_REQUIRE(st && parent && depth && hidden, "forward_tree: null pointer");
+  FLYAI_REQUIRE(st->dev && st->host, "forward_tree: workspace not set");
+  FLYAI_REQUIRE(st->cos_tab && st->sin_tab, "forward_tree: rope tables not set");
+  const flyai_stage_config& c = st->cfg;
+  FLYAI_REQUIRE(n >= 1 && n <= 64, "forward_tree: tree size %d outside [1, 64]", n);
+  FLYAI_REQUIRE(n <= c.max_tokens, "forward_tree: %d nodes > max_tokens %d", n, c.max_tokens);
+  FLYAI_REQUIRE(start >= 0 && kv_cap > 0 && kv_cap % 64 == 0 && kv_base >= 0 && kv_base % 8 == 0,
+                "forward_tree: needs start >= 0, kv_cap %% 64 == 0 and kv_base %% 8 == 0");
+  // validate_tree (phase0/fastverify.py:29-49): parents in range and not self, depths consistent,
+  // which forces acyclicity -- checked before any parent walk
+  for (int i = 0; i < n; ++i) {
+    FLYAI_REQUIRE(parent[i] >= -1 && parent[i] < n && parent[i] != i,
+                  "forward_tree: tree node %d: parent %d out of range [-1, %d)", i, parent[i], n);
+    FLYAI_REQUIRE(depth[i] >= 0, "forward_tree: tree node %d: depth %d invalid", i, depth[i]);
+  }
+  for (int i = 0; i < n; ++i) {
+    const int want = parent[i] == -1 ? 0 : depth[parent[i]] + 1;
+    FLYAI_REQUIRE(depth[i] == want, "forward_tree: tree node %d: depth %d != %d (parent %d; cycle or bad depth)",
+                  i, depth[i], want, parent[i]);
+  }
+  const int64_t need = (int64_t)start + n;
+  if (need > kv_cap)
+    return set_error(FLYAI_ERANGE, "tree decode needs %lld positions > KV capacity %d", (long long)need, kv_cap);
+  if (need > c.rope_positions)
+    return set_error(FLYAI_ERANGE, "tree decode needs %lld positions > rope table %d", (long long)need,
+                     c.rope_positions);
+  for (int l = 0; l < c.n_layers; ++l)
+    FLYAI_REQUIRE(st->layers[l].wqkv, "forward_tree: layer %d not bound", l);
+  flyai_attn_tree tree;
+  memset(&tree, 0, sizeof(tree));
+  tree.start = start;
+  tree.n_nodes = n;
+  for (int i = 0; i < n; ++i) {
+    tree.depth[i] = depth[i];
+    uint64_t a = 0;
+    for (int j = i; j != -1; j = parent[j]) a |= 1ull << j;  // ends: depth falls along the walk
+    tree.ancestors[i] = a;
+  }
+  hipStream_t s = as_stream(stream);
+  StepPlan sp;
+  sp.Tn = n;
+  sp.S = 1;
+  int n_items[2], n_groups[2];
+  for (int p = 0; p < 2; ++p) {
+    RUN(attn_plan_tree(tree, c.n_kv_heads, p == 0 ? 0 : c.window, c.attn_split_keys, st->plan_items[p].data(),
+                       c.max_attn_items, st->plan_groups[p].data(), st->max_groups, &n_items[p],
+                       &n_groups[p], &sp.n_small[p]));
+    sp.grid_items[p] = n_items[p];
+    sp.grid_groups[p] = n_groups[p];
+  }
+  const int32_t q_len = n, st0 = start;
+  RUN(stage_blob(st, sp, &q_len, &st0, &kv_base, &kv_cap, n_items, n_groups, &tree, s));
+  return record_step(st, sp, nullptr, hidden, s);
 }

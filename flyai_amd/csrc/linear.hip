@@ -334,13 +334,15 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(
     const int32_t* __restrict__ seq_id, const uint16_t* __restrict__ cos_tab,
     const uint16_t* __restrict__ sin_tab, int rope_positions, int Hq, int Hkv, int D,
     const int64_t* __restrict__ kv_base, const int32_t* __restrict__ kv_cap,
-    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool) {
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
+    const int32_t* __restrict__ kv_pos) {
   const int t = blockIdx.x;
   const int pos = positions[t];
   if (pos < 0 || pos >= rope_positions) return;  // outside the rotary table: no read, no write
   const int b = seq_id[t];
   const int cap = kv_cap[b];
-  const bool in_cap = pos < cap;
+  const int slot = kv_pos ? kv_pos[t] : pos;  // tree verify writes node i at its own slot
+  const bool in_cap = slot >= 0 && slot < cap;
   const int64_t base = kv_base[b];
   const int D2 = D / 2;
   const int width = (Hq + 2 * Hkv) * D;
@@ -365,7 +367,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(
       q_out[((size_t)t * Hq + h) * D + d + D2] = f2bf(second);
     } else if (in_cap) {
       const int gk = h - Hq;
-      uint16_t* kp = k_pool + base + ((size_t)gk * cap + pos) * D;
+      uint16_t* kp = k_pool + base + ((size_t)gk * cap + slot) * D;
       kp[d] = f2bf(first);
       kp[d + D2] = f2bf(second);
     }
@@ -373,7 +375,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(
   if (in_cap) {
     for (int i = tid; i < Hkv * D; i += nthr) {
       const int gv = i / D, d = i % D;
-      v_pool[base + ((size_t)gv * D + d) * cap + pos] = f2bf(val((Hq + Hkv) * D + gv * D + d));
+      v_pool[base + ((size_t)gv * D + d) * cap + slot] = f2bf(val((Hq + Hkv) * D + gv * D + d));
     }
   }
 }
@@ -388,7 +390,8 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_vec_kernel(
     const int32_t* __restrict__ positions, const int32_t* __restrict__ seq_id,
     const uint16_t* __restrict__ cos_tab, const uint16_t* __restrict__ sin_tab, int rope_positions,
     int Hq, int Hkv, int D, const int64_t* __restrict__ kv_base, const int32_t* __restrict__ kv_cap,
-    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool) {
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
+    const int32_t* __restrict__ kv_pos) {
   const int t = blockIdx.x;
   const int u = blockIdx.y * blockDim.x + threadIdx.x;
   const int D2 = D / 2, Q2 = D2 / 4, QV = D / 4;
@@ -398,7 +401,9 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_vec_kernel(
   if (pos < 0 || pos >= rope_positions) return;  // outside the rotary table: no read, no write
   const int b = seq_id[t];
   const int cap = kv_cap[b];
-  const bool in_cap = pos < cap;
+  // the K/V slot: the position itself, or the tree node's slot in tree verify
+  const int slot = kv_pos ? kv_pos[t] : pos;
+  const bool in_cap = slot >= 0 && slot < cap;
   const int64_t base = kv_base[b];
   const int width = (Hq + 2 * Hkv) * D;
   const size_t stride = (size_t)M * width;
@@ -432,7 +437,7 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_vec_kernel(
       second[j] = f2bf(bf16_round(bf16_round(x2[j] * c) + bf16_round(x1[j] * sn)));
     }
     uint16_t* dst = h < Hq ? q_out + ((size_t)t * Hq + h) * D
-                           : k_pool + base + ((size_t)(h - Hq) * cap + pos) * D;
+                           : k_pool + base + ((size_t)(h - Hq) * cap + slot) * D;
     *reinterpret_cast<uint2*>(dst + d0) = make_uint2(first[0] | ((uint32_t)first[1] << 16),
                                                      first[2] | ((uint32_t)first[3] << 16));
     *reinterpret_cast<uint2*>(dst + d0 + D2) = make_uint2(second[0] | ((uint32_t)second[1] << 16),
@@ -442,7 +447,7 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_vec_kernel(
     float o[4];
     sum4((Hq + Hkv) * D + gv * D + d0, o);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v_pool[base + ((size_t)gv * D + d0 + j) * cap + pos] = f2bf(o[j]);
+    for (int j = 0; j < 4; ++j) v_pool[base + ((size_t)gv * D + d0 + j) * cap + slot] = f2bf(o[j]);
   }
 }
 
@@ -453,16 +458,17 @@ int launch_rope_kv(const uint16_t* qkv, const int32_t* positions, const int32_t*
   if (T == 0) return FLYAI_OK;
   hipLaunchKernelGGL(rope_kv_append_kernel<false>, dim3(T), dim3(256), 0, s, qkv, nullptr, 0, T,
                      nullptr, positions, seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base,
-                     kv_cap, q_out, k_pool, v_pool);
+                     kv_cap, q_out, k_pool, v_pool, nullptr);
   return check_launch("rope_kv_append");
 }
 
-// QKV projection + RoPE + KV append: split-K GEMM, then the fused finalize
+// QKV projection + RoPE + KV append: split-K GEMM, then the fused finalize.  kv_pos (nullable) gives
+// each token's K/V slot when it differs from its rotary position (tree verify).
 int launch_qkv_rope_kv(const uint16_t* x, const uint16_t* Wqkv, const uint16_t* bqkv, float* part,
                        const int32_t* positions, const int32_t* seq_id, const uint16_t* cos_tab,
                        const uint16_t* sin_tab, int rope_positions, int T, int H, int Hq, int Hkv,
                        int D, const int64_t* kv_base, const int32_t* kv_cap, uint16_t* q_out,
-                       uint16_t* k_pool, uint16_t* v_pool, hipStream_t s) {
+                       uint16_t* k_pool, uint16_t* v_pool, const int32_t* kv_pos, hipStream_t s) {
   if (T == 0) return FLYAI_OK;
   const int width = (Hq + 2 * Hkv) * D;
   int rc = launch_gemm_splitk(x, Wqkv, T, width, H, part, s);
@@ -474,15 +480,15 @@ int launch_qkv_rope_kv(const uint16_t* x, const uint16_t* Wqkv, const uint16_t* 
     if (slices <= 8)
       hipLaunchKernelGGL(qkv_rope_kv_vec_kernel<8>, grid, dim3(256), 0, s, part, slices, T, bqkv, positions,
                          seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base, kv_cap, q_out,
-                         k_pool, v_pool);
+                         k_pool, v_pool, kv_pos);
     else
       hipLaunchKernelGGL(qkv_rope_kv_vec_kernel<16>, grid, dim3(256), 0, s, part, slices, T, bqkv, positions,
                          seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base, kv_cap, q_out,
-                         k_pool, v_pool);
+                         k_pool, v_pool, kv_pos);
   } else {
     hipLaunchKernelGGL(rope_kv_append_kernel<true>, dim3(T, 4), dim3(256), 0, s, nullptr, part, slices, T,
                        bqkv, positions, seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base,
-                       kv_cap, q_out, k_pool, v_pool);
+                       kv_cap, q_out, k_pool, v_pool, kv_pos);
   }
   return check_launch("qkv_rope_kv_append");
 }

@@ -8,12 +8,16 @@ constexpr int kPackMaxSeqs = 8192;
 
 // One workgroup: block-wide exclusive scan of q_lens into cu_seqlens (LDS), then every thread
 // walks tokens with a binary search over the scanned offsets.
+// Tree verify (tree_depth != NULL, one sequence): token i is rotated at position
+// starts[0] + tree_depth[i] but its K/V goes to slot starts[0] + i; kv_pos receives the slot
+// positions (it is only written in that mode).
 __global__ __launch_bounds__(kPackThreads) void pack_ragged_kernel(
     const int32_t* __restrict__ q_lens, const int32_t* __restrict__ starts,
     const int64_t* __restrict__ kv_base, const int32_t* __restrict__ kv_cap, int S, int head_dim,
     int max_tokens, int32_t* __restrict__ cu_out, int32_t* __restrict__ positions,
     int32_t* __restrict__ seq_id, int32_t* __restrict__ kv_len, int64_t* __restrict__ kv_slot,
-    int32_t* __restrict__ status) {
+    int32_t* __restrict__ status, const int32_t* __restrict__ tree_depth,
+    int32_t* __restrict__ kv_pos) {
   __shared__ int32_t cu[kPackMaxSeqs + 1];
   __shared__ int32_t wave_tot[kPackThreads / 64];
   const int tid = threadIdx.x;
@@ -67,10 +71,11 @@ __global__ __launch_bounds__(kPackThreads) void pack_ragged_kernel(
       if (cu[mid] <= t) lo = mid; else hi = mid - 1;
     }
     const int b = lo;
-    const int pos = starts[b] + (t - cu[b]);
-    positions[t] = pos;
+    const int slot_pos = starts[b] + (t - cu[b]);
+    positions[t] = tree_depth ? starts[b] + tree_depth[t] : slot_pos;
+    if (tree_depth) kv_pos[t] = slot_pos;
     seq_id[t] = b;
-    kv_slot[t] = (pos < kv_cap[b]) ? kv_base[b] + (int64_t)pos * head_dim : (int64_t)-1;
+    kv_slot[t] = (slot_pos < kv_cap[b]) ? kv_base[b] + (int64_t)slot_pos * head_dim : (int64_t)-1;
   }
 }
 
@@ -91,6 +96,20 @@ extern "C" int flyai_pack_ragged(const int32_t* q_lens, const int32_t* starts,
                 "pack: null pointer");
   hipLaunchKernelGGL(pack_ragged_kernel, dim3(1), dim3(kPackThreads), 0, as_stream(stream),
                      q_lens, starts, kv_base, kv_cap, n_seqs, head_dim, max_tokens, cu_seqlens,
-                     positions, seq_id, kv_len, kv_slot, status_dev);
+                     positions, seq_id, kv_len, kv_slot, status_dev, nullptr, nullptr);
   return check_launch("pack_ragged");
 }
+
+namespace flyai {
+
+int launch_pack(const int32_t* q_lens, const int32_t* starts, const int64_t* kv_base,
+                const int32_t* kv_cap, int S, int head_dim, int max_tokens, int32_t* cu,
+                int32_t* positions, int32_t* seq_id, int32_t* kv_len, int64_t* kv_slot,
+                int32_t* status, const int32_t* tree_depth, int32_t* kv_pos, hipStream_t s) {
+  hipLaunchKernelGGL(pack_ragged_kernel, dim3(1), dim3(kPackThreads), 0, s, q_lens, starts, kv_base,
+                     kv_cap, S, head_dim, max_tokens, cu, positions, seq_id, kv_len, kv_slot, status,
+                     tree_depth, kv_pos);
+  return check_launch("pack_ragged");
+}
+
+}  // namespace flyai

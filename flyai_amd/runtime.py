@@ -4,7 +4,8 @@ call surface of the reference's stage runtimes so they drop in for that path.
 * ``RaggedStage.forward(hidden, q_lens, starts, slots)`` -- one step over a flat token batch that
   mixes decode rows (q=1), spec-verify rows (q=K+1) and chunked-prefill rows (q=chunk).
 * ``FastVerifyStage`` -- ``FastVerify`` (phase0/fastverify.py:80-309): ``reset``, ``prefill(h, start)``,
-  ``decode(h, start)``, ``tree_decode``, ``tree_gather``; raises ``ContextOverflow`` before any write.
+  ``decode(h, start)``, ``tree_decode`` (ancestor-masked tree verify), ``tree_gather``; raises
+  ``ContextOverflow`` before any write.
 * ``BatchedFastVerifyStage`` -- ``BatchedFastVerify`` (phase0/batchverify.py:64-190): ``reset``,
   ``load_prefix(b, src)``, ``decode(h[B, kp1, H], starts[B], use_graph=True)``.
 
@@ -151,12 +152,54 @@ class RaggedStage:
             C.c_void_p(hidden.data_ptr()), C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)))
         return hidden
 
+    def forward_tree(self, hidden, start, par, dep, slot=0):
+        """Tree verify of one sequence (``FastVerify.tree_decode``, phase0/fastverify.py:281-299):
+        hidden bf16 [M, H] holds the M tree nodes (updated in place and returned); node i is rotated
+        at position start + dep[i], its K/V goes to slot start + i and it attends the committed
+        prefix and its ancestors.  The caller validates the tree (``validate_tree``)."""
+        M = len(par)
+        if hidden.dtype != torch.bfloat16 or not hidden.is_contiguous() or tuple(hidden.shape) != (M, self.shape.hidden):
+            raise ValueError(f"hidden must be contiguous bf16 [{M}, {self.shape.hidden}]")
+        if not 0 <= int(slot) < self.kv.n_slots:
+            raise ValueError(f"slot {slot} out of range")
+        pa = np.ascontiguousarray(par, dtype=np.int32)
+        de = np.ascontiguousarray(dep, dtype=np.int32)
+        check(lib().flyai_stage_forward_tree(
+            self._h, int(start), M, pa.ctypes.data_as(C.c_void_p), de.ctypes.data_as(C.c_void_p),
+            self.kv.base(int(slot)), self.kv.cap, C.c_void_p(hidden.data_ptr()),
+            C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)))
+        return hidden
+
     def debug_buffer(self, which, dtype, shape):
         """A view of an internal buffer of the last step (tests only); see flyai_stage.h."""
         ptr = lib().flyai_stage_debug_buffer(self._h, which)
         off = ptr - self.workspace.data_ptr()
         n = int(np.prod(shape)) * torch.tensor([], dtype=dtype).element_size()
         return self.workspace[off:off + n].view(dtype).view(*shape)
+
+
+TREE_MAX_NODES = 64  # ancestor sets are 64-bit masks in the tree attention kernel
+
+
+def validate_tree(M, par, dep):
+    """Reject a malformed tree before any parent walk (``validate_tree``, phase0/fastverify.py:29-49):
+    par/dep are M long; every parent is an int in [-1, M) and not the node itself; depths are
+    non-negative ints with dep[i] == 0 for a root and dep[par[i]] + 1 otherwise (which rules out
+    cycles).  Raises ValueError."""
+    if not isinstance(M, int) or isinstance(M, bool) or M < 1:
+        raise ValueError(f"tree size {M!r} invalid")
+    if len(par) != M or len(dep) != M:
+        raise ValueError(f"tree par/dep lengths {len(par)}/{len(dep)} != {M} nodes")
+    for i in range(M):
+        p, d = par[i], dep[i]
+        if not isinstance(p, int) or isinstance(p, bool) or not (-1 <= p < M) or p == i:
+            raise ValueError(f"tree node {i}: parent {p!r} out of range [-1, {M})")
+        if not isinstance(d, int) or isinstance(d, bool) or d < 0:
+            raise ValueError(f"tree node {i}: depth {d!r} invalid")
+    for i in range(M):
+        want = 0 if par[i] == -1 else dep[par[i]] + 1
+        if dep[i] != want:
+            raise ValueError(f"tree node {i}: depth {dep[i]} != {want} (parent {par[i]}; cycle or bad depth)")
 
 
 def _parts_shape(parts):
@@ -203,7 +246,22 @@ class FastVerifyStage:
         return self.out
 
     def tree_decode(self, h, start, par, dep):
-        raise NotImplementedError("tree verify needs ancestor masks; the ragged kernel is causal-only")
+        """Verify a fixed-topology tree of M nodes in one pass (fastverify.py:281-299): node i at
+        position start + dep[i], K/V at scratch slot start + i, attending the committed prefix and its
+        ancestors.  Malformed trees raise ValueError and overflows ContextOverflow, both before any
+        write.  Trees are limited to 64 nodes (ValueError beyond)."""
+        M = h.shape[1]
+        validate_tree(M, list(par), list(dep))
+        if start + M > self.maxlen:
+            raise ContextOverflow(_lib.FLYAI_ERANGE, f"tree decode needs {start + M} positions > max_ctx "
+                                  f"{self.maxlen} (raise --max-ctx)")
+        if M > TREE_MAX_NODES:
+            raise ValueError(f"tree of {M} nodes exceeds the {TREE_MAX_NODES}-node limit")
+        self.stage.set_graphs(False)
+        flat = h.reshape(M, self.hidden).to(torch.bfloat16).contiguous().clone()
+        self.stage.forward_tree(flat, start, list(par), list(dep), 0)
+        self.tout = flat.view(1, M, self.hidden)
+        return self.tout
 
     def tree_gather(self, start, keep):
         """Compact the accepted path's KV (scratch slots start+keep[i]) to start+i, every layer

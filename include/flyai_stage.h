@@ -287,6 +287,26 @@ int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t dev_bytes, v
 int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens_host, const int32_t* starts_host,
                         const int64_t* kv_base_host, const int32_t* kv_cap_host, int32_t n_seqs,
                         uint16_t* hidden, flyai_stream_t stream);
+/* Tree verify (replaces FastVerify.tree_decode, phase0/fastverify.py:233-299, with the masks of
+ * FastVerify._tset, :250-272, and phase0/tree.py:26-46).  One sequence at committed length `start`
+ * feeds n_nodes tree nodes (hidden bf16 [n_nodes, H], updated in place).  Node i is rotated at
+ * position start + depth[i] and its K/V is written to slot start + i; it attends every committed
+ * key j < start (sliding layers: start + depth[i] - j < window) and the slots of its ancestors and
+ * itself (sliding layers: depth[i] - depth[a] < window).  parent_host/depth_host follow
+ * validate_tree (fastverify.py:29-49): parent[i] in [-1, n), parent[i] != i, depth[i] == 0 for a
+ * root and depth[parent[i]] + 1 otherwise (which rules out cycles); FLYAI_EINVAL otherwise, and for
+ * n_nodes outside [1, 64] (the ancestor sets are 64-bit masks).  start + n_nodes past kv_cap or the
+ * rope table -> FLYAI_ERANGE before any launch.  Always launched directly (no graph). */
+typedef struct {
+  int32_t start;          /* committed length: node i's K/V sits at slot start + i */
+  int32_t n_nodes;        /* 1..64 */
+  int32_t depth[64];      /* node i is rotated at position start + depth[i] */
+  uint64_t ancestors[64]; /* bit a of ancestors[i]: node a is node i or one of its ancestors */
+} flyai_attn_tree;
+
+int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t n_nodes,
+                             const int32_t* parent_host, const int32_t* depth_host, int64_t kv_base,
+                             int32_t kv_cap, uint16_t* hidden, flyai_stream_t stream);
 /* HIP-graph replay of flyai_stage_forward (the CUDA-graph capture of FastVerify.decode /
  * BatchedFastVerify.decode, phase0/fastverify.py:221-231, phase0/batchverify.py:180-190).  When
  * enabled, each step's kernels are one graph per (tokens, sequences, attention-plan capacity) key:

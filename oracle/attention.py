@@ -15,8 +15,12 @@ the current step are written into the cache before attention reads it (``fastver
 so the tokens of a verify or prefill chunk see each other causally.
 
 Parity: pure-Python brute force on tiny shapes (tests), closed-form mask, and a transformers
-fixture of ``eager_attention_forward`` with an additive mask (tests/golden).
+fixture of ``eager_attention_forward`` with an additive mask (tests/golden).  ``tree_attention``
+(tree verify) is pinned by fp64 brute force over the reference's dense tree mask and by the chain
+tree, which must equal causal verify attention.
 """
+import math
+
 import numpy as np
 import torch
 
@@ -86,4 +90,83 @@ def brute_force_attention(q, k_seqs, v_seqs, q_lens, starts, sinks, window, scal
                 for d in range(D):
                     out[t + i, h, d] = sum(ex[j] * V[g, lo + j, d] for j in range(len(ex))) / den
         t += int(ql)
+    return out
+
+
+def tree_ancestors(par):
+    """anc[i] = set of tree nodes on the path root..i, i included (``phase0/tree.py:19-23``)."""
+    out = []
+    for i in range(len(par)):
+        a, j = set(), i
+        while j != -1:
+            a.add(j)
+            j = par[j]
+        out.append(a)
+    return out
+
+
+def tree_attention(q, K, V, start, par, dep, sinks, window, scale=None):
+    """Tree-verify attention of one sequence (``FastVerify._tset`` masks, ``phase0/fastverify.py:
+    250-272``; ``phase0/tree.py:26-46``).  Tree node i is a query at absolute position
+    start + dep[i]; its key/value sit at cache slot start + i.  Node i attends
+
+      * every committed prefix key j < start (on sliding layers only if pos_i - j < window);
+      * tree slot start + t iff node t is an ancestor of i or i itself (on sliding layers only if
+        dep[i] - dep[t] < window).
+
+    q fp32 [M, Hq, D]; K, V fp32 [Hkv, >= start + M, D]; sinks fp32 [Hq].  Softmax with the sink
+    column as in ``ragged_attention``.  Returns bf16-valued fp32 [M, Hq, D]."""
+    q = torch.as_tensor(q).float()
+    M, Hq, D = q.shape
+    scale = D ** -0.5 if scale is None else scale
+    K = torch.as_tensor(K).float()[:, :start + M]
+    V = torch.as_tensor(V).float()[:, :start + M]
+    Hkv = K.shape[0]
+    n_rep = Hq // Hkv
+    anc = tree_ancestors(par)
+    allow = torch.zeros(M, start + M, dtype=torch.bool)
+    for i in range(M):
+        p = start + dep[i]
+        for j in range(start):
+            allow[i, j] = (not window) or (p - j) < window
+        for t in anc[i]:
+            allow[i, start + t] = (not window) or (dep[i] - dep[t]) < window
+    qq = q.view(M, Hkv, n_rep, D).permute(1, 0, 2, 3)                   # [Hkv, M, n_rep, D]
+    s = torch.einsum("gird,gnd->girn", qq, K) * scale
+    s = torch.where(allow[None, :, None, :], s, torch.tensor(float("-inf")))
+    sk = torch.as_tensor(sinks).float().view(Hkv, 1, n_rep, 1).expand(Hkv, M, n_rep, 1)
+    m = torch.maximum(s.amax(dim=-1, keepdim=True), sk)
+    e = torch.exp(s - m)
+    p = e / (e.sum(dim=-1, keepdim=True) + torch.exp(sk - m))
+    o = torch.einsum("girn,gnd->gird", p, V)
+    return bf16(o.permute(1, 0, 2, 3).reshape(M, Hq, D))
+
+
+def brute_force_tree_attention(q, K, V, start, par, dep, sinks, window, scale=None):
+    """fp64 pure-Python loops over the reference's dense additive tree mask (``phase0/tree.py:26-46``:
+    a finfo.min bias everywhere except the allowed cells); the independent check of the above."""
+    q = np.asarray(q, dtype=np.float64)
+    K = np.asarray(K, dtype=np.float64)
+    V = np.asarray(V, dtype=np.float64)
+    M, Hq, D = q.shape
+    scale = D ** -0.5 if scale is None else scale
+    n_rep = Hq // K.shape[0]
+    out = np.zeros((M, Hq, D))
+    for i in range(M):
+        chain, j = [], i
+        while j != -1:
+            chain.append(j)
+            j = par[j]
+        pos_i = start + dep[i]
+        keys = [j for j in range(start) if (not window) or pos_i - j < window]
+        keys += [start + t for t in range(M) if t in chain and ((not window) or pos_i - (start + dep[t]) < window)]
+        for h in range(Hq):
+            g = h // n_rep
+            logits = [sum(q[i, h, d] * K[g, c, d] for d in range(D)) * scale for c in keys]
+            sink = float(sinks[h])
+            mx = max(logits + [sink])
+            ex = [math.exp(v - mx) for v in logits]
+            den = sum(ex) + math.exp(sink - mx)
+            for d in range(D):
+                out[i, h, d] = sum(ex[c] * V[g, keys[c], d] for c in range(len(keys))) / den
     return out

@@ -17,6 +17,7 @@
   token batch: RMSNorm -> q/k/v -> RoPE -> KV write at each token's position (``fastverify.py:
   71-77``, ``batchverify.py:42-48``) -> attention (oracle.attention) -> o_proj -> residual ->
   RMSNorm -> router -> experts -> combine + residual.
+* ``decoder_layer(..., tree=(par, dep))`` -- the tree-verify step (``fastverify.py:233-299``).
 * ``stage_step`` -- the per-layer loop of ``FastVerify._layers`` / ``BatchedFastVerify._layers``
   (``fastverify.py:116-122``, ``batchverify.py:132-138``); layer i is sliding iff ``sliding[i]``.
 """
@@ -123,12 +124,22 @@ def moe_block(x_norm, p: LayerParams, k=4, trace=None):
     return out
 
 
-def decoder_layer(h, p: LayerParams, kv, q_lens, starts, cos_tab, sin_tab, trace=None):
+def decoder_layer(h, p: LayerParams, kv, q_lens, starts, cos_tab, sin_tab, trace=None, tree=None):
     """h bf16-valued fp32 [T, H]; kv = (k_seqs, v_seqs), per-sequence fp32 [Hkv, cap, D] tensors
-    that are written in place.  Returns the new hidden state."""
+    that are written in place.  Returns the new hidden state.
+
+    tree = (par, dep) makes this the tree-verify step of one sequence (``FastVerify.tree_decode``,
+    ``phase0/fastverify.py:233-299``): q_lens == [M], node i is rotated at position
+    start + dep[i], its K/V go to slot start + i, and attention uses the ancestor mask."""
     h = torch.as_tensor(h).float()
     T = h.shape[0]
     pk = pack_ragged(q_lens, starts)
+    if tree is not None:
+        assert len(q_lens) == 1 and int(q_lens[0]) == T == len(tree[0]) == len(tree[1])
+        pk["kv_pos"] = pk["positions"].copy()                    # slot start + i
+        pk["positions"] = (int(starts[0]) + np.asarray(tree[1], dtype=np.int64)).astype(np.int32)
+    else:
+        pk["kv_pos"] = pk["positions"]
     pos = torch.from_numpy(pk["positions"].astype(np.int64))
     xn = rmsnorm(h, p.ln1)
     qkv = linear(xn, p.wqkv, p.bqkv)
@@ -140,11 +151,15 @@ def decoder_layer(h, p: LayerParams, kv, q_lens, starts, cos_tab, sin_tab, trace
     qr, kr = apply_rope(q, c, s), apply_rope(k, c, s)
     k_seqs, v_seqs = kv
     for t in range(T):
-        b, ps = int(pk["seq_id"][t]), int(pk["positions"][t])
+        b, ps = int(pk["seq_id"][t]), int(pk["kv_pos"][t])
         k_seqs[b][:, ps, :] = kr[t]
         v_seqs[b][:, ps, :] = v[t]
-    o = attention.ragged_attention(qr, k_seqs, v_seqs, q_lens, starts, p.sinks,
-                                   WINDOW if p.sliding else 0)
+    if tree is not None:
+        o = attention.tree_attention(qr, k_seqs[0], v_seqs[0], int(starts[0]), list(tree[0]),
+                                     list(tree[1]), p.sinks, WINDOW if p.sliding else 0)
+    else:
+        o = attention.ragged_attention(qr, k_seqs, v_seqs, q_lens, starts, p.sinks,
+                                       WINDOW if p.sliding else 0)
     ao = linear(o.reshape(T, nq), p.wo, p.bo)
     h = bf16(h + ao)
     xn2 = rmsnorm(h, p.ln2)
@@ -155,10 +170,10 @@ def decoder_layer(h, p: LayerParams, kv, q_lens, starts, cos_tab, sin_tab, trace
     return h_out
 
 
-def stage_step(h, layers, kv_per_layer, q_lens, starts, cos_tab, sin_tab, traces=None):
+def stage_step(h, layers, kv_per_layer, q_lens, starts, cos_tab, sin_tab, traces=None, tree=None):
     for i, p in enumerate(layers):
         tr = {} if traces is not None else None
-        h = decoder_layer(h, p, kv_per_layer[i], q_lens, starts, cos_tab, sin_tab, trace=tr)
+        h = decoder_layer(h, p, kv_per_layer[i], q_lens, starts, cos_tab, sin_tab, trace=tr, tree=tree)
         if traces is not None:
             traces.append(tr)
     return h

@@ -363,3 +363,63 @@ def test_deepseek_moe_equals_token_major_restatement():
     for bad in (no_shared, swapped):
         mar_b, cos_b = metrics(bad.float().numpy(), ref)
         assert not (mar_b < 1e-2 and cos_b > 0.99999)
+
+
+# ---- a10 tree verify ---------------------------------------------------------------------------
+
+TREE_PAR = [-1, 0, 1, 2, 0, 4, 1, 6]        # tree.py's example plus a second branch off node 1
+TREE_DEP = [0, 1, 2, 3, 1, 2, 2, 3]
+
+
+def _tree_case(rng, M, start, Hq=4, Hkv=2, D=8):
+    q = bf16(torch.from_numpy(rng.standard_normal((M, Hq, D)).astype(np.float32)))
+    K = torch.from_numpy(rng.standard_normal((Hkv, start + M + 3, D)).astype(np.float32))
+    V = torch.from_numpy(rng.standard_normal((Hkv, start + M + 3, D)).astype(np.float32))
+    sinks = rng.standard_normal(Hq).astype(np.float32)
+    return q, K, V, sinks
+
+
+@pytest.mark.parametrize("window", [0, 3, 6])
+def test_tree_attention_brute_force(window):
+    """FastVerify tree masks (fastverify.py:250-272, tree.py:26-46) against fp64 loops over the
+    reference's dense additive mask."""
+    rng = np.random.default_rng(9)
+    start = 7
+    q, K, V, sinks = _tree_case(rng, len(TREE_PAR), start)
+    got = attention.tree_attention(q, K, V, start, TREE_PAR, TREE_DEP, sinks, window).numpy()
+    ref = attention.brute_force_tree_attention(q.numpy(), K.numpy(), V.numpy(), start, TREE_PAR, TREE_DEP,
+                                               sinks, window)
+    mar, cos = metrics(got, ref)
+    assert mar < 1e-2 and cos > 0.99999
+
+
+@pytest.mark.parametrize("window", [0, 4])
+def test_chain_tree_equals_causal_verify(window):
+    """A chain (par[i] = i-1, dep[i] = i) is an ordinary verify row: tree attention must equal
+    causal ragged attention of q_len M at the same start; a branching tree must not."""
+    rng = np.random.default_rng(10)
+    M, start = 6, 11
+    q, K, V, sinks = _tree_case(rng, M, start)
+    chain_par, chain_dep = list(range(-1, M - 1)), list(range(M))
+    got = attention.tree_attention(q, K, V, start, chain_par, chain_dep, sinks, window).numpy()
+    ref = attention.ragged_attention(q, [K], [V], [M], [start], sinks, window).numpy()
+    mar, cos = metrics(got, ref)
+    assert mar < 1e-6 and cos > 0.9999999
+    q8, K8, V8, s8 = _tree_case(rng, len(TREE_PAR), start)
+    tree = attention.tree_attention(q8, K8, V8, start, TREE_PAR, TREE_DEP, s8, window).numpy()
+    causal = attention.ragged_attention(q8, [K8], [V8], [len(TREE_PAR)], [start], s8, window).numpy()
+    assert metrics(tree, causal)[0] > 1e-2      # siblings must stay invisible
+
+
+def test_tree_attention_planted_sibling_leak_fails():
+    """Planting the classic mistake (a node also sees a sibling's slot) in the brute force must
+    break agreement: the check is sensitive to the ancestor mask."""
+    rng = np.random.default_rng(11)
+    start = 5
+    q, K, V, sinks = _tree_case(rng, len(TREE_PAR), start)
+    got = attention.tree_attention(q, K, V, start, TREE_PAR, TREE_DEP, sinks, 0).numpy()
+    leaky = list(TREE_PAR)
+    leaky[4] = 3            # node 4 re-parented under node 3: now sees nodes 1..3 of the other branch
+    ref = attention.brute_force_tree_attention(q.numpy(), K.numpy(), V.numpy(), start, leaky,
+                                               [0, 1, 2, 3, 4, 5, 2, 3], sinks, 0)
+    assert metrics(got, ref)[0] > 1e-2

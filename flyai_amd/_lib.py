@@ -73,6 +73,11 @@ _PROTOS = {
     "flyai_attn_plan": (C.c_int, [P, P, I32, I32, I32, I32, P, I32, P, I32, P, P, P]),
     "flyai_attn_partials_bytes": (SZ, [I32]),
     "flyai_attn_ragged": (C.c_int, [P, P, P, P, P, P, I32, I32, I32, I32, P, I32, I32, P, I32, P, P, P]),
+    "flyai_bf16_tile_packed_bytes": (SZ, [I32, I32]),
+    "flyai_bf16_tile_repack": (C.c_int, [P, I32, I32, P, P]),
+    "flyai_embed_gather": (C.c_int, [P, P, I32, I32, I32, P, P]),
+    "flyai_lm_head_workspace_bytes": (SZ, [I32, I32]),
+    "flyai_lm_head_argmax": (C.c_int, [P, P, I32, I32, P, I32, P, P, P, P]),
     "flyai_stage_create": (C.c_int, [P, P]),
     "flyai_stage_destroy": (None, [P]),
     "flyai_stage_set_layer": (C.c_int, [P, I32, P]),

@@ -346,3 +346,44 @@ def moe_combine_sum(y_perm, inv, k, shared=None, residual=None, out=None):
     check(lib().flyai_moe_combine_sum(_ptr(y_perm), _ptr(inv), T, k, H, _ptr(shared), _ptr(residual),
                                       _ptr(out), _stream()))
     return out
+
+
+def bf16_tile_repack(w):
+    """nn.Linear weight bf16 [N, K] -> MFMA-fragment tiles (u8 buffer) for lm_head_argmax."""
+    N, K = w.shape
+    _need(w, torch.bfloat16, (N, K), "w")
+    n = int(lib().flyai_bf16_tile_packed_bytes(N, K))
+    if n == 0:
+        raise ValueError("bf16_tile_repack needs N % 16 == 0 and K % 32 == 0")
+    packed = torch.empty(n, dtype=torch.uint8, device=w.device)
+    check(lib().flyai_bf16_tile_repack(_ptr(w), N, K, _ptr(packed), _stream()))
+    return packed
+
+
+def embed_gather(table, ids):
+    """table bf16 [V, H], ids int32 [T] (device) -> bf16 [T, H]."""
+    V, H = table.shape
+    _need(table, torch.bfloat16, (V, H), "table")
+    _need(ids, torch.int32, None, "ids")
+    out = torch.empty(ids.numel(), H, dtype=torch.bfloat16, device=table.device)
+    check(lib().flyai_embed_gather(_ptr(table), _ptr(ids), ids.numel(), H, V, _ptr(out), _stream()))
+    return out
+
+
+def lm_head_argmax(x, w_packed, vocab, rows=None, want_logits=False, workspace=None):
+    """Greedy token of each selected row: x bf16 [R, H] final-normed hidden rows; rows int32 [n]
+    (device; None: all R rows); returns ids int32 [n] (and bf16 logits [n, vocab])."""
+    R, H = x.shape
+    _need(x, torch.bfloat16, (R, H), "x")
+    n = R if rows is None else rows.numel()
+    if rows is not None:
+        _need(rows, torch.int32, (n,), "rows")
+    _need(w_packed, torch.uint8, (int(lib().flyai_bf16_tile_packed_bytes(vocab, H)),), "w_packed")
+    ids = torch.empty(n, dtype=torch.int32, device=x.device)
+    logits = torch.empty(n, vocab, dtype=torch.bfloat16, device=x.device) if want_logits else None
+    need = int(lib().flyai_lm_head_workspace_bytes(n, vocab))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    check(lib().flyai_lm_head_argmax(_ptr(x), _ptr(rows), n, H, _ptr(w_packed), vocab, _ptr(ids),
+                                     _ptr(logits), _ptr(workspace), _stream()))
+    return (ids, logits) if want_logits else ids

@@ -238,6 +238,27 @@ int flyai_attn_ragged(const uint16_t* q, const uint16_t* k_pool, const uint16_t*
                       const flyai_attn_group* groups_dev, int32_t n_groups, float* partials,
                       uint16_t* out, flyai_stream_t stream);
 
+/* ---- head and tail of a served model (the continuous-batch backend's token step) --------------
+ * Embedding: replaces parts["embed"](token_ids) (phase0/specpipe.py:595-596, :779): out[t] =
+ * table[ids[t]] (bf16 [V, H] table; an id outside [0, V) gives a zero row).  H % 8 == 0.
+ * lm_head + greedy pick: replaces lm_head(norm(h)).argmax(-1) (phase0/specpipe.py:796-800; the
+ * greedy branches of Sampler.sample_logits / accept, phase0/specsample.py:78-100).  x holds the
+ * final-normed hidden rows (flyai_rmsnorm); rows (device, nullable) selects n_rows <= 64 of them
+ * (NULL: rows 0..n_rows-1), e.g. only the last token of a prefill chunk (specpipe.py:794-795).
+ * logits[r][v] = bf16(fp32 dot(x[rows[r]], W[v])) (MFMA accumulation); ids[r] = the first v of
+ * maximal logit (torch.argmax semantics).  logits_out (nullable, bf16 [n_rows, V]) receives the
+ * logits.  W is re-packed once by flyai_bf16_tile_repack from the nn.Linear layout [V, H]
+ * (V % 16 == 0, H % 32 == 0; flyai_bf16_tile_packed_bytes(V, H) bytes).  workspace:
+ * flyai_lm_head_workspace_bytes(n_rows, V). */
+size_t flyai_bf16_tile_packed_bytes(int32_t N, int32_t K);
+int flyai_bf16_tile_repack(const uint16_t* w, int32_t N, int32_t K, uint8_t* packed, flyai_stream_t stream);
+int flyai_embed_gather(const uint16_t* table, const int32_t* ids, int32_t T, int32_t H, int32_t V,
+                       uint16_t* out, flyai_stream_t stream);
+size_t flyai_lm_head_workspace_bytes(int32_t n_rows, int32_t V);
+int flyai_lm_head_argmax(const uint16_t* x, const int32_t* rows, int32_t n_rows, int32_t H,
+                         const uint8_t* w_packed, int32_t V, int32_t* ids, uint16_t* logits_out,
+                         void* workspace, flyai_stream_t stream);
+
 /* ---- a10: stage step driver ----------------------------------------------------------------------
  * The per-layer loop of FastVerify._layers / BatchedFastVerify._layers (phase0/fastverify.py:116-122,
  * phase0/batchverify.py:132-138) over GptOssDecoderLayer.forward (modeling_gpt_oss.py:347-376), for

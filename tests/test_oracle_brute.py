@@ -423,3 +423,35 @@ def test_tree_attention_planted_sibling_leak_fails():
     ref = attention.brute_force_tree_attention(q.numpy(), K.numpy(), V.numpy(), start, leaky,
                                                [0, 1, 2, 3, 4, 5, 2, 3], sinks, 0)
     assert metrics(got, ref)[0] > 1e-2
+
+
+# ---- tail: lm_head + greedy pick ----------------------------------------------------------------
+
+def test_greedy_pick_is_first_max():
+    """torch.argmax semantics (the reference's greedy pick): the first index of the maximum."""
+    from oracle import tail
+    rng = np.random.default_rng(30)
+    lg = bf16(torch.from_numpy(rng.integers(-3, 4, size=(40, 17)).astype(np.float32))).numpy()
+    got = tail.greedy_pick(lg)
+    for r in range(lg.shape[0]):
+        best = 0
+        for v in range(1, lg.shape[1]):
+            if lg[r, v] > lg[r, best]:
+                best = v
+        assert got[r] == best
+    assert (got == torch.from_numpy(lg).argmax(-1).numpy()).all()
+
+
+def test_lm_head_logits_exact_on_small_integers():
+    """Integer weights and unit-RMS integer rows: the logits are exact integers (no rounding), so
+    the tail's composition (norm weight applied, weight not transposed) is fixed by the closed form."""
+    from oracle import tail
+    rng = np.random.default_rng(31)
+    H, V = 32, 48
+    h = np.where(rng.random((3, H)) < 0.5, -1.0, 1.0).astype(np.float32)       # RMS exactly 1
+    norm_w = rng.integers(1, 3, size=H).astype(np.float32)
+    lm_w = rng.integers(-2, 3, size=(V, H)).astype(np.float32)
+    got = tail.lm_head_logits(torch.from_numpy(h), torch.from_numpy(norm_w), torch.from_numpy(lm_w), eps=0.0)
+    want = (h * norm_w) @ lm_w.T
+    assert np.array_equal(got.numpy(), want)
+    assert not np.array_equal(got.numpy(), (h * norm_w) @ lm_w[::-1].T)

@@ -228,6 +228,11 @@ __global__ __launch_bounds__(256) void moe_mxfp4_kernel(
 }
 
 constexpr int kNTW = 2;  // weight tiles per wave
+// weight tiles per wave of the decode-sized kernels: 3 divides both projections' tile counts at
+// GPT-OSS shapes (gate_up 360 = 30 x 12, down 180 = 15 x 12), so no workgroup runs half empty;
+// measured at C1 against 1, 2 and 5 (2: gate_up 146.5 / down 84.7 us, 3: 144.6 / 81.3 us)
+constexpr int kNTWGateUp = 3;
+constexpr int kNTWDown = 3;
 
 // compile-time loop: f(integral_constant<int, B>) ... f(integral_constant<int, N-1>)
 template <int B, int N, class F>
@@ -593,8 +598,8 @@ int launch_moe_gate_up(const uint16_t* x, const int32_t* perm, const int32_t* of
   const MxGeom gm = mx_geom(E, 2 * I, H);
   const bool dense = use_dense(T * k_top, E) && H >= 128;  // the tiled kernel reads 128-K groups
   if (H <= 4064) {
-    const int wg_per_e = ceil_div(gm.NT, 4 * kNTW);
-    hipLaunchKernelGGL((moe_mxfp4_kernel<true, kNTW>), dim3(E * wg_per_e), dim3(256),
+    const int wg_per_e = ceil_div(gm.NT, 4 * kNTWGateUp);
+    hipLaunchKernelGGL((moe_mxfp4_kernel<true, kNTWGateUp>), dim3(E * wg_per_e), dim3(256),
                        kRowsPerPass * mx_lds_row_bytes(H), s, x, perm, offsets, k_top, w13, b13, E,
                        2 * I, H, 1, dense ? kDenseFrom : (1 << 30), (void*)h);
     int rc = check_launch("moe_gate_up_mxfp4");
@@ -615,8 +620,8 @@ int launch_moe_down(const uint16_t* h, const int32_t* offsets, const uint8_t* w2
   const MxGeom gm = mx_geom(E, H, I);
   const bool dense = use_dense(rows_total, E) && I >= 128;  // the tiled kernel reads 128-K groups
   if (I <= 4064) {
-    const int wg_per_e = ceil_div(gm.NT, 4 * kNTW);
-    hipLaunchKernelGGL((moe_mxfp4_kernel<false, kNTW>), dim3(E * wg_per_e), dim3(256),
+    const int wg_per_e = ceil_div(gm.NT, 4 * kNTWDown);
+    hipLaunchKernelGGL((moe_mxfp4_kernel<false, kNTWDown>), dim3(E * wg_per_e), dim3(256),
                        kRowsPerPass * mx_lds_row_bytes(I), s, h, nullptr, offsets, 1, w2, b2, E, H, I, 1,
                        dense ? kDenseFrom : (1 << 30), (void*)y);
     int rc = check_launch("moe_down_mxfp4");

@@ -45,7 +45,9 @@ int launch_rmsnorm(const uint16_t* x, const float* w, int T, int H, float eps, u
 
 // ---- bf16 projections: split-K partial GEMM + fused finalize kernels -------------------------------
 // gemm_splitk: workgroup = 4 waves on 4 consecutive 16-feature tiles and one K slice of kKQW groups
-// of 128.  The activation slice (64 rows x 512 K, bf16) is staged once in LDS; each wave issues all
+// of 128.  MFMA step j of group q takes, in lane (r, g), K = 128q + 32j + 8g .. +7 for both operands
+// (any K order shared by the two operands is valid), so each weight load instruction reads one
+// whole 64-byte run of each of its 16 rows.  The activation slice (64 rows x 512 K, bf16) is staged once in LDS; each wave issues all
 // of its weight loads for the slice before its first MFMA (a single HBM round trip per wave) and
 // writes fp32 partial sums part[slice][row][feature].  A finalize kernel adds the slices in slice
 // order (so the result is independent of timing), the bias, and the fused epilogue.
@@ -65,22 +67,83 @@ __global__ __launch_bounds__(256) void gemm_splitk_bf16_kernel(
   const int nkq = min(kKQW, KQ - kq0);
   const bool nval = nt * 16 < N;
   const int feat = nt * 16 + r;
-  // weights for the whole slice, issued up front
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  if (M <= kGemmRows) {
+    // One pass (decode-sized M): the activation slice's loads go out first, then the weights, so the
+    // LDS stores wait only for the activations (loads complete in issue order) and the L2 round trip
+    // for them overlaps the HBM fetch of the weights; the barrier then waits on LDS only.
+    constexpr int kPer = kGemmRows * kKQW * 16 / 256;  // 16-byte vectors per thread
+    u32x4 av[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = j * 256 + (int)threadIdx.x;
+      const int row = i / (kKQW * 16), v = i % (kKQW * 16);
+      const int k = 128 * kq0 + 8 * v;
+      const bool ok = row < M && k < K;
+      av[j] = ok ? *reinterpret_cast<const u32x4*>(x + (size_t)row * K + k) : u32x4{0u, 0u, 0u, 0u};
+    }
+    asm volatile("" ::: "memory");  // keep the activation loads ahead of the weight loads
+    uint4 wv[kKQW][4];
+#pragma unroll
+    for (int q = 0; q < kKQW; ++q) {
+      const int kb = 128 * (kq0 + q);
+      const bool ok = nval && q < nkq;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)  // step j reads K kb + 32j .. +31 (K % 32 == 0)
+        wv[q][j] = ok && kb + 32 * j < K ? reinterpret_cast<const uint4*>(W + (size_t)feat * K + kb)[4 * j + g]
+                                         : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = j * 256 + (int)threadIdx.x;
+      *reinterpret_cast<u32x4*>(&as[i / (kKQW * 16)][i % (kKQW * 16)]) = av[j];
+    }
+    lds_barrier();
+    if (!nval) return;
+    const int mt_count = (M + 15) / 16;
+    f32x4_t acc[4] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f},
+                      f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int q = 0; q < kKQW; ++q) {
+      if (q >= nkq) break;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        if (m >= mt_count) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 av4 = as[16 * m + r][q * 16 + 4 * j + g];
+          acc[m] = mfma16x16x32(as_bf16x8(av4), as_bf16x8(wv[q][j]), acc[m]);
+        }
+      }
+    }
+    float* pp = part + (size_t)slice * M * N;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      if (m >= mt_count) break;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * m + 4 * g + v;
+        if (row < M) pp[(size_t)row * N + feat] = acc[m][v];
+      }
+    }
+    return;
+  }
+  // weights for the whole slice, issued up front (reused by every pass of 64 rows)
   uint4 wv[kKQW][4];
 #pragma unroll
   for (int q = 0; q < kKQW; ++q) {
-    const int k0 = 128 * (kq0 + q) + 32 * g;
-    const bool ok = nval && q < nkq && k0 < K;
+    const int kb = 128 * (kq0 + q);
+    const bool ok = nval && q < nkq;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      wv[q][j] = ok ? reinterpret_cast<const uint4*>(W + (size_t)feat * K + k0)[j] : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < 4; ++j)  // step j reads K kb + 32j .. +31 (K % 32 == 0)
+      wv[q][j] = ok && kb + 32 * j < K ? reinterpret_cast<const uint4*>(W + (size_t)feat * K + kb)[4 * j + g]
+                                       : make_uint4(0, 0, 0, 0);
   }
   for (int m0 = 0; m0 < M; m0 += kGemmRows) {
     const int rows = min(kGemmRows, M - m0);
     __syncthreads();
     // the slice of A goes to LDS with loads batched 8 per thread (one round trip per batch);
     // rows past the pass and K past the row end are stored as zero
-    typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
     for (int b0 = 0; b0 < kGemmRows * kKQW * 16; b0 += 8 * 256) {
       u32x4 v8[8];
 #pragma unroll
@@ -111,7 +174,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_bf16_kernel(
         if (m >= mt_count) break;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint4 av = as[16 * m + r][q * 16 + 4 * g + j];
+          const uint4 av = as[16 * m + r][q * 16 + 4 * j + g];
           acc[m] = mfma16x16x32(as_bf16x8(av), as_bf16x8(wv[q][j]), acc[m]);
         }
       }

@@ -368,8 +368,8 @@ def cpu_baseline(lw, kv, layer_idx, hidden0, q_lens, starts, slots, shape, maxle
                                    lw.w2_scales.cpu().numpy(), lw.b2.cpu().numpy())
     p = olayer.LayerParams(f(lw.ln1), f(lw.ln2), f(lw.wqkv), f(lw.bqkv), f(lw.wo), f(lw.bo), f(lw.sinks),
                            f(lw.router_w), f(lw.router_b), moe, lw.sliding)
-    ks = [f(kv.k_view(layer_idx, s)).clone() for s in slots]
-    vs = [f(kv.v_view(layer_idx, s)).transpose(1, 2).contiguous() for s in slots]
+    ks = [f(kv.k_dense(layer_idx, s)) for s in slots]
+    vs = [f(kv.v_dense(layer_idx, s)) for s in slots]
     cos, sin = olayer.rope_table(maxlen)
     h = f(hidden0)
     print("[bench] cpu oracle: one layer", file=sys.stderr, flush=True)

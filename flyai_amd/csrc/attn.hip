@@ -1,20 +1,20 @@
 // Ragged GQA attention with learned sinks and an optional sliding window, for decode, spec-verify
 // and prefill-chunk rows over per-sequence KV slabs.
 //
-// KV slab of sequence b at element offset kv_base[b] (caller-owned pools, kv_cap[b] % 64 == 0):
-//   K  [Hkv][cap][64]   (row per key)
-//   Vt [Hkv][64][cap]   (V transposed: row per head dim)
+// KV slab of sequence b at element offset kv_base[b] (caller-owned pools, kv_cap[b] % 64 == 0): per
+// kv head a region of cap x 64 elements, tiled in 64-key blocks in the fragment order below
+// (kv_k_off / kv_v_off in common.h), so every K or V load instruction of a wave reads one KiB.
 // Work item = (sequence, kv head, <= 4 query tokens, key split).  Its query rows (tokens x the 8
 // heads of the GQA group, in tiles of 16) are processed by one wave with 16x16x32 bf16 MFMAs:
 //   S^T[16 keys][16 qrows] = K_tile . Q^T       (K as A operand, Q^T as B, head dim reduced)
 //   O^T[16 dims][16 qrows] += Vt_tile . P^T     (Vt as A operand, P^T as B, keys reduced)
 // Operand orders are permuted (any order consistent between the two operands of a product is
-// valid) so that every 16-byte load instruction of the wave reads 64-byte contiguous runs:
+// valid), and the slab stores each block in exactly the order the lanes consume it:
 //   head dims: lane group g supplies dims 8g..8g+7 (step 0) and 32+8g..32+8g+7 (step 1);
 //   keys of a 64-key block: S^T tile kt, row m is key 32*(kt/2) + 8*(m/4) + 4*(kt%2) + m%4, so the
 //   C-layout registers of lane (qrow n, group g) hold keys 8g..8g+7 (tiles 0,1) and 32+8g..+7
 //   (tiles 2,3) -- exactly the P^T operand of the two PV steps and the two 16-byte Vt loads.
-// K of the next block is loaded while the current block computes.  Each item writes (m, l, O[64])
+// K and V of the next block are loaded while the current block computes.  Each item writes (m, l, O[64])
 // per query row; a merge kernel folds the splits and the sink.
 #include <limits.h>
 #include <math.h>
@@ -43,24 +43,34 @@ __device__ __forceinline__ int tile_key(int kt, int m) {
 }
 
 // Every 64-key block starts at a multiple of 64 below key_hi <= cap (cap % 64 == 0), so all 64 keys
-// are inside the slab: the loads below are unconditional (no branch between loads).
+// are inside the slab: the loads below are unconditional (no branch between loads).  The slab is
+// tiled (kv_k_off / kv_v_off in common.h): a 64-key block is 4096 contiguous elements, and each of
+// these 16-byte-per-lane loads reads one contiguous KiB of it.
+// KV is read once per step, so the loads are nontemporal (streamed, as the expert weights are).
+typedef unsigned int attn_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ld_kv(const uint16_t* p) {
+  const attn_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const attn_u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ void load_k_tile(uint4 (&k)[4][2], const uint16_t* __restrict__ K, int kb,
-                                            int n, int g) {
+                                            int lane) {
+  const uint16_t* blk = K + (size_t)kb * 64 + lane * 8;
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
-    const uint16_t* kp = K + (size_t)(kb + tile_key(kt, n)) * 64 + 8 * g;
-    k[kt][0] = *reinterpret_cast<const uint4*>(kp);
-    k[kt][1] = *reinterpret_cast<const uint4*>(kp + 32);
+    k[kt][0] = ld_kv(blk + kt * 1024);
+    k[kt][1] = ld_kv(blk + kt * 1024 + 512);
   }
 }
 
-__device__ __forceinline__ void load_v_tile(uint4 (&v)[4][2], const uint16_t* __restrict__ Vt, int cap,
-                                            int kb, int n, int g) {
+__device__ __forceinline__ void load_v_tile(uint4 (&v)[4][2], const uint16_t* __restrict__ Vt, int kb,
+                                            int lane) {
+  const uint16_t* blk = Vt + (size_t)kb * 64 + lane * 8;
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-      v[dt][h] = *reinterpret_cast<const uint4*>(Vt + (size_t)(16 * dt + n) * cap + kb + 32 * h + 8 * g);
+    for (int dt = 0; dt < 4; ++dt) v[dt][h] = ld_kv(blk + h * 2048 + dt * 512);
 }
 
 // QT query-row tiles of 16 (QT = 1: up to 2 tokens; QT = 2: up to 4 tokens).
@@ -140,12 +150,16 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
     int_hi = min(it.key_hi - 1, it.pos0);
   }
   const int int_lo = max(it.key_lo, window > 0 ? pos_last - window + 1 : 0);
-  uint4 kc[4][2], kn[4][2], vv[4][2];
-  load_k_tile(kc, K, kb_first, n, g);
+  // K and V of the next block are loaded while the current block computes
+  uint4 kc[4][2], kn[4][2], vv[4][2], vn[4][2];
+  load_k_tile(kc, K, kb_first, lane);
+  load_v_tile(vv, Vt, kb_first, lane);
   for (int kb = kb_first; kb < it.key_hi; kb += 64) {
-    load_v_tile(vv, Vt, cap, kb, n, g);
     const bool more = kb + 64 < it.key_hi;
-    if (more) load_k_tile(kn, K, kb + 64, n, g);
+    if (more) {
+      load_k_tile(kn, K, kb + 64, lane);
+      load_v_tile(vn, Vt, kb + 64, lane);
+    }
     const bool interior = kb >= int_lo && kb + 63 <= int_hi;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -225,9 +239,11 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
     }
     if (more) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        kc[kt][0] = kn[kt][0];
-        kc[kt][1] = kn[kt][1];
+      for (int t = 0; t < 4; ++t) {
+        kc[t][0] = kn[t][0];
+        kc[t][1] = kn[t][1];
+        vv[t][0] = vn[t][0];
+        vv[t][1] = vn[t][1];
       }
     }
   }

@@ -83,6 +83,26 @@ __device__ __forceinline__ float warp_max(float v) {
   return v;
 }
 
+// ---- KV slab layout (head_dim 64) ----------------------------------------------------------------
+// A sequence's slab holds, per kv head, a region of cap x 64 bf16 (cap % 64 == 0) made of 64-key
+// blocks of 4096 elements in the attention kernel's MFMA-fragment order, so that every 16-byte-per-
+// lane load of a wave reads one contiguous KiB:
+//   K: [kt 4][step 2][lane 64][8]  lane = 16 gd + n holds key tile_key(kt, n) of the block and dims
+//      32 step + 8 gd .. +7, where tile_key(kt, m) = 32 (kt / 2) + 8 (m / 4) + 4 (kt % 2) + m % 4;
+//   V: [h 2][dt 4][lane 64][8]  lane = 16 gk + n holds dim 16 dt + n and keys 32 h + 8 gk .. +7.
+// kv_k_off / kv_v_off give the element offset of (key position p, dim d) within a head region.
+__host__ __device__ inline int64_t kv_k_off(int p, int d) {
+  const int kk = p & 63;
+  const int kt = 2 * (kk >> 5) + ((kk & 7) >> 2);
+  const int n = 4 * ((kk & 31) >> 3) + (kk & 3);
+  return (int64_t)(p >> 6) * 4096 + kt * 1024 + (d >> 5) * 512 + (16 * ((d & 31) >> 3) + n) * 8 + (d & 7);
+}
+__host__ __device__ inline int64_t kv_v_off(int p, int d) {
+  const int kk = p & 63;
+  return (int64_t)(p >> 6) * 4096 + (kk >> 5) * 2048 + (d >> 4) * 512 + (16 * ((kk & 31) >> 3) + (d & 15)) * 8 +
+         (kk & 7);
+}
+
 inline hipStream_t as_stream(flyai_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }

@@ -429,16 +429,15 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(
       q_out[((size_t)t * Hq + h) * D + d] = f2bf(first);
       q_out[((size_t)t * Hq + h) * D + d + D2] = f2bf(second);
     } else if (in_cap) {
-      const int gk = h - Hq;
-      uint16_t* kp = k_pool + base + ((size_t)gk * cap + slot) * D;
-      kp[d] = f2bf(first);
-      kp[d + D2] = f2bf(second);
+      uint16_t* kh = k_pool + base + (size_t)(h - Hq) * cap * D;  // the head's tiled region
+      kh[kv_k_off(slot, d)] = f2bf(first);
+      kh[kv_k_off(slot, d + D2)] = f2bf(second);
     }
   }
   if (in_cap) {
     for (int i = tid; i < Hkv * D; i += nthr) {
       const int gv = i / D, d = i % D;
-      v_pool[base + ((size_t)gv * D + d) * cap + slot] = f2bf(val((Hq + Hkv) * D + gv * D + d));
+      v_pool[base + (size_t)gv * cap * D + kv_v_off(slot, d)] = f2bf(val((Hq + Hkv) * D + gv * D + d));
     }
   }
 }
@@ -499,18 +498,20 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_vec_kernel(
       first[j] = f2bf(bf16_round(bf16_round(x1[j] * c) - bf16_round(x2[j] * sn)));
       second[j] = f2bf(bf16_round(bf16_round(x2[j] * c) + bf16_round(x1[j] * sn)));
     }
-    uint16_t* dst = h < Hq ? q_out + ((size_t)t * Hq + h) * D
-                           : k_pool + base + ((size_t)(h - Hq) * cap + slot) * D;
-    *reinterpret_cast<uint2*>(dst + d0) = make_uint2(first[0] | ((uint32_t)first[1] << 16),
-                                                     first[2] | ((uint32_t)first[3] << 16));
-    *reinterpret_cast<uint2*>(dst + d0 + D2) = make_uint2(second[0] | ((uint32_t)second[1] << 16),
-                                                          second[2] | ((uint32_t)second[3] << 16));
+    // four consecutive dims from a multiple of 4 stay contiguous in the tiled K layout
+    uint16_t* kh = k_pool + base + (size_t)(h - Hq) * cap * D;
+    uint16_t* d1 = h < Hq ? q_out + ((size_t)t * Hq + h) * D + d0 : kh + kv_k_off(slot, d0);
+    uint16_t* d2 = h < Hq ? q_out + ((size_t)t * Hq + h) * D + d0 + D2 : kh + kv_k_off(slot, d0 + D2);
+    *reinterpret_cast<uint2*>(d1) = make_uint2(first[0] | ((uint32_t)first[1] << 16),
+                                               first[2] | ((uint32_t)first[3] << 16));
+    *reinterpret_cast<uint2*>(d2) = make_uint2(second[0] | ((uint32_t)second[1] << 16),
+                                               second[2] | ((uint32_t)second[3] << 16));
   } else if (in_cap) {
     const int v = u - rot_units, gv = v / QV, d0 = (v % QV) * 4;
     float o[4];
     sum4((Hq + Hkv) * D + gv * D + d0, o);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v_pool[base + ((size_t)gv * D + d0 + j) * cap + slot] = f2bf(o[j]);
+    for (int j = 0; j < 4; ++j) v_pool[base + (size_t)gv * cap * D + kv_v_off(slot, d0 + j)] = f2bf(o[j]);
   }
 }
 
@@ -587,8 +588,8 @@ extern "C" int flyai_rope_kv_append(const uint16_t* qkv, const int32_t* position
                                     int32_t Hq, int32_t Hkv, int32_t D, const int64_t* kv_base,
                                     const int32_t* kv_cap, uint16_t* q_out, uint16_t* k_pool,
                                     uint16_t* v_pool, flyai_stream_t stream) {
-  FLYAI_REQUIRE(T >= 0 && Hq > 0 && Hkv > 0 && D > 0 && D % 2 == 0 && rope_positions > 0,
-                "rope_kv: bad shape");
+  FLYAI_REQUIRE(T >= 0 && Hq > 0 && Hkv > 0 && D == 64 && rope_positions > 0,
+                "rope_kv: bad shape (the tiled KV layout needs head_dim 64)");
   FLYAI_REQUIRE(qkv && positions && seq_id && cos_tab && sin_tab && kv_base && kv_cap && q_out &&
                     k_pool && v_pool,
                 "rope_kv: null pointer");

@@ -9,15 +9,16 @@ call surface of the reference's stage runtimes so they drop in for that path.
 * ``BatchedFastVerifyStage`` -- ``BatchedFastVerify`` (phase0/batchverify.py:64-190): ``reset``,
   ``load_prefix(b, src)``, ``decode(h[B, kp1, H], starts[B], use_graph=True)``.
 
-The KV workspace is one slab per sequence slot in per-layer pools: K [Hkv][cap][D] and V transposed
-[Hkv][D][cap] (the attention kernel streams both with 16-byte loads).  It replaces StaticKV /
-BatchedStaticKV ([B, Hkv, maxlen, D] per layer, fastverify.py:52-77, batchverify.py:29-48)."""
+The KV workspace is one slab per sequence slot in per-layer pools, each kv head a region of cap x 64
+tiled in 64-key blocks in the attention kernel's fragment order (flyai_amd.kvlayout).  It replaces
+StaticKV / BatchedStaticKV ([B, Hkv, maxlen, D] per layer, fastverify.py:52-77,
+batchverify.py:29-48)."""
 import ctypes as C
 
 import numpy as np
 import torch
 
-from . import _lib, ops
+from . import _lib, kvlayout, ops
 from ._lib import ContextOverflow, check, lib
 from .weights import GptOssShape
 
@@ -27,9 +28,12 @@ def _round_up(v, m):
 
 
 class KVWorkspace:
-    """Per-layer K/V pools holding ``n_slots`` sequence slabs of ``cap`` positions each."""
+    """Per-layer K/V pools holding ``n_slots`` sequence slabs of ``cap`` positions each, in the tiled
+    layout of ``flyai_amd.kvlayout`` (what the attention kernel streams)."""
 
     def __init__(self, n_layers, n_slots, maxlen, n_kv_heads=8, head_dim=64, device="cuda"):
+        if head_dim != kvlayout.HEAD_DIM:
+            raise ValueError("the tiled KV layout needs head_dim 64")
         self.n_layers, self.n_slots = n_layers, n_slots
         self.cap = _round_up(max(maxlen, 64), 64)
         self.maxlen = maxlen
@@ -46,20 +50,33 @@ class KVWorkspace:
         for t in self.k + self.v:
             t.zero_()
 
-    def k_view(self, layer, slot):
-        """[Hkv, cap, D] view of one slot's keys."""
-        return self.k[layer][self.base(slot):self.base(slot) + self.slab].view(
-            self.n_kv_heads, self.cap, self.head_dim)
+    def _slab(self, pools, layer, slot):
+        return pools[layer][self.base(slot):self.base(slot) + self.slab]
 
-    def v_view(self, layer, slot):
-        """[Hkv, D, cap] view of one slot's (transposed) values."""
-        return self.v[layer][self.base(slot):self.base(slot) + self.slab].view(
-            self.n_kv_heads, self.head_dim, self.cap)
+    def k_dense(self, layer, slot, positions=None):
+        """Dense [Hkv, P, 64] copy of one slot's keys (all cap positions by default)."""
+        return kvlayout.gather(self._slab(self.k, layer, slot), self.n_kv_heads, self.cap, "k", positions)
+
+    def v_dense(self, layer, slot, positions=None):
+        """Dense [Hkv, P, 64] copy of one slot's values."""
+        return kvlayout.gather(self._slab(self.v, layer, slot), self.n_kv_heads, self.cap, "v", positions)
+
+    def set_dense(self, layer, slot, k, v, positions=None):
+        """Write dense [Hkv, P, 64] keys and values into one slot."""
+        kvlayout.scatter(self._slab(self.k, layer, slot), self.n_kv_heads, self.cap, "k", k, positions)
+        kvlayout.scatter(self._slab(self.v, layer, slot), self.n_kv_heads, self.cap, "v", v, positions)
+
+    def move_positions(self, layer, slot, src, dst):
+        """K/V rows at positions src -> positions dst (all read before any is written)."""
+        k, v = self.k_dense(layer, slot, src), self.v_dense(layer, slot, src)
+        self.set_dense(layer, slot, k, v, dst)
 
     def copy_slot(self, dst, src_ws, src_slot=0):
+        if src_ws.cap != self.cap or src_ws.n_kv_heads != self.n_kv_heads:
+            raise ValueError("load_prefix needs workspaces of the same capacity and heads")
         for l in range(self.n_layers):
-            self.k_view(l, dst).copy_(src_ws.k_view(l, src_slot))
-            self.v_view(l, dst).copy_(src_ws.v_view(l, src_slot))
+            self._slab(self.k, l, dst).copy_(src_ws._slab(src_ws.k, l, src_slot))
+            self._slab(self.v, l, dst).copy_(src_ws._slab(src_ws.v, l, src_slot))
 
 
 class RaggedStage:
@@ -269,9 +286,7 @@ class FastVerifyStage:
         src = torch.tensor([start + k for k in keep], device=self.dev)
         dst = torch.arange(start, start + len(keep), device=self.dev)
         for l in range(self.n_layers):
-            kk, vv = self.cache.k_view(l, 0), self.cache.v_view(l, 0)
-            kk.index_copy_(1, dst, kk.index_select(1, src))
-            vv.index_copy_(2, dst, vv.index_select(2, src))
+            self.cache.move_positions(l, 0, src, dst)
 
 
 class BatchedFastVerifyStage:

@@ -181,7 +181,10 @@ int flyai_moe_combine_sum(const uint16_t* y_perm, const int32_t* inv, int32_t T,
  * (modeling_gpt_oss.py:215-232) with per-op bf16 rounding, then the K/V write at each token's
  * position (StaticKV.update, phase0/fastverify.py:71-77; BatchedStaticKV.update,
  * phase0/batchverify.py:42-48).  KV pool layout per sequence slab (element offset kv_base[b]):
- * K [Hkv][kv_cap[b]][D], V transposed [Hkv][D][kv_cap[b]].  cos_tab/sin_tab bf16
+ * per kv head a region of kv_cap[b] x 64 elements (D must be 64) in 64-key blocks of 4096 elements in
+ * the attention kernel's MFMA-fragment order: K block [kt 4][step 2][lane 64][8], lane 16gd+n holding
+ * key 32(kt/2) + 8(n/4) + 4(kt%2) + n%4 and dims 32step+8gd..+7; V block [h 2][dt 4][lane 64][8], lane
+ * 16gk+n holding dim 16dt+n and keys 32h+8gk..+7 (flyai_amd/kvlayout.py restates it).  cos_tab/sin_tab bf16
  * [rope_positions][D/2]; a token whose position is outside the table or its slab is skipped. */
 int flyai_rmsnorm(const uint16_t* x, const float* w, int32_t T, int32_t H, float eps, uint16_t* y,
                   flyai_stream_t stream);
@@ -201,6 +204,8 @@ int flyai_rope_kv_append(const uint16_t* qkv, const int32_t* positions, const in
  * (phase0/fastverify.py:52-77).  Query token i of sequence b (position p = starts[b]+i) attends
  * keys j in [lo, p], lo = 0 or max(0, p-window+1); logits scaled by D^-0.5; the per-head sink
  * logit joins the softmax denominator only.  q bf16 [T,Hq,D] (rotated); out bf16 [T,Hq,D].
+ * KV slabs in the tiled layout above (flyai_rope_kv_append); every K or V load instruction of a wave
+ * reads one contiguous KiB.
  * Work is split over (sequence, kv head, group of <= 4 query tokens, key split); the host-side
  * plan (flyai_attn_plan) is copied to the device by the caller.  The plan lists groups of <= 2
  * tokens first (n_items_small items, run by a one-tile kernel variant), then the rest.  D == 64,

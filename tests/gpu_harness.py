@@ -41,8 +41,8 @@ def fill_kv_random(kv: KVWorkspace, seed):
 
 
 def oracle_kv(kv: KVWorkspace, layer, slots):
-    ks = [cpu_f32(kv.k_view(layer, s)).clone() for s in slots]
-    vs = [cpu_f32(kv.v_view(layer, s)).transpose(1, 2).contiguous() for s in slots]
+    ks = [cpu_f32(kv.k_dense(layer, s)) for s in slots]
+    vs = [cpu_f32(kv.v_dense(layer, s)) for s in slots]
     return ks, vs
 
 

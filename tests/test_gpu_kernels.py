@@ -6,6 +6,8 @@ import numpy as np
 import pytest
 import torch
 
+from flyai_amd import kvlayout
+
 from oracle import attention as oattn
 from oracle import experts as oexperts
 from oracle import layer as olayer
@@ -250,12 +252,18 @@ def test_rope_kv_append_bit_exact():
     rq = olayer.apply_rope(qc[:, :Hq * D].view(T, Hq, D), cos[p], sin[p])
     rk = olayer.apply_rope(qc[:, Hq * D:(Hq + Hkv) * D].view(T, Hkv, D), cos[p], sin[p])
     assert torch.equal(q.float().cpu(), rq)
-    kcpu = kp.float().cpu().view(3, Hkv, cap, D)
-    vcpu = vp.float().cpu().view(3, Hkv, D, cap)
+    kcpu = [kvlayout.gather(kp[b * slab:(b + 1) * slab], Hkv, cap, "k").float().cpu() for b in range(3)]
+    vcpu = [kvlayout.gather(vp[b * slab:(b + 1) * slab], Hkv, cap, "v").float().cpu() for b in range(3)]
+    written = set()
     for t in range(T):
         b, ps = int(pk["seq_id"][t]), int(pk["positions"][t])
-        assert torch.equal(kcpu[b, :, ps, :], rk[t])
-        assert torch.equal(vcpu[b, :, :, ps], qc[t, (Hq + Hkv) * D:].view(Hkv, D))
+        written.add((b, ps))
+        assert torch.equal(kcpu[b][:, ps, :], rk[t])
+        assert torch.equal(vcpu[b][:, ps, :], qc[t, (Hq + Hkv) * D:].view(Hkv, D))
+    # nothing else in the slabs was touched (the tiled offsets of distinct positions never overlap)
+    for b in range(3):
+        others = [p_ for p_ in range(cap) if (b, p_) not in written]
+        assert not kcpu[b][:, others].any() and not vcpu[b][:, others].any()
 
 
 # ---- a8 ----------------------------------------------------------------------------------------
@@ -277,8 +285,8 @@ def test_attention_vs_oracle(window, q_lens, starts):
     capt = torch.tensor([cap] * S, dtype=torch.int32, device=DEV)
     items, groups, n_small = ops.attn_plan(q_lens, starts, Hkv, window, 512)
     out = ops.attn_ragged(q, kp, vp, base, capt, sinks, window, items, groups, n_small, Hkv)
-    ks = [kp[b * slab:(b + 1) * slab].float().cpu().view(Hkv, cap, D) for b in range(S)]
-    vs = [vp[b * slab:(b + 1) * slab].float().cpu().view(Hkv, D, cap).transpose(1, 2) for b in range(S)]
+    ks = [kvlayout.gather(kp[b * slab:(b + 1) * slab], Hkv, cap, "k").float().cpu() for b in range(S)]
+    vs = [kvlayout.gather(vp[b * slab:(b + 1) * slab], Hkv, cap, "v").float().cpu() for b in range(S)]
     ref = oattn.ragged_attention(q.float().cpu(), ks, vs, q_lens, starts, sinks.cpu(), window)
     mar, cos = _metrics(out.float().cpu().numpy(), ref.numpy())
     assert mar <= MAR and cos >= COS, f"attention: {mar:.3g} {cos:.6f}"
@@ -294,11 +302,12 @@ def test_attention_ignores_unwritten_nan_slots():
     slab = Hkv * cap * D
     kp = torch.full((S * slab,), float("nan"), device=DEV).to(torch.bfloat16)
     vp = torch.full((S * slab,), float("nan"), device=DEV).to(torch.bfloat16)
-    kv = kp.view(S, Hkv, cap, D)
-    vv = vp.view(S, Hkv, D, cap)
     for b, (ql, st) in enumerate(zip(q_lens, starts)):
-        kv[b, :, :st + ql] = torch.randn(Hkv, st + ql, D, device=DEV, generator=_gen(60 + b)).to(torch.bfloat16)
-        vv[b, :, :, :st + ql] = torch.randn(Hkv, D, st + ql, device=DEV, generator=_gen(70 + b)).to(torch.bfloat16)
+        pos = torch.arange(st + ql, device=DEV)
+        kvlayout.scatter(kp[b * slab:(b + 1) * slab], Hkv, cap, "k",
+                         torch.randn(Hkv, st + ql, D, device=DEV, generator=_gen(60 + b)), pos)
+        kvlayout.scatter(vp[b * slab:(b + 1) * slab], Hkv, cap, "v",
+                         torch.randn(Hkv, st + ql, D, device=DEV, generator=_gen(70 + b)), pos)
     q = torch.randn(T, Hq, D, device=DEV, generator=_gen(80)).to(torch.bfloat16)
     sinks = torch.zeros(Hq, device=DEV)
     base = torch.tensor([0, slab], dtype=torch.int64, device=DEV)

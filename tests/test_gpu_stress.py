@@ -90,8 +90,8 @@ def test_stress_batch_layers_vs_oracle():
         share = hist[hot.numpy()].sum() / hist.sum()
         assert 0.35 < share < 0.7, f"hot-expert share {share:.2f}"
         # oracle on the subset, from the GPU's layer input and the GPU-written KV of this layer
-        ks = [cpu_f32(kv.k_view(l, b)).clone() for b, _ in picks]
-        vs = [cpu_f32(kv.v_view(l, b)).transpose(1, 2).contiguous() for b, _ in picks]
+        ks = [cpu_f32(kv.k_dense(l, b)) for b, _ in picks]
+        vs = [cpu_f32(kv.v_dense(l, b)) for b, _ in picks]
         ref = olayer.decoder_layer(cpu_f32(hin)[rows], oracle_layer_params(lw, lw.sliding), (ks, vs),
                                    sub_q, sub_starts, cos, sin)
         mar, cos_ = metrics(cpu_f32(h)[rows].numpy(), ref.numpy())

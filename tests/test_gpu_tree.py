@@ -74,8 +74,8 @@ def test_tree_decode_per_layer_vs_oracle(name, start, M):
         assert mar <= 2e-2 and cos_ >= 0.999, (l, mar, cos_)
         # each node's K/V sits at its own slot (the QKV GEMM's summation order differs from the
         # oracle's, so values agree to bf16 rounding, not bit for bit; a misplaced slot is off by O(1))
-        k_gpu = gh.cpu_f32(kv.k_view(l, 0))[:, start:start + M]
-        v_gpu = gh.cpu_f32(kv.v_view(l, 0))[:, :, start:start + M].transpose(1, 2)
+        k_gpu = gh.cpu_f32(kv.k_dense(l, 0))[:, start:start + M]
+        v_gpu = gh.cpu_f32(kv.v_dense(l, 0))[:, start:start + M]
         for i in range(M):
             for got, want in ((k_gpu[:, i], okv[0][0][:, start + i]), (v_gpu[:, i], okv[1][0][:, start + i])):
                 mar_kv, cos_kv = gh.metrics(got.numpy(), want.numpy())
@@ -120,8 +120,10 @@ def test_fast_verify_tree_decode_then_gather():
     torch.cuda.synchronize()
     assert tuple(out.shape) == (1, M, case["shape"].hidden) and torch.isfinite(out.float()).all()
     keep = [0, 1, 6, 7]
-    k_before = [fv.cache.k_view(l, 0)[:, [start + i for i in keep]].clone() for l in range(2)]
+    k_before = [fv.cache.k_dense(l, 0)[:, [start + i for i in keep]] for l in range(2)]
+    v_before = [fv.cache.v_dense(l, 0)[:, [start + i for i in keep]] for l in range(2)]
     fv.tree_gather(start, keep)
     torch.cuda.synchronize()
     for l in range(2):
-        assert torch.equal(fv.cache.k_view(l, 0)[:, start:start + len(keep)], k_before[l])
+        assert torch.equal(fv.cache.k_dense(l, 0)[:, start:start + len(keep)], k_before[l])
+        assert torch.equal(fv.cache.v_dense(l, 0)[:, start:start + len(keep)], v_before[l])

@@ -169,7 +169,8 @@ extern "C" int flyai_abi_version(void) { return FLYAI_ABI_VERSION; }
 extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** out) {
   FLYAI_REQUIRE(cfg && out, "stage_create: null pointer");
   const flyai_stage_config& c = *cfg;
-  FLYAI_REQUIRE(c.n_layers > 0 && c.hidden > 0 && c.hidden % 64 == 0, "stage: hidden must be a multiple of 64");
+  FLYAI_REQUIRE(c.n_layers > 0 && c.hidden > 0 && c.hidden % 64 == 0 && c.hidden <= 7168,
+                "stage: hidden must be a multiple of 64, at most 7168");
   FLYAI_REQUIRE(c.head_dim == 64 && c.n_kv_heads > 0 && c.n_q_heads == 8 * c.n_kv_heads,
                 "stage: attention kernel needs head_dim 64 and 8 query heads per kv head");
   FLYAI_REQUIRE(c.n_experts >= 4 && c.n_experts <= 256 && c.n_experts % 4 == 0 &&

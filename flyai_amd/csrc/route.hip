@@ -472,8 +472,10 @@ int launch_permute(const int32_t* ids, int T, int k, int E, int32_t* hist, int32
 // ------------------------------------------------------------------------------------------------
 // Combine: out[t] = bf16(sum_s w[t,s] * y_perm[inv[t*k+s]]) (+ residual, rounded again).  When lnw is
 // given, the next layer's input RMSNorm of the new row is written to xn as well (fused: the row is
-// already in this workgroup).
+// already in this workgroup's registers).  Each thread owns up to kCombinePer float4 column groups;
+// the residual and norm weights are loaded before the slot rows, so the row needs one round trip.
 constexpr int kCombineThreads = 1024;
+constexpr int kCombinePer = 2;  // H <= 4 * 1024 * 2
 
 __global__ __launch_bounds__(kCombineThreads) void moe_combine_kernel(
     const float* __restrict__ y_perm, const int32_t* __restrict__ inv,
@@ -481,12 +483,25 @@ __global__ __launch_bounds__(kCombineThreads) void moe_combine_kernel(
     const float* __restrict__ lnw, float eps, uint16_t* __restrict__ xn) {
   __shared__ float red[kCombineThreads / 64];
   const int t = blockIdx.x, tid = threadIdx.x;
+  const int H4 = H / 4;
+  // residual may alias out: it is read here, before any store
+  float4 lw[kCombinePer];
+  uint2 rsd[kCombinePer];
+#pragma unroll
+  for (int c = 0; c < kCombinePer; ++c) {
+    const int i = tid + c * kCombineThreads;
+    lw[c] = (lnw && i < H4) ? reinterpret_cast<const float4*>(lnw)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    rsd[c] = (residual && i < H4) ? reinterpret_cast<const uint2*>(residual + (size_t)t * H)[i] : make_uint2(0, 0);
+  }
   int rows[8];
   float wt[8];
   for (int s = 0; s < k; ++s) { rows[s] = inv[t * k + s]; wt[s] = topk_w[t * k + s]; }
-  const int H4 = H / 4;
   float ss = 0.f;
-  for (int i = tid; i < H4; i += kCombineThreads) {
+  uint16_t ob[kCombinePer][4];
+#pragma unroll
+  for (int c = 0; c < kCombinePer; ++c) {
+    const int i = tid + c * kCombineThreads;
+    if (i >= H4) continue;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s = 0; s < k; ++s) {
       const float4 y = reinterpret_cast<const float4*>(y_perm + (size_t)rows[s] * H)[i];
@@ -497,21 +512,17 @@ __global__ __launch_bounds__(kCombineThreads) void moe_combine_kernel(
     }
     float o[4] = {bf16_round(acc.x), bf16_round(acc.y), bf16_round(acc.z), bf16_round(acc.w)};
     if (residual) {
-      const uint2 r = reinterpret_cast<const uint2*>(residual + (size_t)t * H)[i];
-      o[0] += bf2f(r.x & 0xffff); o[1] += bf2f(r.x >> 16);
-      o[2] += bf2f(r.y & 0xffff); o[3] += bf2f(r.y >> 16);
+      o[0] += bf2f(rsd[c].x & 0xffff); o[1] += bf2f(rsd[c].x >> 16);
+      o[2] += bf2f(rsd[c].y & 0xffff); o[3] += bf2f(rsd[c].y >> 16);
     }
-    uint16_t ob[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      ob[c] = f2bf(o[c]);
-      const float hf = bf2f(ob[c]);
+    for (int j = 0; j < 4; ++j) {
+      ob[c][j] = f2bf(o[j]);
+      const float hf = bf2f(ob[c][j]);
       ss = fmaf(hf, hf, ss);
     }
-    uint2 ov;
-    ov.x = (uint32_t)ob[0] | ((uint32_t)ob[1] << 16);
-    ov.y = (uint32_t)ob[2] | ((uint32_t)ob[3] << 16);
-    reinterpret_cast<uint2*>(out + (size_t)t * H)[i] = ov;
+    reinterpret_cast<uint2*>(out + (size_t)t * H)[i] =
+        make_uint2((uint32_t)ob[c][0] | ((uint32_t)ob[c][1] << 16), (uint32_t)ob[c][2] | ((uint32_t)ob[c][3] << 16));
   }
   if (!lnw) return;
   ss = warp_sum(ss);
@@ -521,8 +532,17 @@ __global__ __launch_bounds__(kCombineThreads) void moe_combine_kernel(
 #pragma unroll
   for (int w = 0; w < kCombineThreads / 64; ++w) tot += red[w];
   const float rr = rsqrtf(tot / (float)H + eps);
-  for (int i = tid; i < H; i += kCombineThreads)
-    xn[(size_t)t * H + i] = f2bf(lnw[i] * (bf2f(out[(size_t)t * H + i]) * rr));
+#pragma unroll
+  for (int c = 0; c < kCombinePer; ++c) {
+    const int i = tid + c * kCombineThreads;
+    if (i >= H4) continue;
+    const float lv[4] = {lw[c].x, lw[c].y, lw[c].z, lw[c].w};
+    uint16_t q[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) q[j] = f2bf(lv[j] * (bf2f(ob[c][j]) * rr));
+    reinterpret_cast<uint2*>(xn + (size_t)t * H)[i] =
+        make_uint2((uint32_t)q[0] | ((uint32_t)q[1] << 16), (uint32_t)q[2] | ((uint32_t)q[3] << 16));
+  }
 }
 
 int launch_combine(const float* y_perm, const int32_t* inv, const float* w, int T, int k, int H,
@@ -562,7 +582,8 @@ extern "C" int flyai_moe_permute(const int32_t* topk_ids, int32_t T, int32_t k, 
 extern "C" int flyai_moe_combine(const float* y_perm, const int32_t* inv, const float* topk_w,
                                  int32_t T, int32_t k, int32_t H, const uint16_t* residual,
                                  uint16_t* out, flyai_stream_t stream) {
-  FLYAI_REQUIRE(T >= 0 && k >= 1 && k <= 8 && H > 0 && H % 4 == 0, "combine: bad shape");
+  FLYAI_REQUIRE(T >= 0 && k >= 1 && k <= 8 && H > 0 && H % 4 == 0 && H <= 4 * kCombineThreads * kCombinePer,
+                "combine: need H %% 4 == 0 and H <= %d", 4 * kCombineThreads * kCombinePer);
   FLYAI_REQUIRE(y_perm && inv && topk_w && out, "combine: null pointer");
   return launch_combine(y_perm, inv, topk_w, T, k, H, residual, out, nullptr, 0.f, nullptr,
                         as_stream(stream));

@@ -35,7 +35,7 @@ class StageConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n_layers", "hidden", "n_q_heads", "n_kv_heads", "head_dim", "n_experts", "top_k",
         "intermediate", "window", "max_tokens", "max_seqs", "max_attn_items", "rope_positions",
-        "attn_split_keys")] + [("rms_eps", C.c_float)]
+        "attn_split_keys")] + [("rms_eps", C.c_float), ("attn_prefill_min", C.c_int32)]
 
 
 class LayerDesc(C.Structure):
@@ -72,6 +72,8 @@ _PROTOS = {
     "flyai_rope_kv_append": (C.c_int, [P, P, P, P, P, I32, I32, I32, I32, I32, P, P, P, P, P, P]),
     "flyai_attn_plan": (C.c_int, [P, P, I32, I32, I32, I32, P, I32, P, I32, P, P, P]),
     "flyai_attn_partials_bytes": (SZ, [I32]),
+    "flyai_attn_plan_prefill": (C.c_int, [P, P, I32, I32, I32, I32, I32, P, I32, P, I32, P, I32, P, P, P, P]),
+    "flyai_attn_prefill": (C.c_int, [P, P, P, P, P, P, I32, I32, I32, I32, P, I32, P, P]),
     "flyai_attn_ragged": (C.c_int, [P, P, P, P, P, P, I32, I32, I32, I32, P, I32, I32, P, I32, P, P, P]),
     "flyai_bf16_tile_packed_bytes": (SZ, [I32, I32]),
     "flyai_bf16_tile_repack": (C.c_int, [P, I32, I32, P, P]),

@@ -25,7 +25,8 @@
 namespace flyai {
 
 constexpr int kAttnRows = 32;     // query rows per item (4 tokens x 8 heads)
-constexpr int kPartFloats = 66;   // m, l, O[64]
+constexpr int kPartFloats = 66;   // m (base-2 units), l, O[64]
+constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ uint4 mask_keys(uint4 v, int key0, int lo, int hi) {
   // zero the bf16 elements whose key (key0 + element index) lies outside [lo, hi)
@@ -73,7 +74,153 @@ __device__ __forceinline__ void load_v_tile(uint4 (&v)[4][2], const uint16_t* __
     for (int dt = 0; dt < 4; ++dt) v[dt][h] = ld_kv(blk + h * 2048 + dt * 512);
 }
 
-// QT query-row tiles of 16 (QT = 1: up to 2 tokens; QT = 2: up to 4 tokens).
+// Per-wave state of QT query-row tiles of 16 (QT = 1: up to 2 tokens; QT = 2: up to 4 tokens): the
+// Q^T operand, each row's position (and, in a tree, its depth and ancestor set), and the running
+// softmax (max, sum, O^T accumulators).  Query row rq = 16*qt + n is token rq/8, head kv_head*8 + rq%8.
+template <int QT>
+struct QRows {
+  bf16x8_t qf[QT][2];
+  int qpos[QT], qdep[QT];
+  bool qval[QT];
+  uint64_t qanc[QT];
+  float m_run[QT], l_run[QT];
+  f32x4_t O[QT][4];
+};
+
+// Load the rows of tokens tok .. tok+ntok-1 (positions pos0 + ti, or tree positions) and reset the
+// running softmax.
+template <int QT, bool TREE>
+__device__ __forceinline__ void rows_init(QRows<QT>& R, const uint16_t* __restrict__ q, int tok, int ntok,
+                                          int pos0, int kv_head, int Hq,
+                                          const flyai_attn_tree* __restrict__ tree,
+                                          const int* __restrict__ dep_s) {
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15, g = lane >> 4;
+  const int tstart = TREE ? tree->start : 0;
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    const int rq = 16 * qt + n;
+    const int ti = rq >> 3;
+    R.qval[qt] = ti < ntok;
+    if (TREE) {
+      const int node = (tok + ti) & 63;  // < n_nodes <= 64 for every valid row
+      R.qdep[qt] = R.qval[qt] ? dep_s[node] : 0;
+      R.qanc[qt] = R.qval[qt] ? tree->ancestors[node] : 0ull;
+      R.qpos[qt] = tstart + R.qdep[qt];
+    } else {
+      R.qdep[qt] = 0;
+      R.qanc[qt] = 0ull;
+      R.qpos[qt] = pos0 + ti;
+    }
+    uint4 a = make_uint4(0, 0, 0, 0), b2 = make_uint4(0, 0, 0, 0);
+    if (R.qval[qt]) {
+      const uint16_t* qp = q + ((size_t)(tok + ti) * Hq + kv_head * 8 + (rq & 7)) * 64 + 8 * g;
+      a = *reinterpret_cast<const uint4*>(qp);
+      b2 = *reinterpret_cast<const uint4*>(qp + 32);
+    }
+    R.qf[qt][0] = as_bf16x8(a);
+    R.qf[qt][1] = as_bf16x8(b2);
+    R.m_run[qt] = -1e30f;
+    R.l_run[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) R.O[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+// One 64-key block kb (K fragments kc, V fragments vv of this lane) against the rows: scores
+// S^T = K . Q^T, the mask (positions in [key_lo, key_hi) within each row's causal / window range, or
+// the tree rule), the online softmax update and O^T += V^T . P^T.  interior: every key of the block is
+// visible to every valid row (no mask).  Values of keys at or past key_hi are zeroed (they may be
+// unwritten, even non-finite; P is 0 there).
+template <int QT, bool TREE>
+__device__ __forceinline__ void rows_block(QRows<QT>& R, const uint4 (&kc)[4][2], uint4 (&vv)[4][2], int kb,
+                                           bool interior, int key_lo, int key_hi, int window,
+                                           const flyai_attn_tree* __restrict__ tree,
+                                           const int* __restrict__ dep_s) {
+  const int g = (threadIdx.x & 63) >> 4;
+  // scores in base-2 units: head_dim^-0.5 * log2(e), so that P = exp2(s - m) is one v_exp_f32
+  const float scale = 0.125f * kLog2e;
+  const int tstart = TREE ? tree->start : 0;
+  if (kb + 64 > key_hi) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) vv[dt][h] = mask_keys(vv[dt][h], kb + 32 * h + 8 * g, INT_MIN, key_hi);
+  }
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    f32x4_t s[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      s[kt] = mfma16x16x32(as_bf16x8(kc[kt][0]), R.qf[qt][0], f32x4_t{0.f, 0.f, 0.f, 0.f});
+      s[kt] = mfma16x16x32(as_bf16x8(kc[kt][1]), R.qf[qt][1], s[kt]);
+    }
+    // lane holds S^T[key kb + tile_key(kt, 4g + v)][qrow n]
+    float bmax = -INFINITY;
+    if (interior && R.qval[qt]) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          s[kt][v] *= scale;
+          bmax = fmaxf(bmax, s[kt][v]);
+        }
+    } else {
+      const int p = R.qpos[qt];
+      const int lo = max(key_lo, window > 0 ? p - window + 1 : 0);
+      const int hi = min(p, key_hi - 1);
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int key = kb + tile_key(kt, 4 * g + v);
+          bool ok;
+          if (TREE) {
+            if (key < tstart) {
+              ok = key >= lo && key < key_hi;  // committed prefix (window on positions)
+            } else {
+              const int j = (key - tstart) & 63;  // in range whenever key < key_hi <= start + n
+              ok = key >= key_lo && key < key_hi && ((R.qanc[qt] >> j) & 1ull) &&
+                   (window == 0 || R.qdep[qt] - dep_s[j] < window);
+            }
+            ok = ok && R.qval[qt];
+          } else {
+            ok = R.qval[qt] && key >= lo && key <= hi;
+          }
+          s[kt][v] = ok ? s[kt][v] * scale : -INFINITY;
+          bmax = fmaxf(bmax, s[kt][v]);
+        }
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    const float m_new = fmaxf(R.m_run[qt], bmax);
+    // v_exp_f32 directly (results below 2^-126 may flush to zero: immaterial for a probability)
+    const float alpha = __builtin_amdgcn_exp2f(R.m_run[qt] - m_new);
+    R.m_run[qt] = m_new;
+    // P rounded to bf16 (the PV operand; the row sum uses the same rounded values).  The cast is
+    // gfx950's v_cvt_pk_bf16_f32: round to nearest even, two values per instruction.
+    float lsum = 0.f;
+    bf16x8_t pt[2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const __bf16 pb = (__bf16)__builtin_amdgcn_exp2f(s[kt][v] - m_new);
+        lsum += (float)pb;
+        pt[kt >> 1][(kt & 1) * 4 + v] = pb;
+      }
+    R.l_run[qt] = R.l_run[qt] * alpha + lsum;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      R.O[qt][dt] *= alpha;
+      R.O[qt][dt] = mfma16x16x32(as_bf16x8(vv[dt][0]), pt[0], R.O[qt][dt]);
+      R.O[qt][dt] = mfma16x16x32(as_bf16x8(vv[dt][1]), pt[1], R.O[qt][dt]);
+    }
+  }
+}
+
+// One work item (<= 4 tokens x the 8 heads of a kv head, one key split) by one wave, K and V
+// streamed from the slab; writes a partial record (m, l, O[64]) per query row.
 // TREE: the batch is one tree-verify sequence; token (= node) i sits at position
 // tree->start + depth[i] (dep_s: the depths, staged in LDS) and sees the committed keys below
 // tree->start plus the tree slots of its ancestor set (FastVerify._tset masks).
@@ -93,54 +240,15 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
   const int64_t base = kv_base[it.seq] + (int64_t)it.kv_head * cap * 64;
   const uint16_t* K = k_pool + base;
   const uint16_t* Vt = v_pool + base;
-  const float scale = 0.125f;  // 64 ** -0.5
-
-  // Q^T operand: qrow rq = 16*qt + n -> token rq/8, head kv_head*8 + rq%8
-  bf16x8_t qf[QT][2];
-  int qpos[QT];
-  bool qval[QT];
-  int qdep[QT];        // TREE: the row's node depth and ancestor set
-  uint64_t qanc[QT];
-  const int tstart = TREE ? tree->start : 0;
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    const int rq = 16 * qt + n;
-    const int ti = rq >> 3;
-    qval[qt] = ti < it.ntok;
-    if (TREE) {
-      const int node = (it.tok + ti) & 63;  // < n_nodes <= 64 for every valid row
-      qdep[qt] = qval[qt] ? dep_s[node] : 0;
-      qanc[qt] = qval[qt] ? tree->ancestors[node] : 0ull;
-      qpos[qt] = tstart + qdep[qt];
-    } else {
-      qdep[qt] = 0;
-      qanc[qt] = 0ull;
-      qpos[qt] = it.pos0 + ti;
-    }
-    uint4 a = make_uint4(0, 0, 0, 0), b2 = make_uint4(0, 0, 0, 0);
-    if (qval[qt]) {
-      const uint16_t* qp = q + ((size_t)(it.tok + ti) * Hq + it.kv_head * 8 + (rq & 7)) * 64 + 8 * g;
-      a = *reinterpret_cast<const uint4*>(qp);
-      b2 = *reinterpret_cast<const uint4*>(qp + 32);
-    }
-    qf[qt][0] = as_bf16x8(a);
-    qf[qt][1] = as_bf16x8(b2);
-  }
-  float m_run[QT], l_run[QT];
-  f32x4_t O[QT][4];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) {
-    m_run[qt] = -1e30f;
-    l_run[qt] = 0.f;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) O[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
+  QRows<QT> R;
+  rows_init<QT, TREE>(R, q, it.tok, it.ntok, it.pos0, it.kv_head, Hq, tree, dep_s);
 
   const int kb_first = it.key_lo & ~63;
   // Blocks fully inside every valid query row's key range need no score mask (wave-uniform test).
   // In a tree only committed keys (below tree->start) can be unmasked for every row.
   int pos_last, int_hi;
   if (TREE) {
+    const int tstart = tree->start;
     int dmax = 0;
     for (int i = 0; i < it.ntok; ++i) dmax = max(dmax, dep_s[(it.tok + i) & 63]);
     pos_last = tstart + dmax;
@@ -161,82 +269,7 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
       load_v_tile(vn, Vt, kb + 64, lane);
     }
     const bool interior = kb >= int_lo && kb + 63 <= int_hi;
-#pragma unroll
-    for (int qt = 0; qt < QT; ++qt) {
-      f32x4_t s[4];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-        s[kt] = mfma16x16x32(as_bf16x8(kc[kt][0]), qf[qt][0], f32x4_t{0.f, 0.f, 0.f, 0.f});
-        s[kt] = mfma16x16x32(as_bf16x8(kc[kt][1]), qf[qt][1], s[kt]);
-      }
-      // lane holds S^T[key kb + tile_key(kt, 4g + v)][qrow n]
-      float bmax = -INFINITY;
-      if (interior && qval[qt]) {
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            s[kt][v] *= scale;
-            bmax = fmaxf(bmax, s[kt][v]);
-          }
-      } else {
-        const int p = qpos[qt];
-        const int lo = max(it.key_lo, window > 0 ? p - window + 1 : 0);
-        const int hi = min(p, it.key_hi - 1);
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int key = kb + tile_key(kt, 4 * g + v);
-            bool ok;
-            if (TREE) {
-              if (key < tstart) {
-                ok = key >= lo && key < it.key_hi;  // committed prefix (window on positions)
-              } else {
-                const int j = (key - tstart) & 63;  // in range whenever key < key_hi <= start + n
-                ok = key >= it.key_lo && key < it.key_hi && ((qanc[qt] >> j) & 1ull) &&
-                     (window == 0 || qdep[qt] - dep_s[j] < window);
-              }
-              ok = ok && qval[qt];
-            } else {
-              ok = qval[qt] && key >= lo && key <= hi;
-            }
-            s[kt][v] = ok ? s[kt][v] * scale : -INFINITY;
-            bmax = fmaxf(bmax, s[kt][v]);
-          }
-      }
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-      bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-      const float m_new = fmaxf(m_run[qt], bmax);
-      const float alpha = __expf(m_run[qt] - m_new);
-      m_run[qt] = m_new;
-      float lsum = 0.f;
-      bf16x8_t pt[2];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float pv = __expf(s[kt][v] - m_new);
-          const uint16_t pb = f2bf(pv);
-          lsum += bf2f(pb);
-          pt[kt >> 1][(kt & 1) * 4 + v] = __builtin_bit_cast(__bf16, pb);
-        }
-      l_run[qt] = l_run[qt] * alpha + lsum;
-      if (qt == 0 && kb + 64 > it.key_hi) {
-        // keys at or past key_hi may be unwritten (even non-finite): zero their values, P is 0 there
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt)
-            vv[dt][h] = mask_keys(vv[dt][h], kb + 32 * h + 8 * g, INT_MIN, it.key_hi);
-      }
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        O[qt][dt] *= alpha;
-        O[qt][dt] = mfma16x16x32(as_bf16x8(vv[dt][0]), pt[0], O[qt][dt]);
-        O[qt][dt] = mfma16x16x32(as_bf16x8(vv[dt][1]), pt[1], O[qt][dt]);
-      }
-    }
+    rows_block<QT, TREE>(R, kc, vv, kb, interior, it.key_lo, it.key_hi, window, tree, dep_s);
     if (more) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -250,20 +283,20 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
   // partial record per query row: [m, l, O[64]]; O^T layout: lane holds dims 16dt + 4g + v of qrow n
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    float l = l_run[qt];
+    float l = R.l_run[qt];
     l += __shfl_xor(l, 16, 64);
     l += __shfl_xor(l, 32, 64);
     const int rq = 16 * qt + n;
-    if (!qval[qt]) continue;
+    if (!R.qval[qt]) continue;
     float* rec = partials + ((size_t)item_idx * kAttnRows + rq) * kPartFloats;
     if (g == 0) {
-      rec[0] = m_run[qt];
+      rec[0] = R.m_run[qt];
       rec[1] = l;
     }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) rec[2 + 16 * dt + 4 * g + v] = O[qt][dt][v];
+      for (int v = 0; v < 4; ++v) rec[2 + 16 * dt + 4 * g + v] = R.O[qt][dt][v];
   }
 }
 
@@ -294,8 +327,119 @@ __global__ __launch_bounds__(64, 2) void attn_partial_kernel(
     attn_item<2, false>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, nullptr, nullptr);
 }
 
-// Merge: per query row, M = max(sink, max_s m_s), L = e^(sink-M) + sum_s l_s e^(m_s-M),
-// out = bf16(sum_s O_s e^(m_s-M) / L).  Thread (row = tid/8, part = tid%8) writes 8 dims.
+// ---- chunked-prefill rows -------------------------------------------------------------------------
+// Work item = (sequence, kv head, up to kPrefillTokens consecutive query tokens): a workgroup of
+// kPrefillWaves waves, wave w owning tokens 4w .. 4w+3 of the item (32 query rows, the same math as a
+// decode item).  The item's 64-key blocks are staged once in LDS for all waves -- the tiled slab
+// block is copied as it is, so each wave reads its K and V fragments as contiguous KiBs -- through two
+// buffers with one barrier per block, the next block's loads in flight while the current one
+// computes.  No key splits: each wave ends with the sink and the normalisation and writes its rows.
+constexpr int kPrefillWaves = kPrefillTokens / 4;
+
+__global__ __launch_bounds__(64 * kPrefillWaves) void attn_prefill_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
+    const int32_t* __restrict__ kv_cap, const float* __restrict__ sinks, int window, int Hq,
+    const flyai_attn_item* __restrict__ items, uint16_t* __restrict__ out) {
+  __shared__ uint4 kvs[2][2][512];  // [buffer][K, V][one 64-key block: 4096 bf16]
+  const flyai_attn_item it = items[blockIdx.x];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int cap = kv_cap[it.seq];
+  const int64_t base = kv_base[it.seq] + (int64_t)it.kv_head * cap * 64;
+  const uint4* Kb = reinterpret_cast<const uint4*>(k_pool + base);
+  const uint4* Vb = reinterpret_cast<const uint4*>(v_pool + base);
+  // this wave's tokens and the keys they see
+  const int ntw = max(0, min(4, it.ntok - 4 * wave));
+  const int tok_w = it.tok + 4 * wave, pos_w = it.pos0 + 4 * wave;
+  QRows<2> R;
+  rows_init<2, false>(R, q, tok_w, ntw, pos_w, it.kv_head, Hq, nullptr, nullptr);
+  const int pos_last = pos_w + max(ntw, 1) - 1;
+  const int lo_w = max(it.key_lo, window > 0 ? pos_w - window + 1 : 0);  // the wave's first visible key
+  const int int_lo = max(it.key_lo, window > 0 ? pos_last - window + 1 : 0);
+  const int int_hi = min(it.key_hi - 1, pos_w);
+
+  // staging: thread tid copies uint4 s = tid + 256 j (j < 4) of the block (K: s < 512, V: s >= 512)
+  constexpr int kPer = 1024 / (64 * kPrefillWaves);
+  const int kb_first = it.key_lo & ~63;
+  // (native vector registers: a uint4 array carried across iterations would live in scratch)
+  attn_u32x4 st[kPer];
+  auto load_block = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int sidx = tid + 64 * kPrefillWaves * j;
+      const uint4* src = sidx < 512 ? Kb + (size_t)kb * 8 + sidx : Vb + (size_t)kb * 8 + (sidx - 512);
+      st[j] = *reinterpret_cast<const attn_u32x4*>(src);
+    }
+  };
+  auto store_block = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int sidx = tid + 64 * kPrefillWaves * j;
+      *reinterpret_cast<attn_u32x4*>(&kvs[buf][sidx >> 9][sidx & 511]) = st[j];
+    }
+  };
+  load_block(kb_first);
+  store_block(0);
+  lds_barrier();
+  int buf = 0;
+  for (int kb = kb_first; kb < it.key_hi; kb += 64) {
+    const bool more = kb + 64 < it.key_hi;
+    if (more) load_block(kb + 64);
+    if (ntw > 0 && kb <= pos_last && kb + 63 >= lo_w) {
+      uint4 kc[4][2], vv[4][2];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        kc[t][0] = kvs[buf][0][t * 128 + lane];
+        kc[t][1] = kvs[buf][0][t * 128 + 64 + lane];
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) vv[dt][h] = kvs[buf][1][h * 256 + dt * 64 + lane];
+      const bool interior = kb >= int_lo && kb + 63 <= int_hi;
+      rows_block<2, false>(R, kc, vv, kb, interior, it.key_lo, it.key_hi, window, nullptr, nullptr);
+    }
+    if (more) store_block(buf ^ 1);  // every wave finished reading that buffer before the last barrier
+    lds_barrier();
+    buf ^= 1;
+  }
+  // out = O 2^(m-M) / (l 2^(m-M) + 2^(sink-M)), M = max(m, sink), all in base-2 units: the merge of a
+  // single split
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    float l = R.l_run[qt];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int rq = 16 * qt + n;
+    if (!R.qval[qt]) continue;
+    const int h = it.kv_head * 8 + (rq & 7);
+    const float sink = sinks[h] * kLog2e;  // base-2 units, as the running max
+    const float M = fmaxf(R.m_run[qt], sink);
+    const float w = exp2f(R.m_run[qt] - M);
+    const float inv = 1.0f / (l * w + exp2f(sink - M));
+    uint16_t* o = out + ((size_t)(tok_w + (rq >> 3)) * Hq + h) * 64;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const uint32_t lo = (uint32_t)f2bf(R.O[qt][dt][0] * w * inv) | ((uint32_t)f2bf(R.O[qt][dt][1] * w * inv) << 16);
+      const uint32_t hi = (uint32_t)f2bf(R.O[qt][dt][2] * w * inv) | ((uint32_t)f2bf(R.O[qt][dt][3] * w * inv) << 16);
+      *reinterpret_cast<uint2*>(o + 16 * dt + 4 * g) = make_uint2(lo, hi);
+    }
+  }
+}
+
+int launch_attn_prefill(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                        const int64_t* kv_base, const int32_t* kv_cap, const float* sinks, int window, int Hq,
+                        const flyai_attn_item* pitems, int n_pitems, uint16_t* out, hipStream_t s) {
+  if (n_pitems == 0) return FLYAI_OK;
+  hipLaunchKernelGGL(attn_prefill_kernel, dim3(n_pitems), dim3(64 * kPrefillWaves), 0, s, q, k_pool, v_pool,
+                     kv_base, kv_cap, sinks, window, Hq, pitems, out);
+  return check_launch("attn_prefill");
+}
+
+// Merge: per query row, in base-2 units (s' = s log2(e), sink' = sink log2(e)): M = max(sink',
+// max_s m_s), L = 2^(sink'-M) + sum_s l_s 2^(m_s-M), out = bf16(sum_s O_s 2^(m_s-M) / L) -- the
+// softmax with the sink column, e^(s - m) = 2^(s' - m').  Thread (row = tid/8, part = tid%8) writes 8 dims.
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ partials,
                                                          const flyai_attn_group* __restrict__ groups,
                                                          const float* __restrict__ sinks, int Hq,
@@ -307,15 +451,15 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   const int ti = rq >> 3;
   if (ti >= gr.ntok) return;
   const int h = gr.kv_head * 8 + (rq & 7);
-  const float sink = sinks[h];
+  const float sink = sinks[h] * kLog2e;  // the partial maxima are in base-2 units
   float M = sink;
   for (int s = 0; s < gr.n_splits; ++s)
     M = fmaxf(M, partials[((size_t)(gr.first_item + s) * kAttnRows + rq) * kPartFloats]);
-  float L = __expf(sink - M);
+  float L = exp2f(sink - M);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int s = 0; s < gr.n_splits; ++s) {
     const float* rec = partials + ((size_t)(gr.first_item + s) * kAttnRows + rq) * kPartFloats;
-    const float wgt = __expf(rec[0] - M);
+    const float wgt = exp2f(rec[0] - M);
     L += rec[1] * wgt;
 #pragma unroll
     for (int d = 0; d < 8; ++d) acc[d] += rec[2 + part * 8 + d] * wgt;
@@ -349,15 +493,49 @@ int launch_attn(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_poo
 
 // Groups of <= 2 query tokens (one 16-row tile) are emitted first, then the larger ones, so the two
 // kernel variants each take one contiguous item range; a group's splits stay consecutive.
+// Sequences with q_len >= prefill_min (0: none) become prefill items instead (attn_prefill_kernel):
+// kPrefillTokens tokens x one kv head each, the chunk's last tiles first (they see the most keys).
 int attn_plan(const int32_t* q_lens, const int32_t* starts, int S, int Hkv, int window,
               int split_keys, flyai_attn_item* items, int max_items, flyai_attn_group* groups,
-              int max_groups, int* n_items, int* n_groups, int* n_small) {
-  int ni = 0, ng = 0;
+              int max_groups, int* n_items, int* n_groups, int* n_small, int prefill_min,
+              flyai_attn_item* pitems, int max_pitems, int* n_pitems) {
+  int ni = 0, ng = 0, np = 0;
+  {
+    int tok = 0;
+    for (int b = 0; b < S; ++b) {
+      const int ql = q_lens[b], st = starts[b];
+      if (prefill_min > 0 && ql >= prefill_min) {
+        for (int i0 = (ql - 1) / kPrefillTokens * kPrefillTokens; i0 >= 0; i0 -= kPrefillTokens) {
+          const int nt = ql - i0 < kPrefillTokens ? ql - i0 : kPrefillTokens;
+          const int p_first = st + i0;
+          for (int g = 0; g < Hkv; ++g) {
+            if (np >= max_pitems)
+              return set_error(FLYAI_ERANGE, "prefill attention plan exceeds capacity (%d items)", max_pitems);
+            flyai_attn_item& it = pitems[np++];
+            it.seq = b;
+            it.kv_head = g;
+            it.tok = tok + i0;
+            it.ntok = nt;
+            it.pos0 = p_first;
+            it.key_lo = window > 0 ? (p_first - window + 1 > 0 ? p_first - window + 1 : 0) : 0;
+            it.key_hi = p_first + nt;
+            it.group = -1;
+          }
+        }
+      }
+      tok += ql;
+    }
+  }
+  *n_pitems = np;
   for (int pass = 0; pass < 2; ++pass) {
     if (pass == 1) *n_small = ni;
     int tok = 0;
     for (int b = 0; b < S; ++b) {
       const int ql = q_lens[b], st = starts[b];
+      if (prefill_min > 0 && ql >= prefill_min) {
+        tok += ql;
+        continue;
+      }
       for (int i0 = 0; i0 < ql; i0 += 4) {
         const int nt = ql - i0 < 4 ? ql - i0 : 4;
         if ((nt <= 2) != (pass == 0)) continue;
@@ -467,8 +645,41 @@ extern "C" int flyai_attn_plan(const int32_t* q_lens_host, const int32_t* starts
                 "attn_plan: null pointer");
   for (int b = 0; b < n_seqs; ++b)
     FLYAI_REQUIRE(q_lens_host[b] >= 1 && starts_host[b] >= 0, "attn_plan: bad q_len/start at %d", b);
+  int np = 0;
   return attn_plan(q_lens_host, starts_host, n_seqs, Hkv, window, split_keys, items_host, max_items,
-                   groups_host, max_groups, n_items, n_groups, n_items_small);
+                   groups_host, max_groups, n_items, n_groups, n_items_small, 0, nullptr, 0, &np);
+}
+
+extern "C" int flyai_attn_plan_prefill(const int32_t* q_lens_host, const int32_t* starts_host,
+                                       int32_t n_seqs, int32_t Hkv, int32_t window, int32_t split_keys,
+                                       int32_t prefill_min, flyai_attn_item* items_host, int32_t max_items,
+                                       flyai_attn_group* groups_host, int32_t max_groups,
+                                       flyai_attn_item* pitems_host, int32_t max_pitems, int32_t* n_items,
+                                       int32_t* n_groups, int32_t* n_items_small, int32_t* n_pitems) {
+  FLYAI_REQUIRE(n_seqs >= 0 && Hkv > 0 && window >= 0 && split_keys >= 64 && split_keys % 64 == 0 &&
+                    prefill_min >= 0,
+                "attn_plan_prefill: split_keys must be a positive multiple of 64");
+  FLYAI_REQUIRE(q_lens_host && starts_host && items_host && groups_host && pitems_host && n_items &&
+                    n_groups && n_items_small && n_pitems,
+                "attn_plan_prefill: null pointer");
+  for (int b = 0; b < n_seqs; ++b)
+    FLYAI_REQUIRE(q_lens_host[b] >= 1 && starts_host[b] >= 0, "attn_plan_prefill: bad q_len/start at %d", b);
+  return attn_plan(q_lens_host, starts_host, n_seqs, Hkv, window, split_keys, items_host, max_items,
+                   groups_host, max_groups, n_items, n_groups, n_items_small, prefill_min, pitems_host,
+                   max_pitems, n_pitems);
+}
+
+extern "C" int flyai_attn_prefill(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                                  const int64_t* kv_base, const int32_t* kv_cap, const float* sinks,
+                                  int32_t window, int32_t Hq, int32_t Hkv, int32_t D,
+                                  const flyai_attn_item* pitems_dev, int32_t n_pitems, uint16_t* out,
+                                  flyai_stream_t stream) {
+  FLYAI_REQUIRE(D == 64 && Hkv > 0 && Hq == 8 * Hkv, "attn_prefill: needs head_dim 64 and 8 query heads per kv head");
+  FLYAI_REQUIRE(n_pitems >= 0 && window >= 0, "attn_prefill: bad counts");
+  FLYAI_REQUIRE(q && k_pool && v_pool && kv_base && kv_cap && sinks && out && (n_pitems == 0 || pitems_dev),
+                "attn_prefill: null pointer");
+  return launch_attn_prefill(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, pitems_dev, n_pitems, out,
+                             as_stream(stream));
 }
 
 extern "C" size_t flyai_attn_partials_bytes(int32_t n_items) {

@@ -56,7 +56,9 @@ int launch_attn(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t
                 const float*, int, int, const flyai_attn_item*, int, int, const flyai_attn_group*, int,
                 const int32_t*, float*, uint16_t*, const flyai_attn_tree*, hipStream_t);
 int attn_plan(const int32_t*, const int32_t*, int, int, int, int, flyai_attn_item*, int,
-              flyai_attn_group*, int, int*, int*, int*);
+              flyai_attn_group*, int, int*, int*, int*, int, flyai_attn_item*, int, int*);
+int launch_attn_prefill(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
+                        const float*, int, int, const flyai_attn_item*, int, uint16_t*, hipStream_t);
 int attn_plan_tree(const flyai_attn_tree&, int, int, int, flyai_attn_item*, int, flyai_attn_group*, int,
                    int*, int*, int*);
 int launch_pack(const int32_t*, const int32_t*, const int64_t*, const int32_t*, int, int, int, int32_t*,
@@ -83,7 +85,7 @@ struct Carve {
 
 struct flyai_stage {
   flyai_stage_config cfg;
-  int qkv_width, max_groups, P;
+  int qkv_width, max_groups, max_pitems, P;
   flyai_layer_desc* layers = nullptr;
   const uint16_t* cos_tab = nullptr;
   const uint16_t* sin_tab = nullptr;
@@ -97,6 +99,7 @@ struct flyai_stage {
   size_t host_half = 0;  // bytes of one pinned staging half (== blob_max)
   std::vector<flyai_attn_item> plan_items[2];
   std::vector<flyai_attn_group> plan_groups[2];
+  std::vector<flyai_attn_item> plan_pitems[2];
   char* dev = nullptr;
   char* host = nullptr;
   hipEvent_t staged[2] = {nullptr, nullptr};
@@ -108,7 +111,7 @@ struct flyai_stage {
   bool graphs = false;
   hipStream_t capture_stream = nullptr;
   struct Graph {
-    int64_t key[6];
+    int64_t key[8];
     hipGraphExec_t exec;
     uint64_t last_use;
   };
@@ -119,17 +122,18 @@ struct flyai_stage {
 static constexpr int kGraphCacheMax = 16;
 static constexpr int kPlanBucket = 64;  // attention plan capacities round up to this
 
-static size_t blob_bytes(int S, int n_items0, int n_items1, int n_groups0, int n_groups1) {
+static size_t blob_bytes(int S, int n_items0, int n_items1, int n_groups0, int n_groups1, int n_pitems) {
   return align256(4 * sizeof(int32_t)) + align256((size_t)S * 4) * 3 + align256((size_t)S * 8) +
          align256((size_t)n_items0 * sizeof(flyai_attn_item)) + align256((size_t)n_items1 * sizeof(flyai_attn_item)) +
          align256((size_t)n_groups0 * sizeof(flyai_attn_group)) + align256((size_t)n_groups1 * sizeof(flyai_attn_group)) +
-         align256(sizeof(flyai_attn_tree));
+         2 * align256((size_t)n_pitems * sizeof(flyai_attn_item)) + align256(sizeof(flyai_attn_tree));
 }
 
 static void layout(flyai_stage* st) {
   const flyai_stage_config& c = st->cfg;
   const size_t S = c.max_seqs, T = c.max_tokens, P = (size_t)T * c.top_k;
-  st->blob_max = blob_bytes(c.max_seqs, c.max_attn_items, c.max_attn_items, st->max_groups, st->max_groups);
+  st->blob_max = blob_bytes(c.max_seqs, c.max_attn_items, c.max_attn_items, st->max_groups, st->max_groups,
+                            st->max_pitems);
   Carve d;
   st->o_blob = d.take(st->blob_max);
   st->o_cu = d.take((S + 1) * 4);
@@ -182,11 +186,13 @@ extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** o
   FLYAI_REQUIRE(c.max_seqs > 0 && c.max_seqs <= 8192, "stage: max_seqs in [1, 8192]");
   FLYAI_REQUIRE(c.max_attn_items > 0 && c.rope_positions > 0, "stage: bad capacities");
   FLYAI_REQUIRE(c.attn_split_keys >= 64 && c.attn_split_keys % 64 == 0, "stage: attn_split_keys % 64");
+  FLYAI_REQUIRE(c.attn_prefill_min >= 0, "stage: attn_prefill_min must be >= 0");
   flyai_stage* st = new (std::nothrow) flyai_stage();
   if (!st) return set_error(FLYAI_EINVAL, "stage_create: out of host memory");
   st->cfg = c;
   st->qkv_width = (c.n_q_heads + 2 * c.n_kv_heads) * c.head_dim;
   st->max_groups = (c.max_seqs + (c.max_tokens + 3) / 4) * c.n_kv_heads;
+  st->max_pitems = c.attn_prefill_min > 0 ? (c.max_seqs + (c.max_tokens + kPrefillTokens - 1) / kPrefillTokens) * c.n_kv_heads : 0;
   st->layers = new (std::nothrow) flyai_layer_desc[c.n_layers];
   if (!st->layers) { delete st; return set_error(FLYAI_EINVAL, "stage_create: out of host memory"); }
   memset(st->layers, 0, sizeof(flyai_layer_desc) * c.n_layers);
@@ -194,6 +200,7 @@ extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** o
     for (int i = 0; i < 2; ++i) {
       st->plan_items[i].resize(c.max_attn_items);
       st->plan_groups[i].resize(st->max_groups);
+      st->plan_pitems[i].resize(st->max_pitems > 0 ? st->max_pitems : 1);
     }
   } catch (...) {
     delete[] st->layers;
@@ -284,7 +291,8 @@ struct StepPlan {
   int Tn, S;
   int grid_items[2], grid_groups[2];  // launch sizes: exact counts, or the plan capacities (graphs)
   int n_small[2];
-  size_t off_counts, off_q, off_st, off_cap, off_base, off_items[2], off_groups[2];
+  int n_pitems[2];  // chunked-prefill attention items (exact counts, part of the graph key)
+  size_t off_counts, off_q, off_st, off_cap, off_base, off_items[2], off_groups[2], off_pitems[2];
   bool tree = false;  // a tree-verify step: the blob carries the flyai_attn_tree at off_tree
   size_t off_tree = 0;
 };
@@ -328,6 +336,9 @@ static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* count
                     sp.n_small[p], reinterpret_cast<const flyai_attn_group*>(blob + sp.off_groups[p]),
                     sp.grid_groups[p], counts ? counts + 2 * p : nullptr, F32(st->o_parts),
                     B16(st->o_attn), tree_d, s));
+    RUN(launch_attn_prefill(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks, L.sliding ? c.window : 0,
+                            c.n_q_heads, reinterpret_cast<const flyai_attn_item*>(blob + sp.off_pitems[p]),
+                            sp.n_pitems[p], B16(st->o_attn), s));
     if (fused_route) {
       // decode-sized: o-proj finalize + residual + RMSNorm + router logits, then top-k + permute
       RUN(launch_linear_residual_rmsnorm_logits(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,
@@ -362,7 +373,8 @@ static int hip_fail(const char* what, hipError_t e) {
 
 // The executable graph for this step's key, captured on first use (least recently used evicted).
 static int step_graph(flyai_stage* st, const StepPlan& sp, hipGraphExec_t* out) {
-  const int64_t key[6] = {sp.Tn, sp.S, sp.grid_items[0], sp.grid_items[1], sp.grid_groups[0], sp.grid_groups[1]};
+  const int64_t key[8] = {sp.Tn, sp.S, sp.grid_items[0], sp.grid_items[1], sp.grid_groups[0], sp.grid_groups[1],
+                          sp.n_pitems[0], sp.n_pitems[1]};
   ++st->use_clock;
   for (auto& g : st->graph_cache)
     if (memcmp(g.key, key, sizeof(key)) == 0) {
@@ -429,6 +441,7 @@ static int stage_blob(flyai_stage* st, StepPlan& sp, const int32_t* q_lens, cons
   sp.off_base = b.take((size_t)S * 8);
   for (int p = 0; p < 2; ++p) sp.off_items[p] = b.take((size_t)sp.grid_items[p] * sizeof(flyai_attn_item));
   for (int p = 0; p < 2; ++p) sp.off_groups[p] = b.take((size_t)sp.grid_groups[p] * sizeof(flyai_attn_group));
+  for (int p = 0; p < 2; ++p) sp.off_pitems[p] = b.take((size_t)sp.n_pitems[p] * sizeof(flyai_attn_item));
   sp.tree = tree != nullptr;
   if (tree) sp.off_tree = b.take(sizeof(flyai_attn_tree));
   if (b.off > st->blob_max) return set_error(FLYAI_ERANGE, "batch blob exceeds its reservation");
@@ -447,6 +460,7 @@ static int stage_blob(flyai_stage* st, StepPlan& sp, const int32_t* q_lens, cons
   for (int p = 0; p < 2; ++p) {
     memcpy(hb + sp.off_items[p], st->plan_items[p].data(), n_items[p] * sizeof(flyai_attn_item));
     memcpy(hb + sp.off_groups[p], st->plan_groups[p].data(), n_groups[p] * sizeof(flyai_attn_group));
+    memcpy(hb + sp.off_pitems[p], st->plan_pitems[p].data(), sp.n_pitems[p] * sizeof(flyai_attn_item));
   }
   if (tree) memcpy(hb + sp.off_tree, tree, sizeof(flyai_attn_tree));
   RUN(copy_h2d(st->dev + st->o_blob, hb, b.off, s));
@@ -491,7 +505,8 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
   for (int p = 0; p < 2; ++p) {
     RUN(attn_plan(q_lens, starts, S, c.n_kv_heads, p == 0 ? 0 : c.window, c.attn_split_keys,
                   st->plan_items[p].data(), c.max_attn_items, st->plan_groups[p].data(), st->max_groups,
-                  &n_items[p], &n_groups[p], &sp.n_small[p]));
+                  &n_items[p], &n_groups[p], &sp.n_small[p], c.attn_prefill_min, st->plan_pitems[p].data(),
+                  st->max_pitems, &sp.n_pitems[p]));
     // replayed graphs are sized by capacities, so that a step with a few more items (longer KV)
     // reuses the graph; the kernels read the live counts from the blob
     auto bucket = [](int n, int cap) { const int b = (n + kPlanBucket - 1) / kPlanBucket * kPlanBucket; return b < cap ? b : cap; };
@@ -568,6 +583,7 @@ extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t 
                        &n_groups[p], &sp.n_small[p]));
     sp.grid_items[p] = n_items[p];
     sp.grid_groups[p] = n_groups[p];
+    sp.n_pitems[p] = 0;
   }
   const int32_t q_len = n, st0 = start;
   RUN(stage_blob(st, sp, &q_len, &st0, &kv_base, &kv_cap, n_items, n_groups, &tree, s));

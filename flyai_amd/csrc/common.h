@@ -103,6 +103,9 @@ __host__ __device__ inline int64_t kv_v_off(int p, int d) {
          (kk & 7);
 }
 
+// query tokens per chunked-prefill attention item (4 waves x 4 tokens)
+constexpr int kPrefillTokens = 16;
+
 inline hipStream_t as_stream(flyai_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }

@@ -221,6 +221,38 @@ def attn_plan(q_lens, starts, n_kv_heads, window, split_keys, max_items=1 << 20)
     return it, gr, ns.value
 
 
+def attn_plan_prefill(q_lens, starts, n_kv_heads, window, split_keys, prefill_min, max_items=1 << 20):
+    """attn_plan with sequences of q_len >= prefill_min as prefill items -> (items, groups, n_small,
+    pitems) on the CPU."""
+    S = len(q_lens)
+    ql = (C.c_int32 * S)(*[int(v) for v in q_lens])
+    st = (C.c_int32 * S)(*[int(v) for v in starts])
+    max_groups = (S + sum((int(v) + 3) // 4 for v in q_lens)) * n_kv_heads
+    max_pitems = (S + sum((int(v) + 15) // 16 for v in q_lens)) * n_kv_heads
+    items = (_lib.AttnItem * max_items)()
+    groups = (_lib.AttnGroup * max_groups)()
+    pitems = (_lib.AttnItem * max_pitems)()
+    ni, ng, ns, npi = C.c_int32(0), C.c_int32(0), C.c_int32(0), C.c_int32(0)
+    check(lib().flyai_attn_plan_prefill(ql, st, S, n_kv_heads, window, split_keys, prefill_min, items, max_items,
+                                        groups, max_groups, pitems, max_pitems, C.byref(ni), C.byref(ng),
+                                        C.byref(ns), C.byref(npi)))
+    it = torch.frombuffer(bytearray(items), dtype=torch.int32).view(max_items, 8)[:ni.value].clone()
+    gr = torch.frombuffer(bytearray(groups), dtype=torch.int32).view(max_groups, 8)[:ng.value].clone()
+    pit = torch.frombuffer(bytearray(pitems), dtype=torch.int32).view(max_pitems, 8)[:npi.value].clone()
+    return it, gr, ns.value, pit
+
+
+def attn_prefill(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, pitems, n_kv_heads, out):
+    """Run prefill items (attn_plan_prefill) into the rows of out bf16 [T, Hq, 64]."""
+    T, Hq, D = q.shape
+    _need(q, torch.bfloat16, (T, Hq, D), "q")
+    _need(out, torch.bfloat16, (T, Hq, D), "out")
+    pit = pitems.to(q.device).contiguous()
+    check(lib().flyai_attn_prefill(_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(kv_base), _ptr(kv_cap), _ptr(sinks),
+                                   window, Hq, n_kv_heads, D, _ptr(pit), pitems.shape[0], _ptr(out), _stream()))
+    return out
+
+
 def attn_ragged(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, items, groups, n_small, n_kv_heads):
     """q bf16 [T, Hq, 64]; items/groups/n_small from attn_plan (moved to the GPU here)."""
     T, Hq, D = q.shape

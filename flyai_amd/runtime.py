@@ -83,7 +83,7 @@ class RaggedStage:
     """One pipeline stage of GPT-OSS decoder layers on libflyai_stage."""
 
     def __init__(self, shape: GptOssShape, layers, rotary, kv: KVWorkspace, max_tokens, max_seqs,
-                 max_attn_items=None, split_keys=1024, device="cuda", use_graphs=False):
+                 max_attn_items=None, split_keys=1024, device="cuda", use_graphs=False, prefill_min=32):
         self.shape, self.layers, self.rotary, self.kv = shape, layers, rotary, kv
         self.device = torch.device(device)
         self.max_tokens, self.max_seqs = max_tokens, max_seqs
@@ -95,7 +95,8 @@ class RaggedStage:
             n_kv_heads=shape.n_kv_heads, head_dim=shape.head_dim, n_experts=shape.n_experts,
             top_k=shape.top_k, intermediate=shape.intermediate, window=shape.window,
             max_tokens=max_tokens, max_seqs=max_seqs, max_attn_items=max_attn_items,
-            rope_positions=rotary.n_positions, attn_split_keys=split_keys, rms_eps=shape.rms_eps)
+            rope_positions=rotary.n_positions, attn_split_keys=split_keys, rms_eps=shape.rms_eps,
+            attn_prefill_min=prefill_min)
         handle = C.c_void_p()
         check(lib().flyai_stage_create(C.byref(cfg), C.byref(handle)))
         self._h = handle

@@ -243,6 +243,23 @@ int flyai_attn_ragged(const uint16_t* q, const uint16_t* k_pool, const uint16_t*
                       const flyai_attn_group* groups_dev, int32_t n_groups, float* partials,
                       uint16_t* out, flyai_stream_t stream);
 
+/* Chunked-prefill rows (SURVEY next item: chunked-prefill attention on device, replacing the flex
+ * prefill of phase0/fastverify.py:138-155).  flyai_attn_plan_prefill is flyai_attn_plan with every
+ * sequence of q_len >= prefill_min (0: none) moved to prefill items instead: 16 consecutive query tokens
+ * x one kv head per item (ntok <= 16, key range [key_lo, key_hi) = the tiles' window start .. last
+ * position + 1, group -1), the chunk's last tiles first.  flyai_attn_prefill runs them: a workgroup of
+ * 4 waves per item shares each 64-key K/V block through LDS and writes the final rows of `out` (sink
+ * and normalisation included; no partials).  Same math, masks and layout as flyai_attn_ragged. */
+int flyai_attn_plan_prefill(const int32_t* q_lens_host, const int32_t* starts_host, int32_t n_seqs,
+                            int32_t Hkv, int32_t window, int32_t split_keys, int32_t prefill_min,
+                            flyai_attn_item* items_host, int32_t max_items, flyai_attn_group* groups_host,
+                            int32_t max_groups, flyai_attn_item* pitems_host, int32_t max_pitems,
+                            int32_t* n_items, int32_t* n_groups, int32_t* n_items_small, int32_t* n_pitems);
+int flyai_attn_prefill(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                       const int64_t* kv_base, const int32_t* kv_cap, const float* sinks, int32_t window,
+                       int32_t Hq, int32_t Hkv, int32_t D, const flyai_attn_item* pitems_dev, int32_t n_pitems,
+                       uint16_t* out, flyai_stream_t stream);
+
 /* ---- head and tail of a served model (the continuous-batch backend's token step) --------------
  * Embedding: replaces parts["embed"](token_ids) (phase0/specpipe.py:595-596, :779): out[t] =
  * table[ids[t]] (bf16 [V, H] table; an id outside [0, V) gives a zero row).  H % 8 == 0.
@@ -274,6 +291,7 @@ typedef struct {
   int32_t n_experts, top_k, intermediate, window;
   int32_t max_tokens, max_seqs, max_attn_items, rope_positions, attn_split_keys;
   float rms_eps;
+  int32_t attn_prefill_min;   /* sequences with q_len >= this take the prefill attention items (0: never) */
 } flyai_stage_config;
 
 typedef struct {

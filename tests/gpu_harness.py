@@ -103,3 +103,16 @@ class _SingleLayerKV:
 
     def base(self, slot):
         return slot * self.slab
+
+
+def tokens_with_same_routing(ids, ref_ids, ref_logits, k):
+    """Tokens whose GPU router ids equal the oracle's.  A differing token must sit on a near-tie of
+    the oracle's logits (k-th and (k+1)-th within 2 bf16 ulps), and at most 2 may differ."""
+    ref_ids = np.asarray(ref_ids)
+    bad = np.nonzero((ids != ref_ids).any(1))[0]
+    assert len(bad) <= 2, f"{len(bad)} tokens routed differently"
+    for t in bad:
+        lg = np.sort(np.asarray(ref_logits, dtype=np.float64)[t])[::-1]
+        ulp = 2.0 ** (np.floor(np.log2(max(abs(lg[k - 1]), abs(lg[k]), 1e-30))) - 7)
+        assert lg[k - 1] - lg[k] <= 2 * ulp, f"token {t} routed differently without a near-tie"
+    return np.setdiff1d(np.arange(ids.shape[0]), bad)

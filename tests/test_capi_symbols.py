@@ -70,10 +70,28 @@ def test_stage_create_validation(lib):
     cfg = _lib.StageConfig(n_layers=1, hidden=2880, n_q_heads=64, n_kv_heads=8, head_dim=128,
                            n_experts=128, top_k=4, intermediate=2880, window=128, max_tokens=64,
                            max_seqs=8, max_attn_items=100, rope_positions=4096, attn_split_keys=512,
-                           rms_eps=1e-5)
+                           rms_eps=1e-5, attn_prefill_min=32)
     h = C.c_void_p()
     assert lib.flyai_stage_create(C.byref(cfg), C.byref(h)) == _lib.FLYAI_EINVAL
     cfg.head_dim = 64
     assert lib.flyai_stage_create(C.byref(cfg), C.byref(h)) == 0
     assert lib.flyai_stage_workspace_bytes(h) > 0
     lib.flyai_stage_destroy(h)
+
+
+def test_attn_plan_prefill_host(lib):
+    """Sequences of q_len >= prefill_min become 16-token prefill items (last tile first); the rest
+    keep the <= 4-token decode items."""
+    from flyai_amd import ops
+    items, groups, n_small, pitems = ops.attn_plan_prefill([1, 40, 3], [10, 100, 0], n_kv_heads=2, window=0,
+                                                           split_keys=512, prefill_min=32)
+    p = pitems.numpy()
+    assert p.shape[0] == 3 * 2
+    # (seq, kv_head, tok, ntok, pos0, key_lo, key_hi, group)
+    assert p[0].tolist() == [1, 0, 1 + 32, 8, 132, 0, 140, -1] and p[1].tolist() == [1, 1, 33, 8, 132, 0, 140, -1]
+    assert p[2].tolist() == [1, 0, 17, 16, 116, 0, 132, -1] and p[4].tolist() == [1, 0, 1, 16, 100, 0, 116, -1]
+    assert sorted(set(items.numpy()[:, 0].tolist())) == [0, 2]
+    _, _, _, pw = ops.attn_plan_prefill([40], [200], n_kv_heads=1, window=128, split_keys=512, prefill_min=32)
+    assert pw.numpy()[0, 5] == 232 - 127 and pw.numpy()[-1, 5] == 200 - 127
+    _, _, _, none = ops.attn_plan_prefill([40], [200], n_kv_heads=1, window=0, split_keys=512, prefill_min=0)
+    assert none.shape[0] == 0

@@ -292,6 +292,48 @@ def test_attention_vs_oracle(window, q_lens, starts):
     assert mar <= MAR and cos >= COS, f"attention: {mar:.3g} {cos:.6f}"
 
 
+@pytest.mark.parametrize("window", [0, 128])
+def test_attention_prefill_items_vs_oracle(window):
+    """Chunked-prefill rows (q_len >= 32) on the prefill kernel, mixed with decode and verify rows on
+    the split kernel, into one output; against the oracle.  The unwritten slots past each sequence
+    hold NaN, which neither kernel may read into a result."""
+    from flyai_amd import ops
+    Hq, Hkv, D, cap = 64, 8, 64, 1600
+    q_lens, starts = [300, 1, 4, 45, 33], [700, 1000, 64, 0, 1200]
+    S, T = len(q_lens), sum(q_lens)
+    slab = Hkv * cap * D
+    kp = torch.full((S * slab,), float("nan"), device=DEV).to(torch.bfloat16)
+    vp = torch.full((S * slab,), float("nan"), device=DEV).to(torch.bfloat16)
+    for b, (ql, st) in enumerate(zip(q_lens, starts)):
+        pos = torch.arange(st + ql, device=DEV)
+        kvlayout.scatter(kp[b * slab:(b + 1) * slab], Hkv, cap, "k",
+                         torch.randn(Hkv, st + ql, D, device=DEV, generator=_gen(90 + b)), pos)
+        kvlayout.scatter(vp[b * slab:(b + 1) * slab], Hkv, cap, "v",
+                         torch.randn(Hkv, st + ql, D, device=DEV, generator=_gen(95 + b)), pos)
+    q = torch.randn(T, Hq, D, device=DEV, generator=_gen(52)).to(torch.bfloat16)
+    sinks = torch.randn(Hq, device=DEV, generator=_gen(53)).to(torch.bfloat16).float()
+    base = torch.tensor([b * slab for b in range(S)], dtype=torch.int64, device=DEV)
+    capt = torch.tensor([cap] * S, dtype=torch.int32, device=DEV)
+    items, groups, n_small, pitems = ops.attn_plan_prefill(q_lens, starts, Hkv, window, 512, 32)
+    assert pitems.shape[0] == (19 + 3 + 3) * Hkv
+    out = ops.attn_ragged(q, kp, vp, base, capt, sinks, window, items, groups, n_small, Hkv)
+    ops.attn_prefill(q, kp, vp, base, capt, sinks, window, pitems, Hkv, out)
+    torch.cuda.synchronize()
+    ks = [kvlayout.gather(kp[b * slab:(b + 1) * slab], Hkv, cap, "k").float().cpu() for b in range(S)]
+    vs = [kvlayout.gather(vp[b * slab:(b + 1) * slab], Hkv, cap, "v").float().cpu() for b in range(S)]
+    ref = oattn.ragged_attention(q.float().cpu(), ks, vs, q_lens, starts, sinks.cpu(), window)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    mar, cos = _metrics(got, ref.numpy())
+    assert mar <= MAR and cos >= COS, f"prefill attention: {mar:.3g} {cos:.6f}"
+    # the prefill path against the split path on the same rows: same math, different blocking
+    items0, groups0, ns0 = ops.attn_plan(q_lens, starts, Hkv, window, 512)
+    out0 = ops.attn_ragged(q, kp, vp, base, capt, sinks, window, items0, groups0, ns0, Hkv)
+    torch.cuda.synchronize()
+    mar0, cos0 = _metrics(got, out0.float().cpu().numpy())
+    assert mar0 < 1e-2 and cos0 > 0.99999
+
+
 def test_attention_ignores_unwritten_nan_slots():
     """Keys/values past each sequence's length (and before its window) are never read into the
     result even when they hold NaN: the kernel masks scores and zeroes out-of-range values."""
@@ -363,6 +405,37 @@ def test_c0_moe_block_vs_oracle():
     assert mar <= MAR and cos >= COS, f"C0 MoE block: {mar:.3g} {cos:.6f}"
     mar, cos = _metrics(xn.float().cpu().numpy(), xn_ref.numpy())
     assert mar < 1e-2 and cos > 0.9999
+
+
+def test_stage_step_with_prefill_chunk_per_layer_vs_oracle():
+    """A chunked-prefill row (q_len 96, prefill attention items) packed with decode and verify rows,
+    layer by layer from the GPU's own input: the attention output within a tight bar, and the layer
+    output on every token routed alike (a token may route differently only on a near-tie of the
+    oracle's logits, which the bf16 rounding of its input can flip)."""
+    import gpu_harness as gh
+    from flyai_amd.runtime import RaggedStage
+    q_lens, starts = [96, 1, 4, 1], [300, 40, 1000, 0]
+    case = gh.small_stage_case(n_layers=2, n_experts=32, seed=4, q_lens=q_lens, starts=starts)
+    shape, kv, T = case["shape"], case["kv"], case["T"]
+    cos, sin = olayer.rope_table(case["maxlen"])
+    h = case["hidden"].clone()
+    for l, lw in enumerate(case["layers"]):
+        okv = gh.oracle_kv(kv, l, case["slots"])
+        st = RaggedStage(shape, [lw], case["rot"], gh._SingleLayerKV(kv, l), max_tokens=128, max_seqs=4)
+        hin = gh.cpu_f32(h)
+        h = st.forward(h.clone(), q_lens, starts, case["slots"])
+        torch.cuda.synchronize()
+        tr = {}
+        ref = olayer.decoder_layer(hin, gh.oracle_layer_params(lw, lw.sliding), okv, q_lens, starts, cos, sin,
+                                   trace=tr)
+        attn = gh.cpu_f32(st.debug_buffer(3, torch.bfloat16, (T, shape.n_q_heads * shape.head_dim))).numpy()
+        mar_a, cos_a = _metrics(attn, tr["attn"].reshape(T, -1).numpy())
+        assert mar_a <= 1e-2 and cos_a >= 0.9999, (l, mar_a, cos_a)
+        ids = st.debug_buffer(4, torch.int32, (T, shape.top_k)).cpu().numpy()
+        good = gh.tokens_with_same_routing(ids, tr["ids"], tr["logits"], shape.top_k)
+        mar, cos_ = _metrics(gh.cpu_f32(h).numpy()[good], ref.numpy()[good])
+        assert mar <= MAR and cos_ >= COS, f"layer {l}: max-abs-rel {mar:.3g} cos {cos_:.6f}"
+        del st
 
 
 def test_batched_equals_solo_bit_exact():

@@ -20,19 +20,6 @@ def _random_tree(rng, M):
     return par, dep
 
 
-def _tokens_with_same_routing(ids, ref_ids, ref_logits, k):
-    """Tokens whose GPU router ids equal the oracle's.  A differing token must sit on a near-tie of
-    the oracle's logits (k-th and (k+1)-th within 2 bf16 ulps), and at most 2 may differ."""
-    ref_ids = np.asarray(ref_ids)
-    bad = np.nonzero((ids != ref_ids).any(1))[0]
-    assert len(bad) <= 2, f"{len(bad)} tokens routed differently"
-    for t in bad:
-        lg = np.sort(np.asarray(ref_logits, dtype=np.float64)[t])[::-1]
-        ulp = 2.0 ** (np.floor(np.log2(max(abs(lg[k - 1]), abs(lg[k]), 1e-30))) - 7)
-        assert lg[k - 1] - lg[k] <= 2 * ulp, f"token {t} routed differently without a near-tie"
-    return np.setdiff1d(np.arange(ids.shape[0]), bad)
-
-
 TREES = {
     "tree8": ([-1, 0, 1, 2, 0, 4, 1, 6], [0, 1, 2, 3, 1, 2, 2, 3]),
     "root_not_first": ([1, -1, 1, 0, 3], [1, 0, 1, 2, 3]),
@@ -68,7 +55,7 @@ def test_tree_decode_per_layer_vs_oracle(name, start, M):
         # the layer output, on every token whose routing agrees (a token may route differently only
         # where the oracle's k-th and (k+1)-th logits are a near-tie the bf16 input rounding can flip)
         ids = st.debug_buffer(4, torch.int32, (M, shape.top_k)).cpu().numpy()
-        good = _tokens_with_same_routing(ids, tr["ids"], tr["logits"], shape.top_k)
+        good = gh.tokens_with_same_routing(ids, tr["ids"], tr["logits"], shape.top_k)
         mar, cos_ = gh.metrics(gh.cpu_f32(h).numpy()[good], ref.numpy()[good])
         print(f"  layer {l}: {len(good)}/{M} tokens routed alike, max-abs-rel {mar:.3e} cos {cos_:.6f}", flush=True)
         assert mar <= 2e-2 and cos_ >= 0.999, (l, mar, cos_)

@@ -327,6 +327,110 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_logits_kernel(
   }
 }
 
+// ---- prefill-sized projections: a tiled GEMM with the split-K kernel's per-element arithmetic ------
+// For many rows the split-K kernel re-stages its activation slice once per 64-row pass and leaves
+// gemm_slices(K) fp32 partial planes for the finalizers.  This kernel tiles M x N instead: a
+// workgroup of 4 waves (2 x 2) owns 128 rows x 128 features, each wave 64 x 64 (4 x 4 MFMA tiles).
+// Per 128-K group the activation and weight tiles are staged in LDS in MFMA-fragment order (tile t,
+// step j: one KiB, lane (r, g) holding row/feature 16t + r, K 32j + 8g .. +7), so every fragment read
+// is a lane-contiguous ds_read_b128; the next group's global loads are in flight during the current
+// group's MFMAs.  Arithmetic per output element is exactly the split-K kernel's: the same MFMA with
+// the same K-to-lane mapping (activations as A, weights as B), each 512-K slice accumulated from zero
+// in (group, step) order, and the slices added left to right in fp32 -- so the one folded plane it
+// writes equals sum_slices of the split-K planes bit for bit, and a row's result does not depend on
+// which kernel the batch size chose.
+constexpr int kTileM = 128, kTileN = 128;
+constexpr int kTiledWaves = 8;      // 4 (rows) x 2 (features), each wave 32 rows x 64 features
+constexpr int kTiledMinRows = 256;  // batches of at least this many rows take the tiled kernel
+
+__global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_bf16_kernel(const uint16_t* __restrict__ x,
+                                                                           const uint16_t* __restrict__ W,
+                                                                           int M, int N, int K,
+                                                                           float* __restrict__ out) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  __shared__ u32x4 as[kTileM / 16][4][64];  // [row tile][step][lane]
+  __shared__ u32x4 ws[kTileN / 16][4][64];  // [feature tile][step][lane]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.y * kTileM, n0 = blockIdx.x * kTileN;
+  const int wm = wave >> 1, wn = wave & 1;  // the wave's 32 x 64 block: row tiles 2wm, 2wm+1
+  const int KG = (K + 127) / 128;
+  // staging: each wave fills whole fragment slabs (tile t, step j) -- slab u = 4 wave + i (i < 4) of
+  // each operand is tile u / 4, step u % 4 -- so its 64 LDS stores are one contiguous KiB (no bank
+  // conflicts); lane (r, g) loads row/feature 16t + r, K 128q + 32j + 8g .. +7
+  constexpr int kSlabs = 32 / kTiledWaves;
+  const int sr = lane & 15, sg = lane >> 4;
+  u32x4 ra[kSlabs], rw[kSlabs];
+  auto load_group = [&](int q) {
+#pragma unroll
+    for (int i = 0; i < kSlabs; ++i) {
+      const int u = kSlabs * wave + i, t = u >> 2, j = u & 3;
+      const int k = 128 * q + 32 * j + 8 * sg;
+      const int row = m0 + 16 * t + sr, feat = n0 + 16 * t + sr;
+      ra[i] = (row < M && k < K) ? *reinterpret_cast<const u32x4*>(x + (size_t)row * K + k) : u32x4{0u, 0u, 0u, 0u};
+      rw[i] = (feat < N && k < K) ? *reinterpret_cast<const u32x4*>(W + (size_t)feat * K + k) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_group = [&]() {
+#pragma unroll
+    for (int i = 0; i < kSlabs; ++i) {
+      const int u = kSlabs * wave + i;
+      as[u >> 2][u & 3][lane] = ra[i];
+      ws[u >> 2][u & 3][lane] = rw[i];
+    }
+  };
+  f32x4_t acc[2][4], tot[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      tot[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  load_group(0);
+  for (int q = 0; q < KG; ++q) {
+    lds_barrier();  // every wave is done with the previous group's tiles
+    store_group();
+    if (q + 1 < KG) load_group(q + 1);
+    lds_barrier();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      bf16x8_t af[2], bw[4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) af[t] = __builtin_bit_cast(bf16x8_t, as[2 * wm + t][j][lane]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) bw[t] = __builtin_bit_cast(bf16x8_t, ws[4 * wn + t][j][lane]);
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = mfma16x16x32(af[a], bw[b], acc[a][b]);
+    }
+    if ((q % kKQW) == kKQW - 1 || q == KG - 1) {  // the end of a 512-K slice: fold it, in slice order
+      const bool first = q < kKQW;
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          tot[a][b] = first ? acc[a][b] : tot[a][b] + acc[a][b];
+          acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+  }
+  // lane (r, g) holds rows 16(2wm + a) + 4g + v of feature 16(4wn + b) + r
+  const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int feat = n0 + 16 * (4 * wn + b) + r;
+      if (feat >= N) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + 16 * (2 * wm + a) + 4 * g + v;
+        if (row < M) out[(size_t)row * N + feat] = tot[a][b][v];
+      }
+    }
+}
+
 int gemm_slices(int K) { return ((K + 127) / 128 + kKQW - 1) / kKQW; }
 
 size_t linear_partials_bytes(int M, int N, int K) { return (size_t)gemm_slices(K) * M * N * sizeof(float); }
@@ -338,14 +442,30 @@ int launch_gemm_splitk(const uint16_t* x, const uint16_t* W, int M, int N, int K
   return check_launch("gemm_splitk_bf16");
 }
 
+// x . W^T into fp32 partial planes for a finalizer: the split-K kernel (gemm_slices(K) planes) for
+// decode-sized M, the tiled kernel (one folded plane, same bits) from kTiledMinRows rows.
+int launch_gemm(const uint16_t* x, const uint16_t* W, int M, int N, int K, float* part, int* slices,
+                hipStream_t s) {
+  if (M >= kTiledMinRows) {
+    *slices = 1;
+    hipLaunchKernelGGL(gemm_tiled_bf16_kernel, dim3(ceil_div(N, kTileN), ceil_div(M, kTileM)),
+                       dim3(64 * kTiledWaves), 0, s,
+                       x, W, M, N, K, part);
+    return check_launch("gemm_tiled_bf16");
+  }
+  *slices = gemm_slices(K);
+  return launch_gemm_splitk(x, W, M, N, K, part, s);
+}
+
 int launch_linear(const uint16_t* x, const uint16_t* W, const uint16_t* b, int M, int N, int K,
                   uint16_t* y, uint16_t* residual, float* part, hipStream_t s) {
   if (M == 0) return FLYAI_OK;
-  int rc = launch_gemm_splitk(x, W, M, N, K, part, s);
+  int slices = 0;
+  int rc = launch_gemm(x, W, M, N, K, part, &slices, s);
   if (rc) return rc;
   const size_t total = (size_t)M * N;
   hipLaunchKernelGGL(linear_finalize_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                     part, gemm_slices(K), b, M, N, y, residual);
+                     part, slices, b, M, N, y, residual);
   return check_launch("linear_finalize");
 }
 
@@ -353,10 +473,10 @@ int launch_linear_residual_rmsnorm(const uint16_t* x, const uint16_t* W, const u
                                    int N, int K, uint16_t* h, const float* lnw, float eps,
                                    uint16_t* xn, float* part, hipStream_t s) {
   if (M == 0) return FLYAI_OK;
-  int rc = launch_gemm_splitk(x, W, M, N, K, part, s);
+  int slices = 0;
+  int rc = launch_gemm(x, W, M, N, K, part, &slices, s);
   if (rc) return rc;
-  hipLaunchKernelGGL(residual_rmsnorm_finalize_kernel, dim3(M), dim3(kRowThreads), 0, s, part,
-                     gemm_slices(K),
+  hipLaunchKernelGGL(residual_rmsnorm_finalize_kernel, dim3(M), dim3(kRowThreads), 0, s, part, slices,
                      b, M, N, h, lnw, eps, xn);
   return check_launch("residual_rmsnorm_finalize");
 }
@@ -374,9 +494,9 @@ int launch_linear_residual_rmsnorm_logits(const uint16_t* x, const uint16_t* W, 
   if (M == 0) return FLYAI_OK;
   if (M > kFusedRouteTokens || N > 7168 || N % 8 || E > 256)
     return set_error(FLYAI_EINVAL, "fused router logits: needs T <= 256, H %% 8 == 0, H <= 7168, E <= 256");
-  int rc = launch_gemm_splitk(x, W, M, N, K, part, s);
+  int slices = 0;
+  int rc = launch_gemm(x, W, M, N, K, part, &slices, s);
   if (rc) return rc;
-  const int slices = gemm_slices(K);
   if (N <= 3072)
     hipLaunchKernelGGL((residual_rmsnorm_logits_kernel<6>), dim3(M, kRouteSplit), dim3(kRowThreads), 0, s,
                        part, slices, b, M, N, h_in, h_out, lnw, eps, xn, rw, rb, E, logits);
@@ -535,9 +655,9 @@ int launch_qkv_rope_kv(const uint16_t* x, const uint16_t* Wqkv, const uint16_t* 
                        uint16_t* k_pool, uint16_t* v_pool, const int32_t* kv_pos, hipStream_t s) {
   if (T == 0) return FLYAI_OK;
   const int width = (Hq + 2 * Hkv) * D;
-  int rc = launch_gemm_splitk(x, Wqkv, T, width, H, part, s);
+  int slices = 0;
+  int rc = launch_gemm(x, Wqkv, T, width, H, part, &slices, s);
   if (rc) return rc;
-  const int slices = gemm_slices(H);
   if (D % 8 == 0 && slices <= 16) {
     const int units = (Hq + Hkv) * (D / 8) + Hkv * (D / 4);
     const dim3 grid(T, ceil_div(units, 256));

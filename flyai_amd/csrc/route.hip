@@ -394,7 +394,20 @@ __global__ __launch_bounds__(kPermWaves * 64) void moe_topk_permute_kernel(
   // in LDS with coalesced loads (rows padded by 16 bytes), so the selection never waits on memory
   const bool staged = T * (E + 4) <= kStagedLogits;
   if (staged) {
-    for (int i = threadIdx.x; i < T * E; i += kPermWaves * 64) lg_s[(i / E) * (E + 4) + i % E] = logits[i];
+    // every load of the thread goes out before the first LDS store (one round trip, not one per
+    // element): T * E < kStagedLogits = 8 per thread
+    constexpr int kPer = kStagedLogits / (kPermWaves * 64);
+    float v[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = threadIdx.x + j * kPermWaves * 64;
+      v[j] = i < T * E ? logits[i] : 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      const int i = threadIdx.x + j * kPermWaves * 64;
+      if (i < T * E) lg_s[(i / E) * (E + 4) + i % E] = v[j];
+    }
     __syncthreads();
   }
   if (staged && E % 16 == 0) {

@@ -230,6 +230,25 @@ def test_rmsnorm_and_linear_vs_oracle():
     assert mar < 1e-2 and cos > 0.9999
 
 
+@pytest.mark.parametrize("N,K", [(5120, 2880), (2880, 4096), (2000, 2880)])
+def test_linear_tiled_equals_split_k_bit_exact(N, K):
+    """Prefill-sized batches (>= 256 rows) take the tiled GEMM, decode-sized ones the split-K GEMM;
+    a row's projection must come out the same bits either way (batch invariance), and within the bar
+    of the oracle."""
+    from flyai_amd import ops
+    M = 300
+    x = torch.randn(M, K, device=DEV, generator=_gen(110)).to(torch.bfloat16)
+    w = (0.02 * torch.randn(N, K, device=DEV, generator=_gen(111))).to(torch.bfloat16)
+    b = (0.1 * torch.randn(N, device=DEV, generator=_gen(112))).to(torch.bfloat16)
+    big = ops.linear(x, w, b)                       # tiled path
+    parts = [ops.linear(x[r0:r0 + 60].contiguous(), w, b) for r0 in range(0, M, 60)]  # split-K path
+    torch.cuda.synchronize()
+    assert torch.equal(big, torch.cat(parts)), "tiled and split-K projections differ"
+    ref = olayer.linear(x.float().cpu(), w.float().cpu(), b.float().cpu())
+    mar, cos = _metrics(big.float().cpu().numpy(), ref.numpy())
+    assert mar < 1e-2 and cos > 0.99999
+
+
 def test_rope_kv_append_bit_exact():
     from flyai_amd import ops
     from flyai_amd.rope import YarnRotary

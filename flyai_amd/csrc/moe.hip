@@ -69,9 +69,9 @@ __global__ __launch_bounds__(256) void mxfp4_repack_kernel(const uint8_t* __rest
 // Workgroup = 4 waves = 4*NTW weight tiles (16 output rows each) of one expert, full K.  The
 // expert's activation rows are staged in LDS, kRowsPerPass at a time, with fully coalesced loads
 // (one pass serves every tile of the workgroup), so the only vector-memory loads in the K loop are
-// the weights: 1 KiB per tile per group of 128 K, streamed through a 4-deep register ring with
-// non-temporal loads (3 groups in flight while one computes).  Each group is dequantised in registers (gfx950 v_cvt_scalef32_pk_bf16_fp4,
-// E8M0 scale in the exponent field) and fed to v_mfma_f32_16x16x32_bf16 with the activation
+// the weights: 1 KiB per tile per group of 128 K, streamed through a DEPTH-deep register ring with
+// non-temporal loads (DEPTH - 1 groups in flight while one computes).  Each group is dequantised in
+// registers (gfx950 v_cvt_scalef32_pk_bf16_fp4, E8M0 scale in the exponent field) and fed to v_mfma_f32_16x16x32_bf16 with the activation
 // fragment read from LDS (rows >= the pass's row count read as zero).  Larger groups take further
 // passes over the weights.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
@@ -89,11 +89,20 @@ __device__ __forceinline__ float swiglu_gptoss(float gate, float up) {
   return (u + 1.0f) * glu;
 }
 
+// compile-time loop: f(integral_constant<int, B>) ... f(integral_constant<int, N-1>)
+template <int B, int N, class F>
+__device__ __forceinline__ void mx_static_for(F&& f) {
+  if constexpr (B < N) {
+    f(std::integral_constant<int, B>{});
+    mx_static_for<B + 1, N>(f);
+  }
+}
+
 constexpr int kRowsPerPass = 8;
 
 __host__ __device__ inline int mx_lds_row_bytes(int K) { return K * 2 + 16; }  // +16 B vs bank conflicts
 
-template <bool GATE_UP, int NTW>
+template <bool GATE_UP, int NTW, int DEPTH>
 __global__ __launch_bounds__(256) void moe_mxfp4_kernel(
     const uint16_t* __restrict__ act, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, int k_top, const uint8_t* __restrict__ packed,
@@ -180,27 +189,24 @@ __global__ __launch_bounds__(256) void moe_mxfp4_kernel(
       }
     };
 
-    // Static bodies of 4 groups: a 4-deep weight ring (3 groups in flight while one computes) and
-    // the next body's scale dword loaded one body ahead, so no wait ever drains the ring.
-    uint4 w0[NTW], w1[NTW], w2[NTW], w3[NTW];
-    uint32_t sc_cur[NTW], sc_nxt[NTW];
-    load_sc(sc_cur, 0);
-    load_w(w0, 0);
-    load_w(w1, 1);
-    load_w(w2, 2);
-    for (int kg4 = 0; kg4 < gm.KG4; ++kg4) {
-      const int kg = 4 * kg4;
-      load_sc(sc_nxt, kg4 + 1);
-      load_w(w3, kg + 3);
-      compute(w0, sc_cur, kg, 0);
-      load_w(w0, kg + 4);
-      compute(w1, sc_cur, kg + 1, 1);
-      load_w(w1, kg + 5);
-      compute(w2, sc_cur, kg + 2, 2);
-      load_w(w2, kg + 6);
-      compute(w3, sc_cur, kg + 3, 3);
+    // Static bodies of DEPTH groups: a DEPTH-deep weight ring (DEPTH - 1 groups in flight while one
+    // computes) and the next body's scale dwords loaded one body ahead, so no wait drains the ring.
+    static_assert(DEPTH % 4 == 0, "a body covers whole scale dwords (4 groups each)");
+    constexpr int kSc = DEPTH / 4;
+    uint4 w[DEPTH][NTW];
+    uint32_t sc_cur[kSc][NTW], sc_nxt[kSc][NTW];
+    mx_static_for<0, kSc>([&](auto q) { load_sc(sc_cur[q], q); });
+    mx_static_for<0, DEPTH - 1>([&](auto j) { load_w(w[j], j); });
+    for (int kg0 = 0; kg0 < gm.KG; kg0 += DEPTH) {
+      mx_static_for<0, kSc>([&](auto q) { load_sc(sc_nxt[q], kg0 / 4 + kSc + q); });
+      mx_static_for<0, DEPTH>([&](auto j) {
+        load_w(w[(j + DEPTH - 1) % DEPTH], kg0 + j + DEPTH - 1);
+        compute(w[j], sc_cur[j / 4], kg0 + j, j % 4);
+      });
+      mx_static_for<0, kSc>([&](auto q) {
 #pragma unroll
-      for (int n = 0; n < NTW; ++n) sc_cur[n] = sc_nxt[n];
+        for (int n = 0; n < NTW; ++n) sc_cur[q][n] = sc_nxt[q][n];
+      });
     }
 
     // epilogue: lane holds D[act row 4g+v][feature r] of each tile
@@ -228,20 +234,28 @@ __global__ __launch_bounds__(256) void moe_mxfp4_kernel(
 }
 
 constexpr int kNTW = 2;  // weight tiles per wave
-// weight tiles per wave of the decode-sized kernels: 3 divides both projections' tile counts at
-// GPT-OSS shapes (gate_up 360 = 30 x 12, down 180 = 15 x 12), so no workgroup runs half empty;
-// measured at C1 against 1, 2 and 5 (2: gate_up 146.5 / down 84.7 us, 3: 144.6 / 81.3 us)
-constexpr int kNTWGateUp = 3;
-constexpr int kNTWDown = 3;
-
-// compile-time loop: f(integral_constant<int, B>) ... f(integral_constant<int, N-1>)
-template <int B, int N, class F>
-__device__ __forceinline__ void mx_static_for(F&& f) {
-  if constexpr (B < N) {
-    f(std::integral_constant<int, B>{});
-    mx_static_for<B + 1, N>(f);
-  }
-}
+// Weight tiles per wave and weight-ring depth (128-K groups) of the decode-sized kernels.  Two tiles
+// and an 8-deep ring keep 14 KiB in flight per wave at 3 waves per SIMD (166 registers), against
+// 9 KiB for 3 tiles and a 4-deep ring (162 registers); the workgroups are also a third smaller, so
+// the end of the launch, where the last workgroups run alone, is shorter.  Measured on the C1 step
+// (9 layers, A/B on one box): 3 tiles x 4 deep 3.13 ms; 2 x 8 3.04 ms; 1 x 8, 2 x 4 and 2 x 12 for
+// gate_up and 1 x 8, 1 x 16 and 2 x 12 for down all slower.  The macros allow such sweeps.
+#ifndef FLYAI_MOE_NTW_GATE_UP
+#define FLYAI_MOE_NTW_GATE_UP 2
+#endif
+#ifndef FLYAI_MOE_NTW_DOWN
+#define FLYAI_MOE_NTW_DOWN 2
+#endif
+#ifndef FLYAI_MOE_DEPTH_GATE_UP
+#define FLYAI_MOE_DEPTH_GATE_UP 8
+#endif
+#ifndef FLYAI_MOE_DEPTH_DOWN
+#define FLYAI_MOE_DEPTH_DOWN 8
+#endif
+constexpr int kNTWGateUp = FLYAI_MOE_NTW_GATE_UP;
+constexpr int kNTWDown = FLYAI_MOE_NTW_DOWN;
+constexpr int kDepthGateUp = FLYAI_MOE_DEPTH_GATE_UP;
+constexpr int kDepthDown = FLYAI_MOE_DEPTH_DOWN;
 
 // ---- dense groups as a tiled GEMM ----------------------------------------------------------------
 // For groups of many rows the weights are still read once from HBM, but each weight byte now feeds
@@ -599,7 +613,7 @@ int launch_moe_gate_up(const uint16_t* x, const int32_t* perm, const int32_t* of
   const bool dense = use_dense(T * k_top, E) && H >= 128;  // the tiled kernel reads 128-K groups
   if (H <= 4064) {
     const int wg_per_e = ceil_div(gm.NT, 4 * kNTWGateUp);
-    hipLaunchKernelGGL((moe_mxfp4_kernel<true, kNTWGateUp>), dim3(E * wg_per_e), dim3(256),
+    hipLaunchKernelGGL((moe_mxfp4_kernel<true, kNTWGateUp, kDepthGateUp>), dim3(E * wg_per_e), dim3(256),
                        kRowsPerPass * mx_lds_row_bytes(H), s, x, perm, offsets, k_top, w13, b13, E,
                        2 * I, H, 1, dense ? kDenseFrom : (1 << 30), (void*)h);
     int rc = check_launch("moe_gate_up_mxfp4");
@@ -621,7 +635,7 @@ int launch_moe_down(const uint16_t* h, const int32_t* offsets, const uint8_t* w2
   const bool dense = use_dense(rows_total, E) && I >= 128;  // the tiled kernel reads 128-K groups
   if (I <= 4064) {
     const int wg_per_e = ceil_div(gm.NT, 4 * kNTWDown);
-    hipLaunchKernelGGL((moe_mxfp4_kernel<false, kNTWDown>), dim3(E * wg_per_e), dim3(256),
+    hipLaunchKernelGGL((moe_mxfp4_kernel<false, kNTWDown, kDepthDown>), dim3(E * wg_per_e), dim3(256),
                        kRowsPerPass * mx_lds_row_bytes(I), s, h, nullptr, offsets, 1, w2, b2, E, H, I, 1,
                        dense ? kDenseFrom : (1 << 30), (void*)y);
     int rc = check_launch("moe_down_mxfp4");

@@ -103,7 +103,7 @@ constexpr int kRowsPerPass = 8;
 __host__ __device__ inline int mx_lds_row_bytes(int K) { return K * 2 + 16; }  // +16 B vs bank conflicts
 
 template <bool GATE_UP, int NTW, int DEPTH>
-__global__ __launch_bounds__(256) void moe_mxfp4_kernel(
+__global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
     const uint16_t* __restrict__ act, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, int k_top, const uint8_t* __restrict__ packed,
     const float* __restrict__ bias, int E, int N, int K, int min_rows, int max_rows,
@@ -131,49 +131,64 @@ __global__ __launch_bounds__(256) void moe_mxfp4_kernel(
   const size_t scale_stride = (size_t)gm.KG4 * 64;
   const char* lds = reinterpret_cast<const char*>(xs_lds);
 
+  auto load_w = [&](uint4 (&w)[NTW], int kg) {
+    const bool bvalid = kg < gm.KG && 4 * kg + g < gm.G;
+#pragma unroll
+    for (int n = 0; n < NTW; ++n)
+      w[n] = (bvalid && n < ntw) ? ld_nt(data + n * tile_stride + (size_t)kg * 1024) : make_uint4(0, 0, 0, 0);
+  };
+  auto load_sc = [&](uint32_t (&sc)[NTW], int kg4) {
+#pragma unroll
+    for (int n = 0; n < NTW; ++n) sc[n] = (kg4 < gm.KG4 && n < ntw) ? scl[n * scale_stride + kg4 * 64] : 0u;
+  };
+  // Static bodies of DEPTH groups: a DEPTH-deep weight ring (DEPTH - 1 groups in flight while one
+  // computes) and the next body's scale dwords loaded one body ahead, so no wait drains the ring.
+  static_assert(DEPTH % 4 == 0, "a body covers whole scale dwords (4 groups each)");
+  constexpr int kSc = DEPTH / 4;
+  uint4 w[DEPTH][NTW];
+  uint32_t sc_cur[kSc][NTW], sc_nxt[kSc][NTW];
+
   for (int m0 = 0; m0 < n_e; m0 += kRowsPerPass) {
     const int rows = min(kRowsPerPass, n_e - m0);
-    __syncthreads();  // the previous pass is done with the LDS rows
-    // staging loads go out in batches of 4 per thread (one round trip per batch, not per vector);
-    // indices past the end are clamped for the load and not stored
+    lds_barrier();  // the previous pass is done with the LDS rows
+    // staging loads go out in batches of kStageBatch per thread (one round trip per batch, not per
+    // vector); indices past the end are clamped for the load and not stored.  Batches of 5
+    // measured 4% slower on the C1 step than 4.  The pass's first weight groups are requested right
+    // after the first batch, so the weight stream does not wait for the activation round trip; the
+    // LDS-only barrier below leaves them in flight.
+    constexpr int kStageBatch = 4;
     const int total = rows * row_vecs;
-    for (int b0 = 0; b0 < total; b0 += 4 * 256) {
-      u32x4_t v4[4];
+    for (int b0 = 0; b0 < total; b0 += kStageBatch * 256) {
+      u32x4_t v4[kStageBatch];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kStageBatch; ++j) {
         const int i = min(b0 + j * 256 + (int)threadIdx.x, total - 1);
         const int rr = i / row_vecs, v = i % row_vecs;
         const int p = row_lo + m0 + rr;
         const int src = GATE_UP ? perm[p] / k_top : p;
         v4[j] = reinterpret_cast<const u32x4_t*>(act + (size_t)src * K)[v];
       }
+      if (b0 == 0) {
+        mx_static_for<0, kSc>([&](auto q) { load_sc(sc_cur[q], q); });
+        mx_static_for<0, DEPTH - 1>([&](auto j) { load_w(w[j], j); });
+      }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kStageBatch; ++j) {
         const int i = b0 + j * 256 + (int)threadIdx.x;
         if (i < total)
           *reinterpret_cast<u32x4_t*>(const_cast<char*>(lds) + (i / row_vecs) * row_bytes + (i % row_vecs) * 16) = v4[j];
       }
     }
-    __syncthreads();
+    lds_barrier();
     if (ntw == 0) continue;
     const bool aval = r < rows;
     const char* arow = lds + r * row_bytes + 64 * g;
 
-    auto load_w = [&](uint4 (&w)[NTW], int kg) {
-      const bool bvalid = kg < gm.KG && 4 * kg + g < gm.G;
-#pragma unroll
-      for (int n = 0; n < NTW; ++n)
-        w[n] = (bvalid && n < ntw) ? ld_nt(data + n * tile_stride + (size_t)kg * 1024) : make_uint4(0, 0, 0, 0);
-    };
-    auto load_sc = [&](uint32_t (&sc)[NTW], int kg4) {
-#pragma unroll
-      for (int n = 0; n < NTW; ++n) sc[n] = (kg4 < gm.KG4 && n < ntw) ? scl[n * scale_stride + kg4 * 64] : 0u;
-    };
     f32x4_t acc[NTW];
 #pragma unroll
     for (int n = 0; n < NTW; ++n) acc[n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     // byte b of sc[n] is the E8M0 scale of group 4*kg4 + b
-    auto compute = [&](const uint4 (&w)[NTW], const uint32_t (&sc)[NTW], int kg, int b) {
+    auto compute = [&](const uint4 (&wg)[NTW], const uint32_t (&sc)[NTW], int kg, int b) {
       uint4 a[4];
       const bool ok = aval && kg < gm.KG && 4 * kg + g < gm.G;
 #pragma unroll
@@ -182,21 +197,13 @@ __global__ __launch_bounds__(256) void moe_mxfp4_kernel(
 #pragma unroll
       for (int n = 0; n < NTW; ++n) {
         const float scale = e8m0_operand((sc[n] >> (8 * b)) & 0xffu);
-        const uint32_t wd[4] = {w[n].x, w[n].y, w[n].z, w[n].w};
+        const uint32_t wd[4] = {wg[n].x, wg[n].y, wg[n].z, wg[n].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           acc[n] = mfma16x16x32(as_bf16x8(a[j]), fp4x8_to_bf16x8(wd[j], scale), acc[n]);
       }
     };
 
-    // Static bodies of DEPTH groups: a DEPTH-deep weight ring (DEPTH - 1 groups in flight while one
-    // computes) and the next body's scale dwords loaded one body ahead, so no wait drains the ring.
-    static_assert(DEPTH % 4 == 0, "a body covers whole scale dwords (4 groups each)");
-    constexpr int kSc = DEPTH / 4;
-    uint4 w[DEPTH][NTW];
-    uint32_t sc_cur[kSc][NTW], sc_nxt[kSc][NTW];
-    mx_static_for<0, kSc>([&](auto q) { load_sc(sc_cur[q], q); });
-    mx_static_for<0, DEPTH - 1>([&](auto j) { load_w(w[j], j); });
     for (int kg0 = 0; kg0 < gm.KG; kg0 += DEPTH) {
       mx_static_for<0, kSc>([&](auto q) { load_sc(sc_nxt[q], kg0 / 4 + kSc + q); });
       mx_static_for<0, DEPTH>([&](auto j) {

@@ -110,6 +110,61 @@ inline hipStream_t as_stream(flyai_stream_t s) { return reinterpret_cast<hipStre
 
 inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 
+// Sorted top-K list helpers, branch-free (compare + select), so lanes of a wave never diverge.
+// topk_insert_strict: (v, id) enters in front of the first entry it strictly exceeds and every
+// entry behind it moves down one place (the last falls off) -- equal values keep the earlier (lower)
+// id ahead, the same list a strict-greater insertion at the end followed by bubbling past strictly
+// smaller values gives.  (Comparing the displaced entry again instead of moving it would swap two
+// equal values.)  topk_insert_ordered: the same under (value desc, id asc).
+template <int K>
+__device__ __forceinline__ void topk_insert_strict(float (&sv)[K], int (&si)[K], float v, int id) {
+  bool moved = false;  // once the new entry is in, every later entry moves down unconditionally
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const bool gt = moved || v > sv[j];
+    moved = gt;
+    const float tv = sv[j];
+    const int ti = si[j];
+    sv[j] = gt ? v : tv;
+    si[j] = gt ? id : ti;
+    v = gt ? tv : v;
+    id = gt ? ti : id;
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void topk_insert_ordered(float (&sv)[K], int (&si)[K], float v, int id) {
+  bool moved = false;
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const bool gt = moved || v > sv[j] || (v == sv[j] && id < si[j]);
+    moved = gt;
+    const float tv = sv[j];
+    const int ti = si[j];
+    sv[j] = gt ? v : tv;
+    si[j] = gt ? id : ti;
+    v = gt ? tv : v;
+    id = gt ? ti : id;
+  }
+}
+
+// ids ascending, carrying their weights (odd-even transposition sort, K passes, branch-free)
+template <int K>
+__device__ __forceinline__ void sort_ids_with_weights(int (&si)[K], float (&ex)[K]) {
+#pragma unroll
+  for (int pass = 0; pass < K; ++pass)
+#pragma unroll
+    for (int j = pass & 1; j + 1 < K; j += 2) {
+      const bool sw = si[j] > si[j + 1];
+      const int a = si[j], b = si[j + 1];
+      const float x = ex[j], y = ex[j + 1];
+      si[j] = sw ? b : a;
+      si[j + 1] = sw ? a : b;
+      ex[j] = sw ? y : x;
+      ex[j + 1] = sw ? x : y;
+    }
+}
+
 // Top-k + softmax of one token by one lane.  The lane streams its token's logits in ascending expert
 // id and keeps a sorted list of K (value, id); a value enters only if strictly greater than the
 // current K-th and bubbles up past strictly smaller values, so equal values keep ascending ids --
@@ -133,31 +188,13 @@ __device__ __forceinline__ void topk_softmax_lane(const float* __restrict__ lrow
       const float4& q = v4[i >> 2];
       const float v = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
       const int id = e0 + i;
-      if (id < E && v > sv[K - 1]) {
-        sv[K - 1] = v;
-        si[K - 1] = id;
-#pragma unroll
-        for (int j = K - 1; j > 0; --j) {
-          if (sv[j] > sv[j - 1]) {
-            const float tv = sv[j]; sv[j] = sv[j - 1]; sv[j - 1] = tv;
-            const int ti = si[j]; si[j] = si[j - 1]; si[j - 1] = ti;
-          }
-        }
-      }
+      topk_insert_strict<K>(sv, si, id < E ? v : -INFINITY, id);
     }
   }
   float ex[K], sum = 0.f;
 #pragma unroll
   for (int j = 0; j < K; ++j) { ex[j] = expf(sv[j] - sv[0]); sum += ex[j]; }
-  // ascending ids (odd-even transposition sort, K passes)
-#pragma unroll
-  for (int pass = 0; pass < K; ++pass)
-#pragma unroll
-    for (int j = pass & 1; j + 1 < K; j += 2)
-      if (si[j] > si[j + 1]) {
-        const int ti = si[j]; si[j] = si[j + 1]; si[j + 1] = ti;
-        const float te = ex[j]; ex[j] = ex[j + 1]; ex[j + 1] = te;
-      }
+  sort_ids_with_weights<K>(si, ex);
 #pragma unroll
   for (int j = 0; j < K; ++j) {
     ids_out[j] = si[j];
@@ -201,14 +238,7 @@ __device__ __forceinline__ void topk_softmax_wave_vals(const float (&v)[4], int 
   float ex[K], sum = 0.f;
 #pragma unroll
   for (int j = 0; j < K; ++j) { ex[j] = expf(sv[j] - sv[0]); sum += ex[j]; }
-#pragma unroll
-  for (int pass = 0; pass < K; ++pass)
-#pragma unroll
-    for (int j = pass & 1; j + 1 < K; j += 2)
-      if (si[j] > si[j + 1]) {
-        const int ti = si[j]; si[j] = si[j + 1]; si[j + 1] = ti;
-        const float te = ex[j]; ex[j] = ex[j + 1]; ex[j + 1] = te;
-      }
+  sort_ids_with_weights<K>(si, ex);
 #pragma unroll
   for (int j = 0; j < K; ++j)
     if (lane == j) {
@@ -251,18 +281,7 @@ __device__ __forceinline__ void topk_softmax_quad(const float* __restrict__ lrow
     const float4 q = *reinterpret_cast<const float4*>(lrow + e0);
     const float vv[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (vv[i] > sv[K - 1]) {
-        sv[K - 1] = vv[i];
-        si[K - 1] = e0 + i;
-#pragma unroll
-        for (int j = K - 1; j > 0; --j)
-          if (sv[j] > sv[j - 1]) {
-            const float tv = sv[j]; sv[j] = sv[j - 1]; sv[j - 1] = tv;
-            const int ti = si[j]; si[j] = si[j - 1]; si[j - 1] = ti;
-          }
-      }
-    }
+    for (int i = 0; i < 4; ++i) topk_insert_strict<K>(sv, si, vv[i], e0 + i);
   }
 #pragma unroll
   for (int o = 1; o <= 2; o <<= 1) {
@@ -271,32 +290,12 @@ __device__ __forceinline__ void topk_softmax_quad(const float* __restrict__ lrow
 #pragma unroll
     for (int j = 0; j < K; ++j) { pv[j] = __shfl_xor(sv[j], o, 64); pi[j] = __shfl_xor(si[j], o, 64); }
 #pragma unroll
-    for (int m = 0; m < K; ++m) {
-      // insert (pv[m], pi[m]) under (value desc, id asc)
-      const bool in = pv[m] > sv[K - 1] || (pv[m] == sv[K - 1] && pi[m] < si[K - 1]);
-      if (in) {
-        sv[K - 1] = pv[m];
-        si[K - 1] = pi[m];
-#pragma unroll
-        for (int j = K - 1; j > 0; --j)
-          if (sv[j] > sv[j - 1] || (sv[j] == sv[j - 1] && si[j] < si[j - 1])) {
-            const float tv = sv[j]; sv[j] = sv[j - 1]; sv[j - 1] = tv;
-            const int ti = si[j]; si[j] = si[j - 1]; si[j - 1] = ti;
-          }
-      }
-    }
+    for (int m = 0; m < K; ++m) topk_insert_ordered<K>(sv, si, pv[m], pi[m]);
   }
   float ex[K], sum = 0.f;
 #pragma unroll
   for (int j = 0; j < K; ++j) { ex[j] = expf(sv[j] - sv[0]); sum += ex[j]; }
-#pragma unroll
-  for (int pass = 0; pass < K; ++pass)
-#pragma unroll
-    for (int j = pass & 1; j + 1 < K; j += 2)
-      if (si[j] > si[j + 1]) {
-        const int ti = si[j]; si[j] = si[j + 1]; si[j + 1] = ti;
-        const float te = ex[j]; ex[j] = ex[j + 1]; ex[j + 1] = te;
-      }
+  sort_ids_with_weights<K>(si, ex);
   if (sub == 0) {
 #pragma unroll
     for (int j = 0; j < K; ++j) {

@@ -114,38 +114,37 @@ inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
 // topk_insert_strict: (v, id) enters in front of the first entry it strictly exceeds and every
 // entry behind it moves down one place (the last falls off) -- equal values keep the earlier (lower)
 // id ahead, the same list a strict-greater insertion at the end followed by bubbling past strictly
-// smaller values gives.  (Comparing the displaced entry again instead of moving it would swap two
-// equal values.)  topk_insert_ordered: the same under (value desc, id asc).
+// smaller values gives.  Every comparison is of the new entry (comparing a displaced entry again
+// would swap two equal values), and no comparison waits on another.  topk_insert_ordered: the same under (value desc, id asc).
 template <int K>
-__device__ __forceinline__ void topk_insert_strict(float (&sv)[K], int (&si)[K], float v, int id) {
-  bool moved = false;  // once the new entry is in, every later entry moves down unconditionally
+__device__ __forceinline__ void topk_insert_at(float (&sv)[K], int (&si)[K], float v, int id, const bool (&gt)[K]) {
+  // gt[] is monotonic over the sorted list (false ... false, true ... true): the new entry goes to
+  // the first true position and the entries from there on shift down one place; slot j reads only
+  // slot j-1, so walking down from the end overwrites nothing still needed
 #pragma unroll
-  for (int j = 0; j < K; ++j) {
-    const bool gt = moved || v > sv[j];
-    moved = gt;
-    const float tv = sv[j];
-    const int ti = si[j];
-    sv[j] = gt ? v : tv;
-    si[j] = gt ? id : ti;
-    v = gt ? tv : v;
-    id = gt ? ti : id;
+  for (int j = K - 1; j >= 0; --j) {
+    const bool prev = j > 0 && gt[j - 1];
+    const float pv = j > 0 ? sv[j - 1] : v;
+    const int pi = j > 0 ? si[j - 1] : id;
+    sv[j] = gt[j] ? (prev ? pv : v) : sv[j];
+    si[j] = gt[j] ? (prev ? pi : id) : si[j];
   }
 }
 
 template <int K>
-__device__ __forceinline__ void topk_insert_ordered(float (&sv)[K], int (&si)[K], float v, int id) {
-  bool moved = false;
+__device__ __forceinline__ void topk_insert_strict(float (&sv)[K], int (&si)[K], float v, int id) {
+  bool gt[K];
 #pragma unroll
-  for (int j = 0; j < K; ++j) {
-    const bool gt = moved || v > sv[j] || (v == sv[j] && id < si[j]);
-    moved = gt;
-    const float tv = sv[j];
-    const int ti = si[j];
-    sv[j] = gt ? v : tv;
-    si[j] = gt ? id : ti;
-    v = gt ? tv : v;
-    id = gt ? ti : id;
-  }
+  for (int j = 0; j < K; ++j) gt[j] = v > sv[j];
+  topk_insert_at<K>(sv, si, v, id, gt);
+}
+
+template <int K>
+__device__ __forceinline__ void topk_insert_ordered(float (&sv)[K], int (&si)[K], float v, int id) {
+  bool gt[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) gt[j] = v > sv[j] || (v == sv[j] && id < si[j]);
+  topk_insert_at<K>(sv, si, v, id, gt);
 }
 
 // ids ascending, carrying their weights (odd-even transposition sort, K passes, branch-free)
@@ -264,19 +263,20 @@ __device__ __forceinline__ void topk_softmax_wave(const float* __restrict__ lrow
   topk_softmax_wave_vals<K>(v, E, lane, ids_out, w_out);
 }
 
-// The same top-k + softmax with four lanes per token (lanes 4t .. 4t+3, `sub` = lane % 4): each
-// lane keeps the sorted top K of its quarter of the logits (ascending ids, strict > insertion), then
-// two xor-shuffle rounds merge the lists under (value desc, id asc), so all four lanes hold the
-// same sorted selection as topk_softmax_lane and compute the identical softmax; sub 0 writes.
-// lrow must be 16-byte aligned and the quarter Q = E/4 a multiple of 4 (E % 16 == 0).
-template <int K>
-__device__ __forceinline__ void topk_softmax_quad(const float* __restrict__ lrow, int E, int sub,
-                                                  int32_t* ids_out, float* w_out) {
+// The same top-k + softmax with LANES lanes per token (lanes LANES*t .. LANES*t + LANES-1, `sub` =
+// lane % LANES): each lane keeps the sorted top K of its 1/LANES of the logits (ascending ids,
+// strict > insertion), then log2(LANES) xor-shuffle rounds merge the lists under (value desc, id
+// asc), so all lanes of the group hold the same sorted selection as topk_softmax_lane and compute
+// the identical softmax; sub 0 writes.  lrow must be 16-byte aligned and the share Q = E/LANES a
+// multiple of 4 (E % (4*LANES) == 0).
+template <int K, int LANES>
+__device__ __forceinline__ void topk_softmax_group(const float* __restrict__ lrow, int E, int sub,
+                                                   int32_t* ids_out, float* w_out) {
   float sv[K];
   int si[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) { sv[j] = -INFINITY; si[j] = 0x7fffffff; }
-  const int Q = E / 4;
+  const int Q = E / LANES;
   for (int e0 = sub * Q; e0 < (sub + 1) * Q; e0 += 4) {
     const float4 q = *reinterpret_cast<const float4*>(lrow + e0);
     const float vv[4] = {q.x, q.y, q.z, q.w};
@@ -284,7 +284,7 @@ __device__ __forceinline__ void topk_softmax_quad(const float* __restrict__ lrow
     for (int i = 0; i < 4; ++i) topk_insert_strict<K>(sv, si, vv[i], e0 + i);
   }
 #pragma unroll
-  for (int o = 1; o <= 2; o <<= 1) {
+  for (int o = 1; o < LANES; o <<= 1) {
     float pv[K];
     int pi[K];
 #pragma unroll

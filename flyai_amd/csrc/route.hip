@@ -416,7 +416,7 @@ __global__ __launch_bounds__(kPermWaves * 64) void moe_topk_permute_kernel(
     for (int t0 = 0; t0 < T; t0 += kPermWaves * 16) {
       const int t = t0 + (threadIdx.x >> 2);
       // whole quads stay together (T rounds the quad index, never splits one)
-      if (t < T) topk_softmax_quad<K>(lg_s + t * (E + 4), E, sub, ids_s + t * K, topk_w + (size_t)t * K);
+      if (t < T) topk_softmax_group<K, 4>(lg_s + t * (E + 4), E, sub, ids_s + t * K, topk_w + (size_t)t * K);
     }
   } else {
     for (int t = threadIdx.x; t < T; t += kPermWaves * 64)

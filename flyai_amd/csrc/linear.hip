@@ -1,4 +1,6 @@
 // Layer glue: RMSNorm, bf16 projections with bias (+ residual), RoPE + KV append.
+#include <type_traits>
+
 #include "common.h"
 
 namespace flyai {
@@ -207,6 +209,44 @@ __device__ __forceinline__ float sum_slices(const float* __restrict__ part, int 
   return s;
 }
 
+// The thread's ITERS columns (tid + kRowThreads * it) of token row t: the split-K slices summed in
+// slice order, + bias, rounded, + the residual, rounded (the sum_slices order).  Every load of the
+// first SMAX slices, the bias, the residual and the norm weight is issued before the first add, so
+// the row costs one memory round trip instead of one per column; slices past SMAX, if any, are
+// added afterwards in order.  Columns past H are clamped for the loads and left out of ss.
+template <int ITERS, int SMAX>
+__device__ __forceinline__ void row_residual(const float* __restrict__ part, int slices, size_t stride,
+                                             const uint16_t* __restrict__ b, const uint16_t* __restrict__ h_in,
+                                             const float* __restrict__ lnw, int t, int H,
+                                             uint16_t (&hv)[ITERS], float (&lw)[ITERS], float& ss) {
+  const int tid = threadIdx.x;
+  float pv[ITERS][SMAX], bv[ITERS], hp[ITERS];
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int i = min(tid + it * kRowThreads, H - 1);
+    const size_t idx = (size_t)t * H + i;
+#pragma unroll
+    for (int q = 0; q < SMAX; ++q) pv[it][q] = part[(size_t)min(q, slices - 1) * stride + idx];
+    bv[it] = b ? bf2f(b[i]) : 0.f;
+    hp[it] = bf2f(h_in[idx]);
+    lw[it] = lnw[i];
+  }
+  ss = 0.f;
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int i = tid + it * kRowThreads;
+    const size_t idx = (size_t)t * H + min(i, H - 1);
+    float o = pv[it][0];
+#pragma unroll
+    for (int q = 1; q < SMAX; ++q)
+      if (q < slices) o += pv[it][q];
+    for (int q = SMAX; q < slices; ++q) o += part[(size_t)q * stride + idx];
+    hv[it] = f2bf(hp[it] + bf16_round(o + bv[it]));
+    const float hf = bf2f(hv[it]);
+    if (i < H) ss = fmaf(hf, hf, ss);
+  }
+}
+
 // y = bf16(sum + b); with residual: residual <- bf16(residual + y)
 __global__ __launch_bounds__(256) void linear_finalize_kernel(const float* __restrict__ part, int slices,
                                                               const uint16_t* __restrict__ b, int M,
@@ -222,25 +262,25 @@ __global__ __launch_bounds__(256) void linear_finalize_kernel(const float* __res
 
 // o_proj epilogue fused with the post-attention RMSNorm: h <- bf16(h + bf16(sum + b)),
 // xn = bf16(w * (h * rsqrt(mean(h^2) + eps))).  One workgroup per token row.
+template <int ITERS, int SMAX>
 __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_finalize_kernel(
     const float* __restrict__ part, int slices, const uint16_t* __restrict__ b, int M, int H,
     uint16_t* __restrict__ h, const float* __restrict__ lnw, float eps, uint16_t* __restrict__ xn) {
   __shared__ float red[kRowThreads / 64];
   const int t = blockIdx.x, tid = threadIdx.x;
-  const size_t stride = (size_t)M * H;
-  float ss = 0.f;
-  for (int i = tid; i < H; i += kRowThreads) {
-    const size_t idx = (size_t)t * H + i;
-    const float o = bf16_round(sum_slices(part, slices, stride, idx) + (b ? bf2f(b[i]) : 0.f));
-    const uint16_t hv = f2bf(bf2f(h[idx]) + o);
-    h[idx] = hv;
-    const float hf = bf2f(hv);
-    ss = fmaf(hf, hf, ss);
+  uint16_t hv[ITERS];
+  float lw[ITERS], ss;
+  row_residual<ITERS, SMAX>(part, slices, (size_t)M * H, b, h, lnw, t, H, hv, lw, ss);
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int i = tid + it * kRowThreads;
+    if (i < H) h[(size_t)t * H + i] = hv[it];
   }
   const float rr = rsqrtf(block_sum_1024(ss, red) / (float)H + eps);
-  for (int i = tid; i < H; i += kRowThreads) {
-    const size_t idx = (size_t)t * H + i;
-    xn[idx] = f2bf(lnw[i] * (bf2f(h[idx]) * rr));
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int i = tid + it * kRowThreads;
+    if (i < H) xn[(size_t)t * H + i] = f2bf(lw[it] * (bf2f(hv[it]) * rr));
   }
 }
 
@@ -253,7 +293,7 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_finalize_kernel(
 // kernel never exchange data (a device-scope fence would write back the L2).
 constexpr int kRouteSplit = 4;
 
-template <int JMAX>
+template <int JMAX, int SMAX>
 __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_logits_kernel(
     const float* __restrict__ part, int slices, const uint16_t* __restrict__ b, int M, int H,
     const uint16_t* __restrict__ h_in, uint16_t* __restrict__ h_out, const float* __restrict__ lnw,
@@ -279,22 +319,24 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_logits_kernel(
       }
   };
   load_batch(e_lo + wave * kBatch);
-  const size_t stride = (size_t)M * H;
-  float ss = 0.f;
-  for (int i = tid; i < H; i += kRowThreads) {
-    const size_t idx = (size_t)t * H + i;
-    const float o = bf16_round(sum_slices(part, slices, stride, idx) + (b ? bf2f(b[i]) : 0.f));
-    const uint16_t hv = f2bf(bf2f(h_in[idx]) + o);
-    xs[i] = hv;  // the new residual, normalised in place below
-    if (split == 0) h_out[idx] = hv;
-    const float hf = bf2f(hv);
-    ss = fmaf(hf, hf, ss);
+  constexpr int kIters = (JMAX * 512 + kRowThreads - 1) / kRowThreads;  // columns per thread
+  uint16_t hv[kIters];
+  float lw[kIters], ss;
+  row_residual<kIters, SMAX>(part, slices, (size_t)M * H, b, h_in, lnw, t, H, hv, lw, ss);
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    const int i = tid + it * kRowThreads;
+    if (i < H && split == 0) h_out[(size_t)t * H + i] = hv[it];
   }
   const float rr = rsqrtf(block_sum_1024(ss, red) / (float)H + eps);
-  for (int i = tid; i < H; i += kRowThreads) {
-    const uint16_t v = f2bf(lnw[i] * (bf2f(xs[i]) * rr));
-    if (split == 0) xn[(size_t)t * H + i] = v;
-    xs[i] = v;
+#pragma unroll
+  for (int it = 0; it < kIters; ++it) {
+    const int i = tid + it * kRowThreads;
+    if (i < H) {
+      const uint16_t v = f2bf(lw[it] * (bf2f(hv[it]) * rr));
+      if (split == 0) xn[(size_t)t * H + i] = v;
+      xs[i] = v;
+    }
   }
   __syncthreads();
   for (int e0 = e_lo + wave * kBatch; e0 < e_hi; e0 += (kRowThreads / 64) * kBatch) {
@@ -476,8 +518,20 @@ int launch_linear_residual_rmsnorm(const uint16_t* x, const uint16_t* W, const u
   int slices = 0;
   int rc = launch_gemm(x, W, M, N, K, part, &slices, s);
   if (rc) return rc;
-  hipLaunchKernelGGL(residual_rmsnorm_finalize_kernel, dim3(M), dim3(kRowThreads), 0, s, part, slices,
-                     b, M, N, h, lnw, eps, xn);
+  if (N > 7 * kRowThreads) return set_error(FLYAI_EINVAL, "residual_rmsnorm: H <= %d", 7 * kRowThreads);
+  auto go = [&](auto iters, auto smax) {
+    hipLaunchKernelGGL((residual_rmsnorm_finalize_kernel<decltype(iters)::value, decltype(smax)::value>), dim3(M),
+                       dim3(kRowThreads), 0, s, part, slices, b, M, N, h, lnw, eps, xn);
+  };
+  using I3 = std::integral_constant<int, 3>;
+  using I7 = std::integral_constant<int, 7>;
+  using S1 = std::integral_constant<int, 1>;
+  using S8 = std::integral_constant<int, 8>;
+  if (N <= 3 * kRowThreads) {
+    if (slices == 1) go(I3{}, S1{}); else go(I3{}, S8{});
+  } else {
+    if (slices == 1) go(I7{}, S1{}); else go(I7{}, S8{});
+  }
   return check_launch("residual_rmsnorm_finalize");
 }
 
@@ -497,12 +551,21 @@ int launch_linear_residual_rmsnorm_logits(const uint16_t* x, const uint16_t* W, 
   int slices = 0;
   int rc = launch_gemm(x, W, M, N, K, part, &slices, s);
   if (rc) return rc;
-  if (N <= 3072)
-    hipLaunchKernelGGL((residual_rmsnorm_logits_kernel<6>), dim3(M, kRouteSplit), dim3(kRowThreads), 0, s,
-                       part, slices, b, M, N, h_in, h_out, lnw, eps, xn, rw, rb, E, logits);
-  else
-    hipLaunchKernelGGL((residual_rmsnorm_logits_kernel<14>), dim3(M, kRouteSplit), dim3(kRowThreads), 0, s,
-                       part, slices, b, M, N, h_in, h_out, lnw, eps, xn, rw, rb, E, logits);
+  auto go = [&](auto jmax, auto smax) {
+    hipLaunchKernelGGL((residual_rmsnorm_logits_kernel<decltype(jmax)::value, decltype(smax)::value>),
+                       dim3(M, kRouteSplit), dim3(kRowThreads), 0, s, part, slices, b, M, N, h_in, h_out, lnw,
+                       eps, xn, rw, rb, E, logits);
+  };
+  using J6 = std::integral_constant<int, 6>;
+  using J14 = std::integral_constant<int, 14>;
+  using S1 = std::integral_constant<int, 1>;
+  using S8 = std::integral_constant<int, 8>;
+  using S4 = std::integral_constant<int, 4>;
+  if (N <= 3072) {
+    if (slices == 1) go(J6{}, S1{}); else go(J6{}, S8{});
+  } else {  // 7 columns per thread: 4 slices in registers keep it out of scratch
+    if (slices == 1) go(J14{}, S1{}); else go(J14{}, S4{});
+  }
   return check_launch("residual_rmsnorm_logits");
 }
 

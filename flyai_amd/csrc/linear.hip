@@ -560,11 +560,10 @@ int launch_linear_residual_rmsnorm_logits(const uint16_t* x, const uint16_t* W, 
   using J14 = std::integral_constant<int, 14>;
   using S1 = std::integral_constant<int, 1>;
   using S8 = std::integral_constant<int, 8>;
-  using S4 = std::integral_constant<int, 4>;
   if (N <= 3072) {
     if (slices == 1) go(J6{}, S1{}); else go(J6{}, S8{});
-  } else {  // 7 columns per thread: 4 slices in registers keep it out of scratch
-    if (slices == 1) go(J14{}, S1{}); else go(J14{}, S4{});
+  } else {  // 7 columns per thread and 14 router chunks: more slices in registers would spill
+    go(J14{}, S1{});
   }
   return check_launch("residual_rmsnorm_logits");
 }

@@ -440,6 +440,8 @@ int launch_attn_prefill(const uint16_t* q, const uint16_t* k_pool, const uint16_
 // Merge: per query row, in base-2 units (s' = s log2(e), sink' = sink log2(e)): M = max(sink',
 // max_s m_s), L = 2^(sink'-M) + sum_s l_s 2^(m_s-M), out = bf16(sum_s O_s 2^(m_s-M) / L) -- the
 // softmax with the sink column, e^(s - m) = 2^(s' - m').  Thread (row = tid/8, part = tid%8) writes 8 dims.
+constexpr int kMergeM = 16, kMergeChunk = 4;
+
 __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict__ partials,
                                                          const flyai_attn_group* __restrict__ groups,
                                                          const float* __restrict__ sinks, int Hq,
@@ -452,17 +454,42 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
   if (ti >= gr.ntok) return;
   const int h = gr.kv_head * 8 + (rq & 7);
   const float sink = sinks[h] * kLog2e;  // the partial maxima are in base-2 units
+  const int n = gr.n_splits;
+  auto rec_of = [&](int s) {
+    return partials + ((size_t)(gr.first_item + min(s, n - 1)) * kAttnRows + rq) * kPartFloats;
+  };
+  // The split maxima are read kMergeM at a time and the split records kMergeChunk at a time, every
+  // load of a batch issued before its first use (a round trip per batch, not per split); indices past
+  // the last split are clamped for the loads and left out.  The sums run in split order as before.
   float M = sink;
-  for (int s = 0; s < gr.n_splits; ++s)
-    M = fmaxf(M, partials[((size_t)(gr.first_item + s) * kAttnRows + rq) * kPartFloats]);
+  for (int s0 = 0; s0 < n; s0 += kMergeM) {
+    float mv[kMergeM];
+#pragma unroll
+    for (int j = 0; j < kMergeM; ++j) mv[j] = rec_of(s0 + j)[0];
+#pragma unroll
+    for (int j = 0; j < kMergeM; ++j)
+      if (s0 + j < n) M = fmaxf(M, mv[j]);
+  }
   float L = exp2f(sink - M);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s = 0; s < gr.n_splits; ++s) {
-    const float* rec = partials + ((size_t)(gr.first_item + s) * kAttnRows + rq) * kPartFloats;
-    const float wgt = exp2f(rec[0] - M);
-    L += rec[1] * wgt;
+  for (int s0 = 0; s0 < n; s0 += kMergeChunk) {
+    float rm[kMergeChunk], rl[kMergeChunk], rd[kMergeChunk][8];
 #pragma unroll
-    for (int d = 0; d < 8; ++d) acc[d] += rec[2 + part * 8 + d] * wgt;
+    for (int j = 0; j < kMergeChunk; ++j) {
+      const float* rec = rec_of(s0 + j);
+      rm[j] = rec[0];
+      rl[j] = rec[1];
+#pragma unroll
+      for (int d = 0; d < 8; ++d) rd[j][d] = rec[2 + part * 8 + d];
+    }
+#pragma unroll
+    for (int j = 0; j < kMergeChunk; ++j)
+      if (s0 + j < n) {
+        const float wgt = exp2f(rm[j] - M);
+        L += rl[j] * wgt;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) acc[d] += rd[j][d] * wgt;
+      }
   }
   const float inv = 1.0f / L;
   uint16_t* o = out + ((size_t)(gr.tok + ti) * Hq + h) * 64 + part * 8;

@@ -641,42 +641,64 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_vec_kernel(
   const int D2 = D / 2, Q2 = D2 / 4, QV = D / 4;
   const int rot_units = (Hq + Hkv) * Q2;
   if (u >= rot_units + Hkv * QV) return;
+  // Every load that depends only on (t, u) -- the token's indices, the unit's split-K partials and
+  // bias -- goes out before the first use, and the rotary table and the sequence's KV geometry in
+  // the next batch: two memory round trips in all.  Slices past `slices` are clamped for the load and
+  // never added; the sums run in slice order as in sum_slices.
   const int pos = positions[t];
-  if (pos < 0 || pos >= rope_positions) return;  // outside the rotary table: no read, no write
   const int b = seq_id[t];
-  const int cap = kv_cap[b];
-  // the K/V slot: the position itself, or the tree node's slot in tree verify
-  const int slot = kv_pos ? kv_pos[t] : pos;
-  const bool in_cap = slot >= 0 && slot < cap;
-  const int64_t base = kv_base[b];
+  const int slot_in = kv_pos ? kv_pos[t] : 0;
+  const bool rot = u < rot_units;
+  const int h = u / Q2, d0r = (u % Q2) * 4;                       // rotary unit
+  const int gv = (u - rot_units) / QV, d0v = ((u - rot_units) % QV) * 4;  // V unit
+  const int f1 = rot ? h * D + d0r : (Hq + Hkv) * D + gv * D + d0v;
+  const int f2 = rot ? f1 + D2 : f1;
   const int width = (Hq + 2 * Hkv) * D;
   const size_t stride = (size_t)M * width;
   const float* row = part + (size_t)t * width;
-  auto sum4 = [&](int f, float (&o)[4]) __attribute__((always_inline)) {
-    float4 v[NS];
+  float4 p1[NS], p2[NS];
 #pragma unroll
-    for (int i = 0; i < NS; ++i)
-      v[i] = i < slices ? *reinterpret_cast<const float4*>(row + i * stride + f) : make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 a = v[0];
+  for (int i = 0; i < NS; ++i) {
+    const size_t off = (size_t)min(i, slices - 1) * stride;
+    p1[i] = *reinterpret_cast<const float4*>(row + off + f1);
+    p2[i] = *reinterpret_cast<const float4*>(row + off + f2);
+  }
+  float b1[4], b2[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    b1[j] = bias ? bf2f(bias[f1 + j]) : 0.f;
+    b2[j] = bias ? bf2f(bias[f2 + j]) : 0.f;
+  }
+  if (pos < 0 || pos >= rope_positions) return;  // outside the rotary table: no read, no write
+  const int cap = kv_cap[b];
+  const int64_t base = kv_base[b];
+  // the K/V slot: the position itself, or the tree node's slot in tree verify
+  const int slot = kv_pos ? slot_in : pos;
+  const bool in_cap = slot >= 0 && slot < cap;
+  auto sum4 = [&](const float4 (&pv)[NS], const float (&bv)[4], float (&o)[4]) __attribute__((always_inline)) {
+    float4 a = pv[0];
 #pragma unroll
     for (int i = 1; i < NS; ++i)
-      if (i < slices) { a.x += v[i].x; a.y += v[i].y; a.z += v[i].z; a.w += v[i].w; }
+      if (i < slices) { a.x += pv[i].x; a.y += pv[i].y; a.z += pv[i].z; a.w += pv[i].w; }
     const float av[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] = bf16_round(av[j] + (bias ? bf2f(bias[f + j]) : 0.f));
+    for (int j = 0; j < 4; ++j) o[j] = bf16_round(av[j] + bv[j]);
   };
-  if (u < rot_units) {
-    const int h = u / Q2, d0 = (u % Q2) * 4;
+  if (rot) {
+    const int d0 = d0r;
     if (h >= Hq && !in_cap) return;
-    float x1[4], x2[4];
-    sum4(h * D + d0, x1);
-    sum4(h * D + d0 + D2, x2);
     const uint16_t* cr = cos_tab + (size_t)pos * D2 + d0;
     const uint16_t* sr = sin_tab + (size_t)pos * D2 + d0;
+    float cv[4], sv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { cv[j] = bf2f(cr[j]); sv[j] = bf2f(sr[j]); }
+    float x1[4], x2[4];
+    sum4(p1, b1, x1);
+    sum4(p2, b2, x2);
     uint16_t first[4], second[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const float c = bf2f(cr[j]), sn = bf2f(sr[j]);
+      const float c = cv[j], sn = sv[j];
       first[j] = f2bf(bf16_round(bf16_round(x1[j] * c) - bf16_round(x2[j] * sn)));
       second[j] = f2bf(bf16_round(bf16_round(x2[j] * c) + bf16_round(x1[j] * sn)));
     }
@@ -689,11 +711,10 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_vec_kernel(
     *reinterpret_cast<uint2*>(d2) = make_uint2(second[0] | ((uint32_t)second[1] << 16),
                                                second[2] | ((uint32_t)second[3] << 16));
   } else if (in_cap) {
-    const int v = u - rot_units, gv = v / QV, d0 = (v % QV) * 4;
     float o[4];
-    sum4((Hq + Hkv) * D + gv * D + d0, o);
+    sum4(p1, b1, o);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) v_pool[base + (size_t)gv * cap * D + kv_v_off(slot, d0 + j)] = f2bf(o[j]);
+    for (int j = 0; j < 4; ++j) v_pool[base + (size_t)gv * cap * D + kv_v_off(slot, d0v + j)] = f2bf(o[j]);
   }
 }
 

@@ -744,14 +744,17 @@ int launch_qkv_rope_kv(const uint16_t* x, const uint16_t* Wqkv, const uint16_t* 
   if (D % 8 == 0 && slices <= 16) {
     const int units = (Hq + Hkv) * (D / 8) + Hkv * (D / 4);
     const dim3 grid(T, ceil_div(units, 256));
-    if (slices <= 8)
-      hipLaunchKernelGGL(qkv_rope_kv_vec_kernel<8>, grid, dim3(256), 0, s, part, slices, T, bqkv, positions,
-                         seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base, kv_cap, q_out,
-                         k_pool, v_pool, kv_pos);
-    else
-      hipLaunchKernelGGL(qkv_rope_kv_vec_kernel<16>, grid, dim3(256), 0, s, part, slices, T, bqkv, positions,
-                         seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base, kv_cap, q_out,
-                         k_pool, v_pool, kv_pos);
+    // the slice count the kernel loads unconditionally: exact for the tiled GEMM's one plane and for
+    // K = 2880 (6 planes), rounded up otherwise (clamped loads past `slices` are never added)
+    auto go = [&](auto ns) {
+      hipLaunchKernelGGL((qkv_rope_kv_vec_kernel<decltype(ns)::value>), grid, dim3(256), 0, s, part, slices, T,
+                         bqkv, positions, seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base, kv_cap,
+                         q_out, k_pool, v_pool, kv_pos);
+    };
+    if (slices == 1) go(std::integral_constant<int, 1>{});
+    else if (slices <= 6) go(std::integral_constant<int, 6>{});
+    else if (slices <= 8) go(std::integral_constant<int, 8>{});
+    else go(std::integral_constant<int, 16>{});
   } else {
     hipLaunchKernelGGL(rope_kv_append_kernel<true>, dim3(T, 4), dim3(256), 0, s, nullptr, part, slices, T,
                        bqkv, positions, seq_id, cos_tab, sin_tab, rope_positions, Hq, Hkv, D, kv_base,

@@ -116,7 +116,10 @@ def _layer_indices(reader):
     idx = set()
     for name in reader.keys():
         if name.startswith("model.layers."):
-            idx.add(int(name.split(".")[2]))
+            part = name.split(".")[2]
+            if not part.isdigit():
+                raise MXFP4LayoutError(f"unexpected decoder-layer tensor name {name}")
+            idx.add(int(part))
     return idx
 
 

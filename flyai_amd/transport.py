@@ -312,7 +312,9 @@ def _sendall(sock, parts):
 # ---- pinned staging for device tensors -------------------------------------------------------------
 
 class _PinnedRing:
-    """RING_SLOTS pinned host chunks and the copy stream their device copies run on, per device."""
+    """RING_SLOTS pinned host chunks and the copy stream their device copies run on, one per device
+    and direction.  A transfer holds its ring for its whole frame, so concurrent sends (or
+    receives) of one process on one device take turns."""
 
     def __init__(self, device, chunk_bytes=CHUNK_BYTES, slots=RING_SLOTS):
         self.device = torch.device(device)

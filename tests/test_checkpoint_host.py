@@ -96,6 +96,13 @@ def test_layer_count_and_missing_layers(tmp_path):
         _inspect(tmp_path, missing)
 
 
+def test_malformed_layer_name_fails_closed(tmp_path):
+    t = _tensors(tiny_config())
+    t["model.layers.x.mlp.router.weight"] = torch.zeros(2, 32, dtype=torch.bfloat16)
+    with pytest.raises(MXFP4LayoutError, match="layer tensor name"):
+        _inspect(tmp_path, t)
+
+
 def test_missing_packed_experts(tmp_path):
     t = {n: x for n, x in _tensors(tiny_config()).items() if not n.startswith("model.layers.0.mlp.experts.")}
     with pytest.raises(MXFP4LayoutError, match="missing packed"):

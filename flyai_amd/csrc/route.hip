@@ -31,21 +31,22 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
     }
   const int vecs = H / 8;
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-  for (int b0 = 0; b0 < TT * vecs; b0 += 4 * 256) {  // loads batched 4 per thread
-    u32x4 v4[4];
+  // every staging load of the thread goes out (with the weights above) before the first LDS store:
+  // one memory round trip for the whole workgroup (H <= JMAX * 512 bounds the count)
+  constexpr int kPer = (TT * JMAX * 64 + 255) / 256;
+  u32x4 v4[kPer];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = b0 + j * 256 + tid;
-      const int t = i / vecs, v = i % vecs;
-      const bool ok = i < TT * vecs && t < nt;
-      const u32x4 val = reinterpret_cast<const u32x4*>(x + (ok ? (size_t)(t0 + t) * H : 0))[ok ? v : 0];
-      v4[j] = ok ? val : u32x4{0u, 0u, 0u, 0u};
-    }
+  for (int j = 0; j < kPer; ++j) {
+    const int i = j * 256 + tid;
+    const int t = i / vecs, v = i % vecs;
+    const bool ok = i < TT * vecs && t < nt;
+    const u32x4 val = reinterpret_cast<const u32x4*>(x + (ok ? (size_t)(t0 + t) * H : 0))[ok ? v : 0];
+    v4[j] = ok ? val : u32x4{0u, 0u, 0u, 0u};
+  }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = b0 + j * 256 + tid;
-      if (i < TT * vecs) reinterpret_cast<u32x4*>(xs + (i / vecs) * H)[i % vecs] = v4[j];
-    }
+  for (int j = 0; j < kPer; ++j) {
+    const int i = j * 256 + tid;
+    if (i < TT * vecs) reinterpret_cast<u32x4*>(xs + (i / vecs) * H)[i % vecs] = v4[j];
   }
   __syncthreads();
   float acc[EPW][TT];

@@ -312,6 +312,32 @@ def test_attention_vs_oracle(window, q_lens, starts):
 
 
 @pytest.mark.parametrize("window", [0, 128])
+def test_attention_many_splits_vs_oracle(window):
+    """128-key splits: up to 32 splits per (token, head), so the merge reads its split maxima and
+    records over several batches, including a partial last batch."""
+    from flyai_amd import ops
+    Hq, Hkv, D, cap = 64, 8, 64, 4160
+    q_lens, starts = [1, 4, 2], [4093, 2301, 17]
+    S, T = len(q_lens), sum(q_lens)
+    slab = Hkv * cap * D
+    kp = torch.randn(S * slab, device=DEV, generator=_gen(60)).to(torch.bfloat16)
+    vp = torch.randn(S * slab, device=DEV, generator=_gen(61)).to(torch.bfloat16)
+    q = torch.randn(T, Hq, D, device=DEV, generator=_gen(62)).to(torch.bfloat16)
+    sinks = torch.randn(Hq, device=DEV, generator=_gen(63)).to(torch.bfloat16).float()
+    base = torch.tensor([b * slab for b in range(S)], dtype=torch.int64, device=DEV)
+    capt = torch.tensor([cap] * S, dtype=torch.int32, device=DEV)
+    items, groups, n_small = ops.attn_plan(q_lens, starts, Hkv, window, 128)
+    if window == 0:
+        assert max(int(g[1]) for g in groups.cpu().view(-1, 8).tolist()) >= 32
+    out = ops.attn_ragged(q, kp, vp, base, capt, sinks, window, items, groups, n_small, Hkv)
+    ks = [kvlayout.gather(kp[b * slab:(b + 1) * slab], Hkv, cap, "k").float().cpu() for b in range(S)]
+    vs = [kvlayout.gather(vp[b * slab:(b + 1) * slab], Hkv, cap, "v").float().cpu() for b in range(S)]
+    ref = oattn.ragged_attention(q.float().cpu(), ks, vs, q_lens, starts, sinks.cpu(), window)
+    mar, cos = _metrics(out.float().cpu().numpy(), ref.numpy())
+    assert mar <= MAR and cos >= COS, f"attention: {mar:.3g} {cos:.6f}"
+
+
+@pytest.mark.parametrize("window", [0, 128])
 def test_attention_prefill_items_vs_oracle(window):
     """Chunked-prefill rows (q_len >= 32) on the prefill kernel, mixed with decode and verify rows on
     the split kernel, into one output; against the oracle.  The unwritten slots past each sequence
@@ -388,6 +414,31 @@ def test_stage_step_per_layer_vs_oracle():
     for l, (o, r) in enumerate(zip(outs, refs)):
         mar, cos = _metrics(o, r)
         assert mar <= MAR and cos >= COS, f"layer {l}: max-abs-rel {mar:.3g} cos {cos:.6f}"
+
+
+def test_stage_step_hidden_3584_per_layer_vs_oracle():
+    """Hidden 3584 (> 3072): the router-logits finalizer's wide variant, which keeps one split-K
+    slice in registers and adds the other 7 of the 4096-wide o-proj in its tail loop."""
+    from gpu_harness import oracle_layer_params, oracle_kv, fill_kv_random, metrics
+    from flyai_amd.rope import YarnRotary
+    from flyai_amd.runtime import KVWorkspace, RaggedStage
+    from flyai_amd.weights import GptOssShape, synthetic_layer
+    shape = GptOssShape(hidden=3584, n_experts=8)
+    lw = synthetic_layer(shape, 77, DEV, sliding=False, keep_hf=True)
+    rot = YarnRotary(2048, device=DEV)
+    q_lens, starts = [1, 4, 1], [300, 17, 1500]
+    kv = KVWorkspace(1, 3, 2048, shape.n_kv_heads, shape.head_dim, DEV)
+    fill_kv_random(kv, 78)
+    T = sum(q_lens)
+    h = torch.randn(T, shape.hidden, device=DEV, generator=_gen(79)).to(torch.bfloat16)
+    okv = oracle_kv(kv, 0, [0, 1, 2])
+    st = RaggedStage(shape, [lw], rot, kv, max_tokens=64, max_seqs=3)
+    out = st.forward(h.clone(), q_lens, starts, [0, 1, 2])
+    torch.cuda.synchronize()
+    cos, sin = olayer.rope_table(2048)
+    ref = olayer.decoder_layer(h.float().cpu(), oracle_layer_params(lw, False), okv, q_lens, starts, cos, sin)
+    mar, cs = metrics(out.float().cpu().numpy(), ref.numpy())
+    assert mar <= MAR and cs >= COS, f"hidden 3584 layer: {mar:.3g} {cs:.6f}"
 
 
 def test_c0_moe_block_vs_oracle():

@@ -2,6 +2,8 @@
 // Index outputs are bit-exact against the oracle: the logits use one fixed fp32 summation order
 // (64 lane partials over k = lane + 64 j, then a xor butterfly 32,16,8,4,2,1) and ties in top-k
 // go to the lower expert id.
+#include <type_traits>
+
 #include "common.h"
 
 namespace flyai {
@@ -491,9 +493,10 @@ int launch_permute(const int32_t* ids, int T, int k, int E, int32_t* hist, int32
 constexpr int kCombineThreads = 1024;
 constexpr int kCombinePer = 2;  // H <= 4 * 1024 * 2
 
+template <int K>
 __global__ __launch_bounds__(kCombineThreads) void moe_combine_kernel(
     const float* __restrict__ y_perm, const int32_t* __restrict__ inv,
-    const float* __restrict__ topk_w, int k, int H, const uint16_t* residual, uint16_t* out,
+    const float* __restrict__ topk_w, int H, const uint16_t* residual, uint16_t* out,
     const float* __restrict__ lnw, float eps, uint16_t* __restrict__ xn) {
   __shared__ float red[kCombineThreads / 64];
   const int t = blockIdx.x, tid = threadIdx.x;
@@ -507,18 +510,24 @@ __global__ __launch_bounds__(kCombineThreads) void moe_combine_kernel(
     lw[c] = (lnw && i < H4) ? reinterpret_cast<const float4*>(lnw)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
     rsd[c] = (residual && i < H4) ? reinterpret_cast<const uint2*>(residual + (size_t)t * H)[i] : make_uint2(0, 0);
   }
-  int rows[8];
-  float wt[8];
-  for (int s = 0; s < k; ++s) { rows[s] = inv[t * k + s]; wt[s] = topk_w[t * k + s]; }
+  int rows[K];
+  float wt[K];
+#pragma unroll
+  for (int s = 0; s < K; ++s) { rows[s] = inv[t * K + s]; wt[s] = topk_w[t * K + s]; }
   float ss = 0.f;
   uint16_t ob[kCombinePer][4];
 #pragma unroll
   for (int c = 0; c < kCombinePer; ++c) {
     const int i = tid + c * kCombineThreads;
     if (i >= H4) continue;
+    // the K slot rows' loads all go out before the first add (one round trip); sums in slot order
+    float4 yv[K];
+#pragma unroll
+    for (int s = 0; s < K; ++s) yv[s] = reinterpret_cast<const float4*>(y_perm + (size_t)rows[s] * H)[i];
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < k; ++s) {
-      const float4 y = reinterpret_cast<const float4*>(y_perm + (size_t)rows[s] * H)[i];
+#pragma unroll
+    for (int s = 0; s < K; ++s) {
+      const float4 y = yv[s];
       acc.x = fmaf(wt[s], y.x, acc.x);
       acc.y = fmaf(wt[s], y.y, acc.y);
       acc.z = fmaf(wt[s], y.z, acc.z);
@@ -563,8 +572,21 @@ int launch_combine(const float* y_perm, const int32_t* inv, const float* w, int 
                    const uint16_t* residual, uint16_t* out, const float* lnw, float eps,
                    uint16_t* xn, hipStream_t s) {
   if (T == 0) return FLYAI_OK;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(kCombineThreads), 0, s, y_perm, inv, w, k, H, residual,
-                     out, lnw, eps, xn);
+  auto go = [&](auto kk) {
+    hipLaunchKernelGGL((moe_combine_kernel<decltype(kk)::value>), dim3(T), dim3(kCombineThreads), 0, s, y_perm, inv,
+                       w, H, residual, out, lnw, eps, xn);
+  };
+  switch (k) {
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 3: go(std::integral_constant<int, 3>{}); break;
+    case 4: go(std::integral_constant<int, 4>{}); break;
+    case 5: go(std::integral_constant<int, 5>{}); break;
+    case 6: go(std::integral_constant<int, 6>{}); break;
+    case 7: go(std::integral_constant<int, 7>{}); break;
+    case 8: go(std::integral_constant<int, 8>{}); break;
+    default: return set_error(FLYAI_EINVAL, "combine: top_k must be 1..8");
+  }
   return check_launch("moe_combine");
 }
 

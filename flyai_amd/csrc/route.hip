@@ -103,7 +103,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
 
 int launch_router_logits(const uint16_t* x, const uint16_t* w, const uint16_t* b, int T, int H,
                          int E, float* logits, hipStream_t s) {
-  if (H <= 3072) {  // 8 staged rows stay under 48 KiB of LDS; 6 chunks of 512
+  if (H <= 3072 && T >= 256) {  // prefill-sized: 16 experts per workgroup halve the x re-reads
+    hipLaunchKernelGGL((router_logits_kernel<8, 4, 6, true>), dim3(ceil_div(T, 8), ceil_div(E, 16)),
+                       dim3(256), 8 * H * sizeof(uint16_t), s, x, w, b, T, H, E, logits);
+  } else if (H <= 3072) {  // 8 staged rows stay under 48 KiB of LDS; 6 chunks of 512
     hipLaunchKernelGGL((router_logits_kernel<8, 2, 6, true>), dim3(ceil_div(T, 8), ceil_div(E, 8)),
                        dim3(256), 8 * H * sizeof(uint16_t), s, x, w, b, T, H, E, logits);
   } else {

@@ -41,7 +41,8 @@ class StageConfig(C.Structure):
 class LayerDesc(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in (
         "ln1", "ln2", "wqkv", "bqkv", "wo", "bo", "sinks", "router_w", "router_b", "w13_packed",
-        "b13", "w2_packed", "b2", "k_pool", "v_pool")] + [("sliding", C.c_int32), ("pad", C.c_int32)]
+        "b13", "w2_packed", "b2", "k_pool", "v_pool")] + [("sliding", C.c_int32), ("pad", C.c_int32),
+                                                          ("kv_pool_elems", C.c_int64)]
 
 
 P, I32, I64, F32, SZ = C.c_void_p, C.c_int32, C.c_int64, C.c_float, C.c_size_t

@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <new>
 #include <string>
 #include <vector>
@@ -118,6 +119,7 @@ struct flyai_stage {
   std::vector<Graph> graph_cache;
   uint64_t use_clock = 0;
   int graphs_captured = 0;
+  std::vector<int> slab_order;  // host scratch of the slab-overlap check (max_seqs entries)
 };
 static constexpr int kGraphCacheMax = 16;
 static constexpr int kPlanBucket = 64;  // attention plan capacities round up to this
@@ -197,6 +199,7 @@ extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** o
   if (!st->layers) { delete st; return set_error(FLYAI_EINVAL, "stage_create: out of host memory"); }
   memset(st->layers, 0, sizeof(flyai_layer_desc) * c.n_layers);
   try {
+    st->slab_order.resize(c.max_seqs);
     for (int i = 0; i < 2; ++i) {
       st->plan_items[i].resize(c.max_attn_items);
       st->plan_groups[i].resize(st->max_groups);
@@ -212,9 +215,16 @@ extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** o
   return FLYAI_OK;
 }
 
+// A captured graph keeps the workspace, weight, pool and rope pointers bound when it was captured:
+// every setter that rebinds one of them drops the cache, and the next step captures again.
+static void drop_graphs(flyai_stage* st) {
+  for (auto& g : st->graph_cache) hipGraphExecDestroy(g.exec);
+  st->graph_cache.clear();
+}
+
 extern "C" void flyai_stage_destroy(flyai_stage* st) {
   if (!st) return;
-  for (auto& g : st->graph_cache) hipGraphExecDestroy(g.exec);
+  drop_graphs(st);
   if (st->capture_stream) hipStreamDestroy(st->capture_stream);
   for (int i = 0; i < 2; ++i)
     if (st->staged[i]) hipEventDestroy(st->staged[i]);
@@ -228,12 +238,15 @@ extern "C" int flyai_stage_set_layer(flyai_stage* st, int32_t layer, const flyai
   FLYAI_REQUIRE(d->ln1 && d->ln2 && d->wqkv && d->wo && d->sinks && d->router_w && d->router_b &&
                     d->w13_packed && d->b13 && d->w2_packed && d->b2 && d->k_pool && d->v_pool,
                 "set_layer: null weight pointer");
+  FLYAI_REQUIRE(d->kv_pool_elems > 0, "set_layer: kv_pool_elems must be > 0");
+  drop_graphs(st);
   st->layers[layer] = *d;
   return FLYAI_OK;
 }
 
 extern "C" int flyai_stage_set_rope(flyai_stage* st, const uint16_t* cos_tab, const uint16_t* sin_tab) {
   FLYAI_REQUIRE(st && cos_tab && sin_tab, "set_rope: null pointer");
+  drop_graphs(st);
   st->cos_tab = cos_tab;
   st->sin_tab = sin_tab;
   return FLYAI_OK;
@@ -251,6 +264,7 @@ extern "C" int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t d
                 "set_workspace: need %zu device and %zu pinned host bytes", st->dev_bytes,
                 2 * st->host_half);
   FLYAI_REQUIRE(((uintptr_t)dev_ws & 255) == 0, "set_workspace: device workspace must be 256-byte aligned");
+  drop_graphs(st);
   st->dev = static_cast<char*>(dev_ws);
   st->host = static_cast<char*>(host_pinned);
   if (!st->events_ready) {
@@ -469,12 +483,38 @@ static int stage_blob(flyai_stage* st, StepPlan& sp, const int32_t* q_lens, cons
   return FLYAI_OK;
 }
 
+// Every sequence's slab [kv_base, kv_base + Hkv * kv_cap * D) must end inside the smallest bound pool,
+// and no two sequences' slabs may overlap: their K/V appends would race and each would read the other's
+// keys.  Host-side, before any launch (the reference raises ContextOverflow before any write,
+// phase0/fastverify.py:23-26).
+static int check_slabs(flyai_stage* st, const int64_t* kv_base, const int32_t* kv_cap, int S) {
+  const flyai_stage_config& c = st->cfg;
+  int64_t pool = INT64_MAX;
+  for (int l = 0; l < c.n_layers; ++l) pool = std::min(pool, st->layers[l].kv_pool_elems);
+  const int64_t per_pos = (int64_t)c.n_kv_heads * c.head_dim;
+  for (int b = 0; b < S; ++b) {
+    const int64_t end = kv_base[b] + (int64_t)kv_cap[b] * per_pos;
+    if (end > pool)
+      return set_error(FLYAI_ERANGE, "sequence %d: KV slab [%lld, %lld) ends past the pools (%lld elements)", b,
+                       (long long)kv_base[b], (long long)end, (long long)pool);
+  }
+  if (S < 2) return FLYAI_OK;
+  int* order = st->slab_order.data();
+  for (int b = 0; b < S; ++b) order[b] = b;
+  std::sort(order, order + S, [&](int a, int b) { return kv_base[a] < kv_base[b]; });
+  for (int i = 0; i + 1 < S; ++i) {
+    const int a = order[i], b = order[i + 1];
+    if (kv_base[a] + (int64_t)kv_cap[a] * per_pos > kv_base[b])
+      return set_error(FLYAI_EINVAL, "sequences %d and %d have overlapping KV slabs (bases %lld and %lld)", a, b,
+                       (long long)kv_base[a], (long long)kv_base[b]);
+  }
+  return FLYAI_OK;
+}
+
 extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const int32_t* starts,
                                    const int64_t* kv_base, const int32_t* kv_cap, int32_t S,
                                    uint16_t* hidden, flyai_stream_t stream) {
   FLYAI_REQUIRE(st && q_lens && starts && kv_base && kv_cap && hidden, "forward: null pointer");
-  FLYAI_REQUIRE(st->dev && st->host, "forward: workspace not set");
-  FLYAI_REQUIRE(st->cos_tab && st->sin_tab, "forward: rope tables not set");
   const flyai_stage_config& c = st->cfg;
   FLYAI_REQUIRE(S >= 1 && S <= c.max_seqs, "forward: n_seqs %d out of [1, %d]", S, c.max_seqs);
   int64_t T = 0;
@@ -496,6 +536,9 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
     return set_error(FLYAI_ERANGE, "batch has %lld tokens > max_tokens %d", (long long)T, c.max_tokens);
   for (int l = 0; l < c.n_layers; ++l)
     FLYAI_REQUIRE(st->layers[l].wqkv, "forward: layer %d not bound", l);
+  RUN(check_slabs(st, kv_base, kv_cap, S));
+  FLYAI_REQUIRE(st->dev && st->host, "forward: workspace not set");
+  FLYAI_REQUIRE(st->cos_tab && st->sin_tab, "forward: rope tables not set");
   hipStream_t s = as_stream(stream);
 
   StepPlan sp;
@@ -535,8 +578,6 @@ extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t 
                                         const int32_t* depth, int64_t kv_base, int32_t kv_cap,
                                         uint16_t* hidden, flyai_stream_t stream) {
   FLYAI_REQUIRE(st && parent && depth && hidden, "forward_tree: null pointer");
-  FLYAI_REQUIRE(st->dev && st->host, "forward_tree: workspace not set");
-  FLYAI_REQUIRE(st->cos_tab && st->sin_tab, "forward_tree: rope tables not set");
   const flyai_stage_config& c = st->cfg;
   FLYAI_REQUIRE(n >= 1 && n <= 64, "forward_tree: tree size %d outside [1, 64]", n);
   FLYAI_REQUIRE(n <= c.max_tokens, "forward_tree: %d nodes > max_tokens %d", n, c.max_tokens);
@@ -562,6 +603,9 @@ extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t 
                      c.rope_positions);
   for (int l = 0; l < c.n_layers; ++l)
     FLYAI_REQUIRE(st->layers[l].wqkv, "forward_tree: layer %d not bound", l);
+  RUN(check_slabs(st, &kv_base, &kv_cap, 1));
+  FLYAI_REQUIRE(st->dev && st->host, "forward_tree: workspace not set");
+  FLYAI_REQUIRE(st->cos_tab && st->sin_tab, "forward_tree: rope tables not set");
   flyai_attn_tree tree;
   memset(&tree, 0, sizeof(tree));
   tree.start = start;

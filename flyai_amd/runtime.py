@@ -100,28 +100,41 @@ class RaggedStage:
         handle = C.c_void_p()
         check(lib().flyai_stage_create(C.byref(cfg), C.byref(handle)))
         self._h = handle
-        self._keep = []
+        self.layers = list(layers)
         for i, lw in enumerate(layers):
-            d = _lib.LayerDesc(
-                ln1=lw.ln1.data_ptr(), ln2=lw.ln2.data_ptr(), wqkv=lw.wqkv.data_ptr(),
-                bqkv=lw.bqkv.data_ptr(), wo=lw.wo.data_ptr(), bo=lw.bo.data_ptr(),
-                sinks=lw.sinks.data_ptr(), router_w=lw.router_w.data_ptr(),
-                router_b=lw.router_b.data_ptr(), w13_packed=lw.w13_packed.data_ptr(),
-                b13=lw.b13.data_ptr(), w2_packed=lw.w2_packed.data_ptr(), b2=lw.b2.data_ptr(),
-                k_pool=kv.k[i].data_ptr(), v_pool=kv.v[i].data_ptr(), sliding=int(lw.sliding), pad=0)
-            check(lib().flyai_stage_set_layer(self._h, i, C.byref(d)))
+            self.set_layer(i, lw)
         check(lib().flyai_stage_set_rope(self._h, C.c_void_p(rotary.cos.data_ptr()),
                                          C.c_void_p(rotary.sin.data_ptr())))
-        dev_bytes = int(lib().flyai_stage_workspace_bytes(self._h))
         host_bytes = int(lib().flyai_stage_host_staging_bytes(self._h))
-        self.workspace = torch.empty(dev_bytes + 256, dtype=torch.uint8, device=self.device)
-        off = (-self.workspace.data_ptr()) % 256
-        self._ws_ptr = self.workspace.data_ptr() + off
         self.staging = torch.empty(host_bytes, dtype=torch.uint8, pin_memory=True)
-        check(lib().flyai_stage_set_workspace(self._h, C.c_void_p(self._ws_ptr), dev_bytes,
-                                              C.c_void_p(self.staging.data_ptr()), host_bytes))
+        self.set_workspace()
         self.use_graphs = False
         self.set_graphs(use_graphs)
+
+    def set_layer(self, i, lw):
+        """Bind layer i to the weights of ``lw`` and the workspace's layer-i KV pools.  Drops every
+        captured step graph (they hold the previous pointers)."""
+        kv = self.kv
+        d = _lib.LayerDesc(
+            ln1=lw.ln1.data_ptr(), ln2=lw.ln2.data_ptr(), wqkv=lw.wqkv.data_ptr(),
+            bqkv=lw.bqkv.data_ptr(), wo=lw.wo.data_ptr(), bo=lw.bo.data_ptr(),
+            sinks=lw.sinks.data_ptr(), router_w=lw.router_w.data_ptr(),
+            router_b=lw.router_b.data_ptr(), w13_packed=lw.w13_packed.data_ptr(),
+            b13=lw.b13.data_ptr(), w2_packed=lw.w2_packed.data_ptr(), b2=lw.b2.data_ptr(),
+            k_pool=kv.k[i].data_ptr(), v_pool=kv.v[i].data_ptr(), sliding=int(lw.sliding), pad=0,
+            kv_pool_elems=min(kv.k[i].numel(), kv.v[i].numel()))
+        check(lib().flyai_stage_set_layer(self._h, i, C.byref(d)))
+        self.layers[i] = lw
+
+    def set_workspace(self):
+        """Bind a freshly allocated device workspace (and the pinned staging).  Drops every captured
+        step graph."""
+        dev_bytes = int(lib().flyai_stage_workspace_bytes(self._h))
+        ws = torch.empty(dev_bytes + 256, dtype=torch.uint8, device=self.device)
+        ptr = ws.data_ptr() + (-ws.data_ptr()) % 256
+        check(lib().flyai_stage_set_workspace(self._h, C.c_void_p(ptr), dev_bytes,
+                                              C.c_void_p(self.staging.data_ptr()), self.staging.numel()))
+        self.workspace, self._ws_ptr = ws, ptr
 
     def set_graphs(self, enable):
         """Replay each step as a HIP graph, one per (tokens, sequences, attention-plan bucket), captured
@@ -156,6 +169,8 @@ class RaggedStage:
         for s in slots:
             if not 0 <= int(s) < self.kv.n_slots:
                 raise ValueError(f"slot {s} out of range")
+        if len(set(int(s) for s in slots)) != S:
+            raise ValueError("two sequences of one step share a KV slot (their K/V writes would race)")
         ql = np.ascontiguousarray(q_lens, dtype=np.int32)
         st = np.ascontiguousarray(starts, dtype=np.int32)
         base = np.ascontiguousarray([self.kv.base(int(s)) for s in slots], dtype=np.int64)

@@ -34,7 +34,7 @@ typedef void* flyai_stream_t;
                              phase0/fastverify.py:23-26), raised before any write */
 #define FLYAI_EHIP -3     /* a HIP runtime call failed */
 
-#define FLYAI_ABI_VERSION 1
+#define FLYAI_ABI_VERSION 2
 
 /* Last error message of the calling thread ("" when none). */
 const char* flyai_last_error(void);
@@ -185,7 +185,9 @@ int flyai_moe_combine_sum(const uint16_t* y_perm, const int32_t* inv, int32_t T,
  * the attention kernel's MFMA-fragment order: K block [kt 4][step 2][lane 64][8], lane 16gd+n holding
  * key 32(kt/2) + 8(n/4) + 4(kt%2) + n%4 and dims 32step+8gd..+7; V block [h 2][dt 4][lane 64][8], lane
  * 16gk+n holding dim 16dt+n and keys 32h+8gk..+7 (flyai_amd/kvlayout.py restates it).  cos_tab/sin_tab bf16
- * [rope_positions][D/2]; a token whose position is outside the table or its slab is skipped. */
+ * [rope_positions][D/2]; a token whose position is outside the table or its slab is skipped.  kv_base and
+ * kv_cap are device arrays here, so these standalone kernels cannot check a slab against its pool: the
+ * caller keeps every slab inside its pools (flyai_stage_forward checks this on the host). */
 int flyai_rmsnorm(const uint16_t* x, const float* w, int32_t T, int32_t H, float eps, uint16_t* y,
                   flyai_stream_t stream);
 size_t flyai_linear_workspace_bytes(int32_t M, int32_t N, int32_t K);
@@ -209,7 +211,8 @@ int flyai_rope_kv_append(const uint16_t* qkv, const int32_t* positions, const in
  * Work is split over (sequence, kv head, group of <= 4 query tokens, key split); the host-side
  * plan (flyai_attn_plan) is copied to the device by the caller.  The plan lists groups of <= 2
  * tokens first (n_items_small items, run by a one-tile kernel variant), then the rest.  D == 64,
- * Hq/Hkv == 8, kv_cap[b] % 64 == 0, kv_base[b] % 8 == 0, starts[b] + q_lens[b] <= kv_cap[b].
+ * Hq/Hkv == 8, kv_cap[b] % 64 == 0, kv_base[b] % 8 == 0, starts[b] + q_lens[b] <= kv_cap[b], and every
+ * slab inside its pools (device arrays: not checked here; flyai_stage_forward checks them).
  * Partials scratch: flyai_attn_partials_bytes(n_items). */
 typedef struct {
   int32_t seq;      /* sequence index b */
@@ -309,13 +312,17 @@ typedef struct {
   const uint8_t* w2_packed;   /* flyai_mxfp4_repack of down blocks/scales */
   const float* b2;            /* fp32 [E, H] */
   uint16_t* k_pool;           /* this layer's K pool */
-  uint16_t* v_pool;           /* this layer's V pool (transposed slabs) */
+  uint16_t* v_pool;           /* this layer's V pool (tiled slabs, same size as k_pool) */
   int32_t sliding;            /* 1: sliding-window layer */
   int32_t pad;
+  int64_t kv_pool_elems;      /* bf16 elements of k_pool and of v_pool (each); > 0 */
 } flyai_layer_desc;
 
 typedef struct flyai_stage flyai_stage;
 
+/* Rebinding rule: flyai_stage_set_layer, flyai_stage_set_rope and flyai_stage_set_workspace drop every
+ * captured step graph (see flyai_stage_set_graphs), because a graph keeps the pointers bound when it was
+ * captured; the next step with graphs enabled captures again from the new bindings. */
 int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** out);
 void flyai_stage_destroy(flyai_stage* st);
 int flyai_stage_set_layer(flyai_stage* st, int32_t layer, const flyai_layer_desc* desc);
@@ -327,7 +334,10 @@ int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t dev_bytes, v
                               size_t host_bytes);
 /* One step.  Batch description on the host (validated here; ContextOverflow -> FLYAI_ERANGE before
  * any launch): per sequence q_lens, starts, kv_base (element offset of its slab in every layer's
- * pools), kv_cap.  hidden: device bf16 [T, H] in packed token order, updated in place. */
+ * pools), kv_cap.  hidden: device bf16 [T, H] in packed token order, updated in place.
+ * Slab bounds: sequence b's slab is [kv_base[b], kv_base[b] + n_kv_heads*kv_cap[b]*head_dim) in every
+ * layer's pools.  A slab that ends past the smallest bound kv_pool_elems -> FLYAI_ERANGE; two
+ * sequences whose slabs overlap (their K/V writes would race) -> FLYAI_EINVAL; both before any launch. */
 int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens_host, const int32_t* starts_host,
                         const int64_t* kv_base_host, const int32_t* kv_cap_host, int32_t n_seqs,
                         uint16_t* hidden, flyai_stream_t stream);
@@ -340,7 +350,8 @@ int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens_host, const int32
  * validate_tree (fastverify.py:29-49): parent[i] in [-1, n), parent[i] != i, depth[i] == 0 for a
  * root and depth[parent[i]] + 1 otherwise (which rules out cycles); FLYAI_EINVAL otherwise, and for
  * n_nodes outside [1, 64] (the ancestor sets are 64-bit masks).  start + n_nodes past kv_cap or the
- * rope table -> FLYAI_ERANGE before any launch.  Always launched directly (no graph). */
+ * rope table, or a slab past the pools -> FLYAI_ERANGE before any launch.  Always launched directly
+ * (no graph). */
 typedef struct {
   int32_t start;          /* committed length: node i's K/V sits at slot start + i */
   int32_t n_nodes;        /* 1..64 */

@@ -16,6 +16,7 @@ E8M0 byte 255 is NaN (OCP MX v1.0 section 5.4); every value scaled by it is NaN.
 against the transformers fixture (tests/golden) and against the table below.
 """
 import numpy as np
+import torch
 
 # mxfp4.py:29-46, in code order 0..15 (codes 8..15 are the negatives, sign = bit 3).
 FP4_VALUES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0,
@@ -33,14 +34,18 @@ def e8m0_to_f32(s):
     return out.astype(np.float32)
 
 
+_PAIR_LUT_T = torch.from_numpy(PAIR_LUT)
+
+
 def dequant(blocks, scales):
-    """blocks u8 [..., G, 16], scales u8 [..., G] -> float32 [..., G*32] (exact)."""
-    blocks = np.asarray(blocks, dtype=np.uint8)
+    """blocks u8 [..., G, 16], scales u8 [..., G] -> float32 [..., G*32] (exact).  The table lookup
+    and the power-of-two scaling run as torch CPU ops, which use every intra-op thread."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.uint8)
     scales = np.asarray(scales, dtype=np.uint8)
     assert blocks.shape[:-1] == scales.shape and blocks.shape[-1] == 16
-    vals = PAIR_LUT[blocks].reshape(*blocks.shape[:-1], 32)   # low nibble first
-    vals *= e8m0_to_f32(scales)[..., None]
-    return vals.reshape(*blocks.shape[:-2], blocks.shape[-2] * 32).astype(np.float32)
+    vals = _PAIR_LUT_T[torch.from_numpy(blocks).long()].reshape(*blocks.shape[:-1], 32)  # low nibble first
+    vals *= torch.from_numpy(e8m0_to_f32(scales))[..., None]
+    return vals.reshape(*blocks.shape[:-2], blocks.shape[-2] * 32).numpy()
 
 
 def dequant_rows(blocks, scales, rows):

@@ -36,7 +36,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.flyai_abi_version() == 1
+    assert lib.flyai_abi_version() == 2
     from flyai_amd import _lib
     rc = lib.flyai_moe_permute(None, 4, 4, 300, None, None, None, None, None)
     assert rc == _lib.FLYAI_EINVAL

@@ -1,0 +1,219 @@
+"""The benchmark workloads themselves, run through the stage and checked against the oracle.
+
+* C1 (the headline): 9-layer GPT-OSS-shaped stage, 128 experts top-4, a ragged batch of 32 sequences
+  (24 decode + 8 four-token verify rows, T = 56) with KV lengths U[512, 8192] -- exactly bench.py's
+  batch.  One sliding and one full layer, each from the GPU's own input, against the oracle on the
+  whole batch; routing invariants on the whole batch; batched == solo on three streams through a
+  two-layer stage (the batch being replaced is phase0/batchverify.py:166-190).
+* C2: one 2048-token prefill chunk at prior KV 4096 plus 48 decode rows (T = 2096, ~65 rows per
+  expert, so the dense expert GEMM and the prefill attention items run).  Invariants on the whole
+  batch; the oracle on the chunk's last rows and every decode row, as their own ragged batch, from
+  the GPU's layer input and the GPU-written KV.
+* C3: the DeepSeek-V3-shaped FP8 layer (H 7168, 256 experts top-8 grouped sigmoid with the Zipf-
+  shaped bias, one shared expert) on bench.py's 64-sequence batch of 1/2/4 tokens (T = 155).  The
+  router bit-exact on the whole batch; the oracle on 32 tokens, every one of which sits in the hot
+  expert's dense group.
+
+A subset comparison is valid because a row's result does not depend on its batch mates
+(test_batched_equals_solo_bit_exact, test_dense_and_row_pass_experts_bit_identical).  Bars: the
+north_star's max-abs-rel 2e-2 and cosine 0.999 per layer, and cosine 0.999 on the layer's increment
+(h_out - h_in) alone, since the residual dominates the sum."""
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import layer as olayer
+
+pytestmark = pytest.mark.gpu
+
+MAR, COS = 2e-2, 0.999
+DEV = "cuda"
+
+
+def _routing_invariants(ids, perm, inv, off, E, k):
+    T = ids.shape[0]
+    hist = np.bincount(ids.reshape(-1), minlength=E)
+    assert off[0] == 0 and off[-1] == T * k and np.array_equal(np.diff(off), hist)
+    assert np.array_equal(np.sort(perm), np.arange(T * k))
+    assert np.array_equal(inv[perm], np.arange(T * k))
+    flat = ids.reshape(-1)
+    assert (flat[perm] == np.repeat(np.arange(E), hist)).all()
+    for e in range(E):                              # stable: flat index ascending within an expert
+        seg = perm[off[e]:off[e + 1]]
+        assert (np.diff(seg) > 0).all()
+    assert (np.diff(ids, axis=1) > 0).all(), "ids not ascending / not distinct per token"
+    return hist
+
+
+def _stage_layer_debug(st, T, E, k):
+    ids = st.debug_buffer(4, torch.int32, (T, k)).cpu().numpy()
+    perm = st.debug_buffer(7, torch.int32, (T * k,)).cpu().numpy()
+    inv = st.debug_buffer(8, torch.int32, (T * k,)).cpu().numpy()
+    off = st.debug_buffer(6, torch.int32, (E + 1,)).cpu().numpy()
+    return ids, perm, inv, off
+
+
+def _gptoss_setup(q_lens, starts, n_layers, seed, maxlen):
+    from flyai_amd.rope import YarnRotary
+    from flyai_amd.runtime import KVWorkspace
+    from flyai_amd.weights import GptOssShape, synthetic_layer
+    shape = GptOssShape()
+    layers = [synthetic_layer(shape, seed + i, DEV, sliding=(i % 2 == 0), keep_hf=True) for i in range(n_layers)]
+    rot = YarnRotary(maxlen, device=DEV)
+    kv = KVWorkspace(n_layers, len(q_lens), maxlen, shape.n_kv_heads, shape.head_dim, DEV)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed + 7)
+    for t in kv.k + kv.v:
+        t.normal_(generator=g)
+    h = torch.randn(sum(q_lens), shape.hidden, device=DEV, generator=g).to(torch.bfloat16)
+    return shape, layers, rot, kv, h
+
+
+def test_c1_workload_layers_vs_oracle_and_batch_invariance():
+    from gpu_harness import (_SingleLayerKV, cpu_f32, metrics, oracle_kv, oracle_layer_params,
+                             tokens_with_same_routing)
+    from flyai_amd.runtime import RaggedStage
+    q_lens, starts = bench.c1_batch(0)
+    S, T = len(q_lens), sum(q_lens)
+    assert (S, T) == (32, 56)
+    maxlen = 8192 + 64
+    shape, layers, rot, kv, h0 = _gptoss_setup(q_lens, starts, 2, 1000, maxlen)
+    E, k = shape.n_experts, shape.top_k
+    slots = list(range(S))
+    kv0 = [(a.clone(), b.clone()) for a, b in zip(kv.k, kv.v)]
+    cos, sin = olayer.rope_table(maxlen)
+
+    h = h0.clone()
+    for l, lw in enumerate(layers):
+        okv = oracle_kv(kv, l, slots)
+        st = RaggedStage(shape, [lw], rot, _SingleLayerKV(kv, l), max_tokens=64, max_seqs=S)
+        hin = cpu_f32(h)
+        h = st.forward(h.clone(), q_lens, starts, slots)
+        torch.cuda.synchronize()
+        ids, perm, inv, off = _stage_layer_debug(st, T, E, k)
+        _routing_invariants(ids, perm, inv, off, E, k)
+        assert T * k < 8 * E, "C1 is the decode tail: every group takes the row-pass kernel"
+        tr = {}
+        ref = olayer.decoder_layer(hin, oracle_layer_params(lw, lw.sliding), okv, q_lens, starts, cos, sin, trace=tr)
+        good = tokens_with_same_routing(ids, tr["ids"], tr["logits"], k)
+        out = cpu_f32(h).numpy()
+        mar, c = metrics(out[good], ref.numpy()[good])
+        assert mar <= MAR and c >= COS, f"C1 layer {l}: max-abs-rel {mar:.3g} cos {c:.6f}"
+        _, c = metrics((out - hin.numpy())[good], (ref.numpy() - hin.numpy())[good])
+        assert c >= COS, f"C1 layer {l}: increment cos {c:.6f}"
+        attn = cpu_f32(st.debug_buffer(3, torch.bfloat16, (T, shape.n_q_heads * shape.head_dim))).numpy()
+        mar, c = metrics(attn, tr["attn"].reshape(T, -1).numpy())
+        assert mar <= 1e-2 and c >= 0.9999, f"C1 layer {l} attention: {mar:.3g} {c:.6f}"
+        del st
+
+    # batched == solo, bit for bit, through the two-layer stage
+    for l, (a, b) in enumerate(kv0):
+        kv.k[l].copy_(a)
+        kv.v[l].copy_(b)
+    st = RaggedStage(shape, layers, rot, kv, max_tokens=64, max_seqs=S)
+    batched = st.forward(h0.clone(), q_lens, starts, slots).clone()
+    torch.cuda.synchronize()
+    cu = np.concatenate([[0], np.cumsum(q_lens)])
+    for b in (0, 24, 31):
+        for l, (a, v) in enumerate(kv0):
+            kv.k[l].copy_(a)
+            kv.v[l].copy_(v)
+        solo = st.forward(h0[cu[b]:cu[b + 1]].clone(), [q_lens[b]], [starts[b]], [b])
+        torch.cuda.synchronize()
+        assert torch.equal(solo, batched[cu[b]:cu[b + 1]]), f"C1 stream {b}: solo differs from batched"
+
+
+def test_c2_workload_layers_vs_oracle():
+    from gpu_harness import _SingleLayerKV, cpu_f32, metrics, oracle_layer_params, tokens_with_same_routing
+    from flyai_amd.runtime import RaggedStage
+    q_lens, starts = bench.c2_batch(0)
+    S, T = len(q_lens), sum(q_lens)
+    assert (S, T, q_lens[0], starts[0]) == (49, 2096, 2048, 4096)
+    maxlen = 8192 + 64
+    shape, layers, rot, kv, h = _gptoss_setup(q_lens, starts, 2, 3000, maxlen)
+    E, k = shape.n_experts, shape.top_k
+    slots = list(range(S))
+    # the subset: the chunk's last 4 rows, its first 2 rows, and every decode row
+    picks = [(0, 4, "tail"), (0, 2, "head")] + [(b, 1, "tail") for b in range(1, S)]
+    cu = np.concatenate([[0], np.cumsum(q_lens)])
+    rows, sub_q, sub_starts = [], [], []
+    for b, n, where in picks:
+        lo = cu[b + 1] - n if where == "tail" else cu[b]
+        rows.extend(range(lo, lo + n))
+        sub_q.append(n)
+        sub_starts.append(starts[b] + (q_lens[b] - n if where == "tail" else 0))
+    rows = np.asarray(rows)
+    sub_slots = [b for b, _, _ in picks]
+    cos, sin = olayer.rope_table(maxlen)
+    for l, lw in enumerate(layers):
+        st = RaggedStage(shape, [lw], rot, _SingleLayerKV(kv, l), max_tokens=T, max_seqs=S)
+        hin = h
+        h = st.forward(hin.clone(), q_lens, starts, slots)
+        torch.cuda.synchronize()
+        assert torch.isfinite(h.float()).all(), f"C2 layer {l}: non-finite output"
+        ids, perm, inv, off = _stage_layer_debug(st, T, E, k)
+        hist = _routing_invariants(ids, perm, inv, off, E, k)
+        assert (hist > 8).sum() >= E // 2, "C2 should put most experts on the dense kernel"
+        # oracle on the subset from the GPU's layer input and the GPU-written KV (each pick reads
+        # its own copy of its sequence's slab)
+        ks = [cpu_f32(kv.k_dense(l, b)) for b in sub_slots]
+        vs = [cpu_f32(kv.v_dense(l, b)) for b in sub_slots]
+        tr = {}
+        hin_sub = cpu_f32(hin)[rows]
+        ref = olayer.decoder_layer(hin_sub, oracle_layer_params(lw, lw.sliding), (ks, vs), sub_q, sub_starts,
+                                   cos, sin, trace=tr)
+        out = cpu_f32(h).numpy()[rows]
+        good = tokens_with_same_routing(ids[rows], tr["ids"], tr["logits"], k)
+        mar, c = metrics(out[good], ref.numpy()[good])
+        assert mar <= MAR and c >= COS, f"C2 layer {l}: max-abs-rel {mar:.3g} cos {c:.6f}"
+        _, c = metrics((out - hin_sub.numpy())[good], (ref.numpy() - hin_sub.numpy())[good])
+        assert c >= COS, f"C2 layer {l}: increment cos {c:.6f}"
+        attn = cpu_f32(st.debug_buffer(3, torch.bfloat16, (T, shape.n_q_heads * shape.head_dim))).numpy()[rows]
+        mar, c = metrics(attn, tr["attn"].reshape(len(rows), -1).numpy())
+        assert mar <= 1e-2 and c >= 0.9999, f"C2 layer {l} attention: {mar:.3g} {c:.6f}"
+        del st
+
+
+def test_c3_workload_layer_vs_oracle():
+    from gpu_harness import metrics
+    from test_gpu_fp8 import GpuFp8Experts
+    from flyai_amd import ops
+    from flyai_amd.runtime import Fp8MoeStage
+    from flyai_amd.weights import DsV3Shape, synthetic_fp8_moe_layer
+    from oracle import experts as oexperts
+    from oracle import routing as oroute
+    sh = DsV3Shape()
+    q_lens = bench.c3_batch(0)
+    T = sum(q_lens)
+    assert (len(q_lens), T) == (64, 155)
+    E, k = sh.n_experts, sh.top_k
+    lw = synthetic_fp8_moe_layer(sh, 2000, DEV, keep_raw=True)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(7)
+    h0 = torch.randn(T, sh.hidden, device=DEV, generator=g).to(torch.bfloat16)
+    xn = ops.rmsnorm(h0, lw.ln, sh.rms_eps)
+    ids, wts, _ = ops.router_grouped_sigmoid(xn, lw.router_w, lw.e_bias, sh.n_group, sh.topk_group, k, sh.route_scale)
+    hist, off, perm, inv = ops.moe_permute(ids, E)
+    h = Fp8MoeStage(sh, [lw]).forward(h0.clone())
+    torch.cuda.synchronize()
+    xc = xn.float().cpu().numpy()
+    rids, rwts, _ = oroute.grouped_sigmoid_route(xc, lw.router_w.float().cpu().numpy(), lw.e_bias.cpu().numpy(),
+                                                 sh.n_group, sh.topk_group, k, sh.route_scale)
+    assert np.array_equal(ids.cpu().numpy(), rids), "C3 router ids differ from the oracle"
+    assert np.array_equal(wts.cpu().numpy(), rwts), "C3 router weights differ from the oracle"
+    hist_np = _routing_invariants(ids.cpu().numpy(), perm.cpu().numpy(), inv.cpu().numpy(), off.cpu().numpy(), E, k)
+    hot = int(np.argmax(hist_np))
+    assert hist_np[hot] > 16, "the hot expert's group must take the dense FP8 kernel"
+    # 32 tokens on the hot expert, spread over the batch
+    on_hot = np.nonzero((rids == hot).any(1))[0]
+    assert len(on_hot) >= 32
+    sub = on_hot[np.linspace(0, len(on_hot) - 1, 32).round().astype(int)]
+    y = oexperts.deepseek_moe(xc[sub], rids[sub], rwts[sub], GpuFp8Experts(lw.raw), GpuFp8Experts(lw.shared_raw))
+    h0c = h0.float().cpu()[sub]
+    ref = (h0c + y).to(torch.bfloat16).float()
+    out = h.float().cpu()[sub]
+    mar, c = metrics(out.numpy(), ref.numpy())
+    assert mar <= MAR and c >= COS, f"C3 layer: {mar:.3g} {c:.6f}"
+    _, c = metrics((out - h0c).numpy(), (ref - h0c).numpy())
+    assert c >= COS, f"C3 MoE increment cos {c:.6f}"

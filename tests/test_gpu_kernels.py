@@ -528,3 +528,40 @@ def test_batched_equals_solo_bit_exact():
         solo = st.forward(case["hidden"][cu[b]:cu[b + 1]].clone(), [q_lens[b]], [starts[b]], [b])
         torch.cuda.synchronize()
         assert torch.equal(solo, batched[cu[b]:cu[b + 1]]), f"stream {b} differs solo vs batched"
+
+
+def test_dense_and_row_pass_experts_bit_identical():
+    """The same rows through the row-pass expert kernel (a batch below the dense cutoff of 8 rows per
+    expert on average) and through the dense tiled GEMM (a batch above it) give bit-identical h and y:
+    both feed the MFMA the same K-to-lane mapping, accumulate the 128-K groups in the same order from
+    zero and share the epilogue arithmetic.  So a row's tokens do not depend on whether its batch
+    mates push the batch across the cutoff (the reference's Triton path measured the opposite,
+    docs/receipts/batched-verify-20260623.json:27-30).  Dense groups of 100 rows take a 96-row pass
+    and a 32-row pass; H = I = 2880 leaves a partial last 128-K group."""
+    from flyai_amd import ops
+    from flyai_amd.weights import GptOssShape, synthetic_moe
+    E, k = 4, 4
+    shape = GptOssShape(n_experts=E)
+    m = synthetic_moe(shape, _gen(31), DEV)
+    w13 = ops.mxfp4_repack(m["w13_blocks"], m["w13_scales"])
+    w2 = ops.mxfp4_repack(m["w2_blocks"], m["w2_scales"])
+    T = 100
+    x = _rms_input(T, shape.hidden, 32)
+    ids = torch.arange(E, dtype=torch.int32, device=DEV).repeat(T, 1).contiguous()  # every token on every expert
+    _, off_a, perm_a, _ = ops.moe_permute(ids, E)
+    h_a = ops.moe_gate_up(x, perm_a, off_a, k, w13, m["b13"], E, shape.intermediate)   # 400 rows: dense
+    y_a = ops.moe_down(h_a, off_a, w2, m["b2"], E, shape.hidden)
+    for sel in ([0, 1, 2, 3, 4, 5, 6], [99, 17, 50], [64, 95, 96, 97]):   # 4 * len(sel) < 32: row-pass
+        sel_t = torch.tensor(sel, device=DEV)
+        ids_b = ids[:len(sel)].contiguous()
+        _, off_b, perm_b, _ = ops.moe_permute(ids_b, E)
+        xb = x[sel_t].contiguous()
+        h_b = ops.moe_gate_up(xb, perm_b, off_b, k, w13, m["b13"], E, shape.intermediate)
+        y_b = ops.moe_down(h_b, off_b, w2, m["b2"], E, shape.hidden)
+        torch.cuda.synchronize()
+        oa, ob = off_a.cpu().tolist(), off_b.cpu().tolist()
+        for e in range(E):
+            ra = torch.tensor([oa[e] + t for t in sel], device=DEV)   # expert e's rows are its tokens in order
+            rb = torch.arange(ob[e], ob[e] + len(sel), device=DEV)
+            assert torch.equal(h_a[ra], h_b[rb]), f"expert {e}, tokens {sel}: gate_up differs"
+            assert torch.equal(y_a[ra], y_b[rb]), f"expert {e}, tokens {sel}: down differs"

@@ -70,6 +70,8 @@ _PROTOS = {
     "flyai_rmsnorm": (C.c_int, [P, P, I32, I32, F32, P, P]),
     "flyai_linear_workspace_bytes": (SZ, [I32, I32, I32]),
     "flyai_linear_bf16": (C.c_int, [P, P, P, I32, I32, I32, P, P, P, P]),
+    "flyai_linear_noalloc_max_bytes": (SZ, []),
+    "flyai_linear_bf16_noalloc": (C.c_int, [P, P, P, I32, I32, I32, P, P, P]),
     "flyai_rope_kv_append": (C.c_int, [P, P, P, P, P, I32, I32, I32, I32, I32, P, P, P, P, P, P]),
     "flyai_attn_plan": (C.c_int, [P, P, I32, I32, I32, I32, P, I32, P, I32, P, P, P]),
     "flyai_attn_partials_bytes": (SZ, [I32]),

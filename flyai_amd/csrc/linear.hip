@@ -1,4 +1,5 @@
 // Layer glue: RMSNorm, bf16 projections with bias (+ residual), RoPE + KV append.
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -786,6 +787,62 @@ extern "C" int flyai_linear_bf16(const uint16_t* x, const uint16_t* w, const uin
                 "linear: need N %% 16 == 0, K %% 32 == 0, K <= 8192");
   FLYAI_REQUIRE(x && w && (y || residual) && workspace, "linear: null pointer");
   return launch_linear(x, w, b, M, N, K, y, residual, workspace, as_stream(stream));
+}
+
+// ---- the linear without allocation --------------------------------------------------------------
+// The split-K partial planes (or the tiled kernel's one folded plane) live in this file-scope device
+// array instead of a caller workspace.  Every GPU the library runs on holds its own copy, at its own
+// address, until the process ends.  In host code the name `scratch` is only a host-side stand-in: its
+// device address comes from hipGetSymbolAddress, resolved once per device with that device current and
+// kept in g_scratch_dev[]; kernels receive that address, never the name.
+constexpr size_t kLinearScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) float scratch[kLinearScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static float* g_scratch_dev[kMaxDevices] = {};
+
+static int linear_scratch(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(FLYAI_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return set_error(FLYAI_EINVAL, "linear_noalloc: device %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(FLYAI_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_dev[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return FLYAI_OK;
+}
+
+// bytes of partial planes launch_gemm writes and the finalizer reads for this shape
+static size_t linear_partials_used(int M, int N, int K) {
+  const int planes = M >= kTiledMinRows ? 1 : gemm_slices(K);
+  return (size_t)planes * M * N * sizeof(float);
+}
+
+extern "C" size_t flyai_linear_noalloc_max_bytes(void) { return kLinearScratchBytes; }
+
+extern "C" int flyai_linear_bf16_noalloc(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t M,
+                                         int32_t N, int32_t K, uint16_t* y, uint16_t* residual,
+                                         flyai_stream_t stream) {
+  FLYAI_REQUIRE(M >= 0 && N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0 && K <= 8192,
+                "linear: need N %% 16 == 0, K %% 32 == 0, K <= 8192");
+  FLYAI_REQUIRE(x && w && (y || residual), "linear: null pointer");
+  const size_t need = linear_partials_used(M, N, K);
+  FLYAI_REQUIRE(need <= kLinearScratchBytes,
+                "linear_noalloc: M=%d N=%d K=%d needs %zu partial bytes > the %zu-byte static scratch", M, N, K,
+                need, kLinearScratchBytes);
+  if (M == 0) return FLYAI_OK;
+  float* part = nullptr;
+  const int rc = linear_scratch(&part);
+  if (rc) return rc;
+  // every partial the finalizer reads is written by this call's GEMM first: nothing needs clearing
+  return launch_linear(x, w, b, M, N, K, y, residual, part, as_stream(stream));
 }
 
 extern "C" int flyai_rope_kv_append(const uint16_t* qkv, const int32_t* positions,

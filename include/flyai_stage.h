@@ -194,6 +194,18 @@ size_t flyai_linear_workspace_bytes(int32_t M, int32_t N, int32_t K);
 int flyai_linear_bf16(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t M, int32_t N,
                       int32_t K, uint16_t* y, uint16_t* residual, float* workspace,
                       flyai_stream_t stream);
+/* flyai_linear_bf16 without allocation.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory or pass a workspace (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results minus the workspace, same kernels and
+ * bits: the fp32 partials live in a static device array of flyai_linear_noalloc_max_bytes() = 16 MiB
+ * that every GPU the library runs on holds until the process ends.  A shape whose partials exceed it
+ * -> FLYAI_EINVAL before any launch (partials = 4*M*N bytes, times ceil(ceil(K/128)/4) planes below 256
+ * rows; one plane from 256 rows).  The first call on a device resolves the array's address there.
+ * Every call on one GPU shares that array and it keeps the last call's contents: calls that overlap on
+ * one GPU (other streams or threads) race, so the caller serialises them. */
+size_t flyai_linear_noalloc_max_bytes(void);
+int flyai_linear_bf16_noalloc(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t M, int32_t N,
+                              int32_t K, uint16_t* y, uint16_t* residual, flyai_stream_t stream);
 int flyai_rope_kv_append(const uint16_t* qkv, const int32_t* positions, const int32_t* seq_id,
                          const uint16_t* cos_tab, const uint16_t* sin_tab, int32_t rope_positions,
                          int32_t T, int32_t Hq, int32_t Hkv, int32_t D, const int64_t* kv_base,

@@ -1,27 +1,39 @@
 """Benchmark: one GPT-OSS-120B-shaped pipeline stage's continuous-batch forward step on one MI355X.
 
-Workload (default): 9 decoder layers (sliding window 128 on even layers, full attention on odd),
-64 query / 8 KV heads of dim 64 with learned sinks, 128-expert top-4 MXFP4 MoE (H = I = 2880);
-a ragged batch of 32 sequences -- 24 single-token decode rows and 8 four-token spec-verify rows
-(56 tokens) -- with per-sequence KV length uniform in [512, 8192]; KV and activations bf16
-N(0,1), weights random-init (synthetic data, seed 0).
+Workload (default, c1): 9 decoder layers (sliding window 128 on even layers, full attention on odd),
+64 query / 8 KV heads of dim 64 with learned sinks, 128-expert top-4 MXFP4 MoE (H = I = 2880); a
+ragged batch of 32 sequences -- 24 single-token decode rows and 8 four-token spec-verify rows (56
+tokens) -- with per-sequence KV length uniform in [512, 8192]; KV and activations bf16 N(0,1),
+weights random-init (synthetic data, seed 0).
 
-A step is one stage forward over that batch.  value = tokens / second over the timed steps.
-The roofline object covers the dominant kernel (the MXFP4 gate_up expert GEMM), timed with HIP
-events on the stream it runs on; its algorithmic bytes count every touched expert's weights and
-scales once plus activations in and out.  cpu_baseline runs the CPU oracle on one of the nine
-layers (same inputs) and scales to the stage.
+A step is one stage forward over that batch.  value = tokens / second over the timed steps, inputs
+resident in HBM.  Beside it:
+* roofline -- the dominant kernel (the MXFP4 gate_up expert GEMM), HIP events on the stream it runs
+  on; its algorithmic bytes count every touched expert's codes, scales and bias once plus
+  activations in and out;
+* moe_layer_us -- one MoE block as a unit: route + top-k/permute, gate_up, down, combine (HIP
+  events over 100 replays after 20 warmup calls, the reference's convention,
+  research/v4_fp8_gemv_bench.py:11-17);
+* hbm_read_ceiling -- what a kernel that only streams reads reaches on this GPU;
+* cpu_baseline -- the CPU oracle on one sliding and one full layer of the same batch (warmup, then
+  the median of 3), scaled to the 9-layer stage.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
---workload c3 measures the DeepSeek-V3-shaped FP8 stage instead: 4 MoE layers (H 7168, 256 experts,
-top-8 grouped sigmoid routing with a Zipf-shaped selection bias, one shared expert, I 2048, e4m3
-weights with 128x128 E8M0 block scales), a ragged batch of 64 sequences of 1, 2 or 4 tokens.
+--workload c2: one 2048-token prefill chunk (prior KV 4096) + 48 decode rows on the same stage.
+--workload c3: the DeepSeek-V3-shaped FP8 stage: 4 MoE layers (H 7168, 256 experts, top-8 grouped
+  sigmoid routing with a Zipf-shaped selection bias, one shared expert, I 2048, e4m3 weights with
+  128x128 E8M0 block scales), a ragged batch of 64 sequences of 1, 2 or 4 tokens.
+--workload wire: activation frames over loopback TCP, HBM to HBM (decode rows h[8, 4, 2880] and a
+  4096-token prefill chunk), through the pageable path and the pinned ring.
 """
 import argparse
 import json
 import os
+import socket
+import statistics
 import sys
+import threading
 import time
 
 import numpy as np
@@ -30,13 +42,29 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0}
+READ_PROBE_WG_PER_CU = 8   # workgroups per CU of the read-streaming probe
 
+
+# ---- workloads -----------------------------------------------------------------------------------
 
 def c1_batch(seed=0):
+    """32 sequences: 24 single-token decode rows, 8 four-token verify rows; KV U[512, 8192]."""
     rng = np.random.default_rng(seed)
     q_lens = [1] * 24 + [4] * 8
     starts = [int(v) for v in rng.integers(512, 8192 + 1, size=32)]
     return q_lens, starts
+
+
+def c2_batch(seed=0):
+    """One 2048-token prefill chunk at prior KV 4096 plus 48 single-token decode rows."""
+    rng = np.random.default_rng(seed)
+    return [2048] + [1] * 48, [4096] + [int(v) for v in rng.integers(512, 8192 + 1, size=48)]
+
+
+def c3_batch(seed=0):
+    rng = np.random.default_rng(seed)
+    return [int(v) for v in rng.choice([1, 2, 4], size=64)]
 
 
 def gate_up_algorithmic_bytes(shape, hist, T, k):
@@ -54,6 +82,15 @@ def down_algorithmic_bytes(shape, hist, T, k):
     return touched * per_expert + T * k * I * 2 + T * k * H * 4, touched
 
 
+def moe_layer_algorithmic_bytes(shape, hist, T, k):
+    """The MoE block's bytes (route + permute + experts + combine): every touched expert's weights,
+    scales and biases once, x in (router and experts), y out, ids and weights."""
+    H, I, E = shape.hidden, shape.intermediate, shape.n_experts
+    touched = int((hist > 0).sum())
+    per_expert = 2 * I * H // 2 + 2 * I * H // 32 + H * I // 2 + H * I // 32 + 4 * (2 * I + H)
+    return touched * per_expert + E * H * 2 + T * H * 2 + T * H * 2 + T * k * 8
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -62,10 +99,14 @@ def main():
     ap.add_argument("--layers", type=int, default=9)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=50)
+    ap.add_argument("--moe-reps", type=int, default=100)
+    ap.add_argument("--read-probe-mib", type=int, default=2048,
+                    help="buffer size of the HBM read-streaming ceiling (0: skip)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after timing, copy a buffer of this many MiB 3 times (a known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
-    ap.add_argument("--workload", choices=("c1", "c2", "c3"), default="c1")
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "wire"), default="c1")
+    ap.add_argument("--frames", type=int, default=20, help="--workload wire: frames per path")
     ap.add_argument("--graphs", action="store_true",
                     help="replay the stage step as a HIP graph (measured slower than direct launches "
                          "on this stack, so off by default)")
@@ -76,9 +117,13 @@ def main():
         sys.exit(2)
     if args.workload == "c3":
         run_c3(args)
+    elif args.workload == "wire":
+        run_wire(args)
     else:
         run_gptoss(args, chunked_prefill=args.workload == "c2")
 
+
+# ---- measurement helpers ---------------------------------------------------------------------------
 
 def copy_probe(mib, dev):
     import torch
@@ -90,11 +135,76 @@ def copy_probe(mib, dev):
         torch.cuda.synchronize()
 
 
-def c2_batch(seed=0):
-    """One 2048-token prefill chunk at prior KV 4096 plus 48 single-token decode rows."""
-    rng = np.random.default_rng(seed)
-    return [2048] + [1] * 48, [4096] + [int(v) for v in rng.integers(512, 8192 + 1, size=48)]
+def hip_event_us(fn, reps, warmup=0):
+    """Average microseconds of fn() over reps calls (HIP events on the current stream, which is the
+    stream flyai_amd.ops passes to the library)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps
 
+
+def hbm_read_ceiling(mib, dev, reps=20, grid_per_cu=None):
+    """GB/s of a read-only streaming kernel over `mib` MiB (normal and nontemporal loads)."""
+    import ctypes as C
+    import torch
+    from flyai_amd._lib import check, lib
+    if mib <= 0:
+        return None
+    buf = torch.empty(mib << 20, dtype=torch.uint8, device=dev)
+    buf.random_(0, 256)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    grid = cus * (grid_per_cu or READ_PROBE_WG_PER_CU)
+    out = {"bytes": buf.numel(), "grid": grid}
+    for name, nt in (("normal_GBps", 0), ("nontemporal_GBps", 1)):
+        def run():
+            check(lib().flyai_hbm_read_probe(C.c_void_p(buf.data_ptr()), buf.numel(), nt, grid,
+                                             C.c_void_p(sink.data_ptr()),
+                                             C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+        us = hip_event_us(run, reps, warmup=3)
+        out[name] = round(buf.numel() / (us * 1e-6) / 1e9, 1)
+    del buf
+    return out
+
+
+def cpu_threads():
+    """Intra-op threads for the CPU oracle: every CPU this process may run on (its affinity mask,
+    which is the box's CPU share), unless OMP_NUM_THREADS narrows it."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = os.environ.get("OMP_NUM_THREADS", "").strip()
+    return max(1, min(n, int(env))) if env.isdigit() else n
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def timed_median(fn, runs=3, warmup=1):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), ts
+
+
+# ---- GPT-OSS stage (c1, c2) ------------------------------------------------------------------------
 
 def run_gptoss(args, chunked_prefill=False):
     import torch
@@ -108,10 +218,11 @@ def run_gptoss(args, chunked_prefill=False):
     shape = GptOssShape()
     q_lens, starts = c2_batch(0) if chunked_prefill else c1_batch(0)
     S, T = len(q_lens), sum(q_lens)
+    E, k = shape.n_experts, shape.top_k
     maxlen = 8192 + 64
     with_cpu = not args.no_cpu and not chunked_prefill
     print(f"[bench] building {args.layers}-layer stage ...", file=sys.stderr, flush=True)
-    layers = [synthetic_layer(shape, 1000 + i, dev, sliding=(i % 2 == 0), keep_hf=(i == 1 and with_cpu))
+    layers = [synthetic_layer(shape, 1000 + i, dev, sliding=(i % 2 == 0), keep_hf=(i < 2 and with_cpu))
               for i in range(args.layers)]
     rot = YarnRotary(maxlen, device=dev)
     kv = KVWorkspace(args.layers, S, maxlen, shape.n_kv_heads, shape.head_dim, dev)
@@ -120,6 +231,9 @@ def run_gptoss(args, chunked_prefill=False):
     for t in kv.k + kv.v:
         t.copy_(torch.randn(t.shape, device=dev, generator=g).to(torch.bfloat16))
     hidden0 = torch.randn(T, shape.hidden, device=dev, generator=g).to(torch.bfloat16)
+    cpu_inputs = None
+    if with_cpu:   # the oracle's copies of layers 0-1 and their KV, taken before any step writes
+        cpu_inputs = cpu_layer_inputs(layers[:2], kv, hidden0, S)
     stage = RaggedStage(shape, layers, rot, kv, max_tokens=max(64, T), max_seqs=S, use_graphs=args.graphs)
     slots = list(range(S))
     torch.cuda.synchronize()
@@ -140,47 +254,51 @@ def run_gptoss(args, chunked_prefill=False):
     ms_per_step = elapsed * 1e3 / args.steps
     value = T * args.steps / elapsed
 
-    # ---- dominant kernel: MXFP4 gate_up of layer 1 (full-attention layer), HIP events ----------
+    # ---- kernels of one MoE block, layer 1's weights, the stage's own RMS-normed rows -------------
     lw = layers[1]
     xn = stage.debug_buffer(0, torch.bfloat16, (T, shape.hidden)).clone()
-    ids, wts = ops.router_topk_softmax(xn, lw.router_w, lw.router_b, shape.top_k)
-    hist, off, perm, inv = ops.moe_permute(ids, shape.n_experts)
-    hmoe = ops.moe_gate_up(xn, perm, off, shape.top_k, lw.w13_packed, lw.b13, shape.n_experts, shape.intermediate)
+    resid = hidden0.clone()
+    ids, wts, hist, off, perm, inv = ops.moe_route_permute(xn, lw.router_w, lw.router_b, k)
+    hmoe = ops.moe_gate_up(xn, perm, off, k, lw.w13_packed, lw.b13, E, shape.intermediate)
+    y = ops.moe_down(hmoe, off, lw.w2_packed, lw.b2, E, shape.hidden)
     torch.cuda.synchronize()
     hist_np = hist.cpu().numpy()
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     reps = args.kernel_reps
-    ev[0].record()
-    for _ in range(reps):
-        ops.moe_gate_up(xn, perm, off, shape.top_k, lw.w13_packed, lw.b13, shape.n_experts, shape.intermediate)
-    ev[1].record()
-    for _ in range(reps):
-        ops.moe_down(hmoe, off, lw.w2_packed, lw.b2, shape.n_experts, shape.hidden)
-    ev[2].record()
-    torch.cuda.synchronize()
-    gu_us = ev[0].elapsed_time(ev[1]) * 1e3 / reps
-    dn_us = ev[1].elapsed_time(ev[2]) * 1e3 / reps
-    gu_bytes, touched = gate_up_algorithmic_bytes(shape, hist_np, T, shape.top_k)
-    dn_bytes, _ = down_algorithmic_bytes(shape, hist_np, T, shape.top_k)
+    gu_us = hip_event_us(lambda: ops.moe_gate_up(xn, perm, off, k, lw.w13_packed, lw.b13, E, shape.intermediate),
+                         reps, warmup=10)
+    dn_us = hip_event_us(lambda: ops.moe_down(hmoe, off, lw.w2_packed, lw.b2, E, shape.hidden), reps, warmup=10)
+
+    def moe_block():
+        i_, w_, _, o_, p_, v_ = ops.moe_route_permute(xn, lw.router_w, lw.router_b, k)
+        h_ = ops.moe_gate_up(xn, p_, o_, k, lw.w13_packed, lw.b13, E, shape.intermediate)
+        y_ = ops.moe_down(h_, o_, lw.w2_packed, lw.b2, E, shape.hidden)
+        ops.moe_combine(y_, v_, w_, residual=resid, out=resid)
+
+    moe_us = hip_event_us(moe_block, args.moe_reps, warmup=20)
+    gu_bytes, touched = gate_up_algorithmic_bytes(shape, hist_np, T, k)
+    dn_bytes, _ = down_algorithmic_bytes(shape, hist_np, T, k)
+    moe_bytes = moe_layer_algorithmic_bytes(shape, hist_np, T, k)
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
     dn_gbs = dn_bytes / (dn_us * 1e-6) / 1e9
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "moe_gate_up_c1_traffic.json")
-    if os.path.exists(tpath):
+    if os.path.exists(tpath) and not chunked_prefill:
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
-
+    ceiling = hbm_read_ceiling(args.read_probe_mib, dev)
     copy_probe(args.copy_probe_mib, dev)
-
-    cpu = None
-    if with_cpu:
-        cpu = cpu_baseline(layers[1], kv, 1, hidden0, q_lens, starts, slots, shape, maxlen, args.layers)
+    step_launch = "hip graph replay" if args.graphs else "direct launches"
+    moe = {"us": round(moe_us, 2), "ops": "route+top-k/permute, gate_up, down, combine",
+           "GB/s": round(moe_bytes / (moe_us * 1e-6) / 1e9, 1),
+           "frac": round(moe_bytes / (moe_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+           "algorithmic_bytes": moe_bytes, "experts_us": round(gu_us + dn_us, 2)}
 
     if chunked_prefill:
-        # dense groups (~65 rows per expert): the gate_up GEMM against the bf16 MFMA peak
-        P = T * shape.top_k
+        # dense groups (~65 rows per expert): the gate_up GEMM against the MFMA peak of its dtype
+        P = T * k
         flops = 2.0 * P * shape.hidden * 2 * shape.intermediate
         tflops = flops / (gu_us * 1e-6) / 1e12
+        peak = MFMA_PEAK_TFLOPS["bf16"]
         line = {
             "metric": "stage tokens/sec at a chunked-prefill mixed batch; MoE layer us; % MFMA roofline",
             "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -189,20 +307,21 @@ def run_gptoss(args, chunked_prefill=False):
             "data": "synthetic (seeded random-init weights, N(0,1) KV and activations)",
             "config": {"workload": "gpt-oss-120b-shaped 9-layer MXFP4 stage, one 2048-token prefill chunk "
                                    "(prior KV 4096) + 48 decode rows (KV 512-8192)",
-                       "layers": args.layers, "tokens": T, "sequences": S, "experts": shape.n_experts,
-                       "top_k": shape.top_k, "hidden": shape.hidden, "parallelism": "single GPU",
-                       "step_launch": "hip graph replay" if args.graphs else "direct launches"},
-            "moe_layer_us": round(gu_us + dn_us, 2),
+                       "layers": args.layers, "tokens": T, "sequences": S, "experts": E,
+                       "top_k": k, "hidden": shape.hidden, "parallelism": "single GPU", "step_launch": step_launch},
+            "moe_layer_us": moe["us"], "moe_layer": moe,
             "roofline": {"bound": "mfma", "kernel": "moe_mxfp4_gemm_kernel<gate_up>", "achieved": round(tflops, 1),
-                         "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                         "peak": peak, "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": None,
                          "algorithmic_flops": flops, "avg_us": round(gu_us, 2), "hbm_GB/s": round(gu_gbs, 1)},
             "kernels": {"moe_down": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),
                                      "TFLOP/s": round(flops / 2 / (dn_us * 1e-6) / 1e12, 1)}},
+            "hbm_read_ceiling": ceiling,
             "cpu_baseline": None,
         }
         print(json.dumps(line))
         return
 
+    cpu = cpu_baseline(cpu_inputs, q_lens, starts, maxlen, args.layers) if with_cpu else None
     line = {
         "metric": "stage tokens/sec at ragged batch 32; MoE layer us; % HBM/MFMA roofline",
         "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -211,25 +330,69 @@ def run_gptoss(args, chunked_prefill=False):
         "data": "synthetic (seeded random-init weights, N(0,1) KV and activations)",
         "config": {"workload": "gpt-oss-120b-shaped 9-layer MXFP4 stage, ragged batch of 32 sequences "
                                "(24 decode + 8 four-token verify = 56 tokens), KV 512-8192",
-                   "layers": args.layers, "tokens": T, "sequences": S, "experts": shape.n_experts,
-                   "top_k": shape.top_k, "hidden": shape.hidden, "parallelism": "single GPU",
-                   "step_launch": "hip graph replay" if args.graphs else "direct launches"},
-        "moe_layer_us": round(gu_us + dn_us, 2),
+                   "layers": args.layers, "tokens": T, "sequences": S, "experts": E,
+                   "top_k": k, "hidden": shape.hidden, "parallelism": "single GPU", "step_launch": step_launch},
+        "moe_layer_us": moe["us"], "moe_layer": moe,
         "roofline": {"bound": "hbm", "kernel": "moe_mxfp4_kernel<gate_up>", "achieved": round(gu_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "algorithmic_bytes": gu_bytes, "avg_us": round(gu_us, 2),
                      "experts_touched": touched},
         "kernels": {"moe_down": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),
                                  "frac": round(dn_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": dn_bytes}},
+        "hbm_read_ceiling": ceiling,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
 
 
-def c3_batch(seed=0):
-    rng = np.random.default_rng(seed)
-    return [int(v) for v in rng.choice([1, 2, 4], size=64)]
+def cpu_layer_inputs(layers, kv, hidden0, S):
+    """Host copies of the given layers (oracle parameters) and of their KV, per slot."""
+    import torch
+    from oracle import experts as oexperts
+    from oracle import layer as olayer
+    f = lambda t: t.detach().float().cpu()
+    out = []
+    for i, lw in enumerate(layers):
+        moe = oexperts.MxExpertWeights(lw.w13_blocks.cpu().numpy(), lw.w13_scales.cpu().numpy(),
+                                       lw.b13.cpu().numpy(), lw.w2_blocks.cpu().numpy(),
+                                       lw.w2_scales.cpu().numpy(), lw.b2.cpu().numpy())
+        p = olayer.LayerParams(f(lw.ln1), f(lw.ln2), f(lw.wqkv), f(lw.bqkv), f(lw.wo), f(lw.bo), f(lw.sinks),
+                               f(lw.router_w), f(lw.router_b), moe, lw.sliding)
+        ks = [f(kv.k_dense(i, s)) for s in range(S)]
+        vs = [f(kv.v_dense(i, s)) for s in range(S)]
+        out.append((p, ks, vs))
+    torch.cuda.synchronize()
+    return {"layers": out, "h": f(hidden0)}
 
+
+def cpu_baseline(inp, q_lens, starts, maxlen, n_layers):
+    """The CPU oracle on one sliding (layer 0) and one full-attention layer (layer 1) of the same
+    batch, each a warmup then the median of 3 runs; the stage estimate is the 9-layer mix (5 sliding,
+    4 full) of those medians."""
+    import torch
+    from oracle import layer as olayer
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    cos, sin = olayer.rope_table(maxlen)
+    print(f"[bench] cpu oracle: one sliding + one full layer, {threads} threads", file=sys.stderr, flush=True)
+    med = []
+    for p, ks, vs in inp["layers"]:
+        def run():   # the layer rewrites the same K/V values at the batch's positions on every run
+            olayer.decoder_layer(inp["h"], p, (ks, vs), q_lens, starts, cos, sin)
+        m, _ = timed_median(run)
+        med.append(m)
+    n_sliding = (n_layers + 1) // 2
+    stage_s = n_sliding * med[0] + (n_layers - n_sliding) * med[1]
+    T = sum(q_lens)
+    return {"value": round(T / stage_s, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu": cpu_model(), "host_cpus": os.cpu_count(),
+            "sample": f"CPU oracle (torch fp32 + numpy) on layer 0 (sliding, median {med[0]:.2f} s) and "
+                      f"layer 1 (full attention, median {med[1]:.2f} s) of the same {T}-token batch, warmup + "
+                      f"median of 3 each; stage = {n_sliding} x sliding + {n_layers - n_sliding} x full = "
+                      f"{stage_s:.2f} s"}
+
+
+# ---- DeepSeek-V3-shaped FP8 stage (c3) ------------------------------------------------------------
 
 def run_c3(args):
     import torch
@@ -279,22 +442,17 @@ def run_c3(args):
     hist_np = hist.cpu().numpy()
     groups = int((hist_np > 0).sum()) + 1
     reps = args.kernel_reps
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-    ev[0].record()
-    for _ in range(reps):
-        ops.moe_gate_up_fp8(xq, xs, perm, off, k, wts, lw.w13_packed, E, I, n_shared=T)
-    ev[1].record()
-    for _ in range(reps):
-        ops.moe_down_fp8(hq, hsc, off, lw.w2_packed, E, H, n_shared=T)
-    ev[2].record()
-    torch.cuda.synchronize()
-    gu_us = ev[0].elapsed_time(ev[1]) * 1e3 / reps
-    dn_us = ev[1].elapsed_time(ev[2]) * 1e3 / reps
+    gu_us = hip_event_us(lambda: ops.moe_gate_up_fp8(xq, xs, perm, off, k, wts, lw.w13_packed, E, I, n_shared=T),
+                         reps, warmup=10)
+    dn_us = hip_event_us(lambda: ops.moe_down_fp8(hq, hsc, off, lw.w2_packed, E, H, n_shared=T), reps, warmup=10)
+    resid = hidden0.clone()
+    moe_us = hip_event_us(lambda: stage.moe(lw, hidden0, resid), args.moe_reps, warmup=20)
     P = T * k + T
     gu_bytes = groups * (2 * I * H + 2 * (I // 128) * (H // 128)) + T * H + T * (H // 128) + P * I * 2
     dn_bytes = groups * (H * I + (H // 128) * (I // 128)) + P * I + P * (I // 128) + P * H * 2
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
     dn_gbs = dn_bytes / (dn_us * 1e-6) / 1e9
+    ceiling = hbm_read_ceiling(args.read_probe_mib, dev)
     copy_probe(args.copy_probe_mib, dev)
 
     cpu = None
@@ -311,13 +469,17 @@ def run_c3(args):
                                "1/2/4 tokens, 256 experts top-8 grouped sigmoid (Zipf-shaped bias) + 1 shared",
                    "layers": n_layers, "tokens": T, "sequences": len(q_lens), "experts": E, "top_k": k,
                    "hidden": H, "intermediate": I, "parallelism": "single GPU"},
-        "moe_layer_us": round(gu_us + dn_us, 2),
+        "moe_layer_us": round(moe_us, 2),
+        "moe_layer": {"us": round(moe_us, 2), "ops": "rmsnorm, grouped router, permute, act quant, gate_up, "
+                                                      "act quant, down, combine (+ shared expert, residual)",
+                      "experts_us": round(gu_us + dn_us, 2)},
         "roofline": {"bound": "hbm", "kernel": "moe_fp8_kernel<gate_up> (tail + dense launches)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": gu_bytes,
                      "avg_us": round(gu_us, 2), "groups_touched": groups},
         "kernels": {"moe_down_fp8": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),
                                      "frac": round(dn_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": dn_bytes}},
+        "hbm_read_ceiling": ceiling,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
@@ -325,61 +487,117 @@ def run_c3(args):
 
 def cpu_baseline_c3(sh, lw, hidden0, n_layers, n_tokens):
     """The CPU oracle's FP8 MoE layer on the first n_tokens tokens of the batch (every expert those
-    tokens route to, plus the shared expert); stage tokens/s = n_tokens / (n_layers * t)."""
+    tokens route to, plus the shared expert), warmup + median of 3; stage tokens/s =
+    n_tokens / (n_layers * t)."""
     import torch
     from oracle import experts as oexperts
     from oracle import layer as olayer
-    threads = min(16, os.cpu_count() or 1)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
 
     class Experts:
         def __init__(self, raw):
-            self.raw = raw
+            self.raw = {n: t.cpu() for n, t in raw.items()}
 
         def expert(self, e, x, weight=None):
             r = self.raw
-            f8 = lambda t: t[e].cpu().view(torch.float8_e4m3fn).float().numpy()
-            e8 = lambda t: np.ldexp(np.float32(1.0), t[e].cpu().numpy().astype(np.int32) - 127).astype(np.float32)
+            f8 = lambda t: t[e].view(torch.float8_e4m3fn).float().numpy()
+            e8 = lambda t: np.ldexp(np.float32(1.0), t[e].numpy().astype(np.int32) - 127).astype(np.float32)
             return oexperts.deepseek_expert(x, f8(r["w1"]), e8(r["s1"]), f8(r["w3"]), e8(r["s3"]),
                                             f8(r["w2"]), e8(r["s2"]), weight)
 
     h = hidden0[:n_tokens].float().cpu()
+    ln, rw, eb = lw.ln.cpu(), lw.router_w.float().cpu().numpy(), lw.e_bias.cpu().numpy()
+    routed, shared = Experts(lw.raw), Experts(lw.shared_raw)
     print("[bench] cpu oracle: one FP8 MoE layer", file=sys.stderr, flush=True)
-    t0 = time.perf_counter()
-    olayer.deepseek_moe_layer(h, lw.ln.cpu(), sh.rms_eps, lw.router_w.float().cpu().numpy(), lw.e_bias.cpu().numpy(),
-                              sh.n_group, sh.topk_group, sh.top_k, sh.route_scale, Experts(lw.raw),
-                              Experts(lw.shared_raw))
-    dt = time.perf_counter() - t0
-    return {"value": round(n_tokens / (dt * n_layers), 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+    m, _ = timed_median(lambda: olayer.deepseek_moe_layer(h, ln, sh.rms_eps, rw, eb, sh.n_group, sh.topk_group,
+                                                          sh.top_k, sh.route_scale, routed, shared))
+    return {"value": round(n_tokens / (m * n_layers), 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu": cpu_model(), "host_cpus": os.cpu_count(),
             "sample": f"CPU oracle (numpy fp64 block GEMMs + torch) on 1 of {n_layers} layers for the first "
-                      f"{n_tokens} tokens of the batch: {dt:.2f} s; stage rate = {n_tokens} / ({n_layers} x layer time)"}
+                      f"{n_tokens} tokens of the batch, warmup + median of 3: {m:.2f} s; stage rate = "
+                      f"{n_tokens} / ({n_layers} x layer time)"}
 
 
-def cpu_baseline(lw, kv, layer_idx, hidden0, q_lens, starts, slots, shape, maxlen, n_layers):
-    """The CPU oracle on one decoder layer of the same batch; stage tokens/s = T / (n_layers * t)."""
+# ---- activation frames over loopback TCP (wire) ---------------------------------------------------
+
+WIRE_GEOMETRIES = {"decode_8x4": (8, 4, 2880), "prefill_1x4096": (1, 4096, 2880)}
+
+
+def _loopback_pair(W):
+    lst = socket.socket()
+    lst.bind(("127.0.0.1", 0))
+    lst.listen(1)
+    a = socket.create_connection(lst.getsockname(), timeout=60)
+    b, _ = lst.accept()
+    lst.close()
+    for s in (a, b):
+        W.tune_socket(s)
+        s.settimeout(60)
+    return a, b
+
+
+def _wire_path(W, path, h, frames, warmup):
+    """Frames of {"op": "verify", "h": h} sent by a thread and landed by the receiver: `socket_only`
+    (CPU to CPU, the socket's own rate), `pageable` (h.cpu(), recv_msg, .to(device): the reference's
+    call pattern) or `pinned_ring` (send_msg of the device tensor, recv_activation).  Time runs from
+    the first timed frame to the last one ready on the receiver's stream."""
     import torch
-    from oracle import experts as oexperts
-    from oracle import layer as olayer
-    threads = min(16, os.cpu_count() or 1)
-    torch.set_num_threads(threads)
-    f = lambda t: t.detach().float().cpu()
-    moe = oexperts.MxExpertWeights(lw.w13_blocks.cpu().numpy(), lw.w13_scales.cpu().numpy(),
-                                   lw.b13.cpu().numpy(), lw.w2_blocks.cpu().numpy(),
-                                   lw.w2_scales.cpu().numpy(), lw.b2.cpu().numpy())
-    p = olayer.LayerParams(f(lw.ln1), f(lw.ln2), f(lw.wqkv), f(lw.bqkv), f(lw.wo), f(lw.bo), f(lw.sinks),
-                           f(lw.router_w), f(lw.router_b), moe, lw.sliding)
-    ks = [f(kv.k_dense(layer_idx, s)) for s in slots]
-    vs = [f(kv.v_dense(layer_idx, s)) for s in slots]
-    cos, sin = olayer.rope_table(maxlen)
-    h = f(hidden0)
-    print("[bench] cpu oracle: one layer", file=sys.stderr, flush=True)
-    t0 = time.perf_counter()
-    olayer.decoder_layer(h, p, (ks, vs), q_lens, starts, cos, sin)
-    dt = time.perf_counter() - t0
-    T = sum(q_lens)
-    return {"value": round(T / (dt * n_layers), 4), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"CPU oracle (torch fp32 + numpy) on 1 of {n_layers} layers (a full-attention layer) "
-                      f"of the same 56-token batch: {dt:.2f} s; stage rate = 56 / ({n_layers} x layer time)"}
+    a, b = _loopback_pair(W)
+    dev = h.device
+    h_host = h.cpu()
+    total = frames + warmup
+
+    def sender():
+        for _ in range(total):
+            W.send_msg(a, {"op": "verify", "h": h.cpu() if path == "pageable" else h if path == "pinned_ring"
+                           else h_host})
+
+    t = threading.Thread(target=sender, daemon=True)
+    torch.cuda.synchronize()
+    t.start()
+    last = None
+    for i in range(total):
+        if i == warmup:
+            start = time.perf_counter()
+        if path == "pageable":
+            last = W.recv_msg(b)["h"].to(dev)
+        elif path == "pinned_ring":
+            last = W.recv_activation(b, dev)["h"]
+        else:
+            last = W.recv_msg(b)["h"]
+        if path != "socket_only":
+            torch.cuda.current_stream(dev).synchronize()
+    elapsed = time.perf_counter() - start
+    t.join(60)
+    a.close(), b.close()
+    nbytes = W.frame_length({"op": "verify", "h": h})
+    return {"ms_per_frame": round(elapsed / frames * 1e3, 4), "GBps": round(nbytes * frames / elapsed / 1e9, 3),
+            "frame_bytes": nbytes, "bytes_equal": bool(torch.equal(last.cpu(), h_host))}
+
+
+def run_wire(args):
+    import torch
+    from flyai_amd import transport as W
+    dev = "cuda"
+    torch.cuda.set_device(0)
+    results = {}
+    for name, shp in WIRE_GEOMETRIES.items():
+        g = torch.Generator(device=dev)
+        g.manual_seed(0)
+        h = torch.randn(shp, device=dev, generator=g).to(torch.bfloat16)
+        results[name] = {p: _wire_path(W, p, h, args.frames, 3) for p in ("socket_only", "pageable", "pinned_ring")}
+        print(f"[bench] wire {name}: {json.dumps(results[name])}", file=sys.stderr, flush=True)
+    pre = results["prefill_1x4096"]
+    line = {"metric": "activation frame HBM-to-HBM over loopback TCP (prefill chunk)",
+            "value": pre["pinned_ring"]["GBps"], "unit": "GB/s", "n_gpus": 1, "steps": args.frames, "warmup": 3,
+            "ms_per_step": pre["pinned_ring"]["ms_per_frame"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seeded N(0,1) activations)",
+            "config": {"workload": "activation frames h[1, 4096, 2880] and h[8, 4, 2880] bf16, loopback TCP, "
+                                   "32 MiB socket buffers", "chunk_bytes": W.CHUNK_BYTES, "ring_slots": W.RING_SLOTS,
+                       "parallelism": "single GPU"},
+            "results": results, "roofline": None, "cpu_baseline": None}
+    print(json.dumps(line))
 
 
 if __name__ == "__main__":

@@ -21,6 +21,7 @@ still arriving.  No frame-sized host buffer exists on either side of the device 
 """
 import ctypes
 import json
+import math
 import os
 import queue
 import socket
@@ -35,9 +36,17 @@ _DTYPES = {str(d): d for d in (torch.float32, torch.float16, torch.bfloat16, tor
                                torch.float8_e5m2, torch.int64, torch.int32, torch.uint8, torch.bool)}
 _ITEMSIZE = {d: torch.empty(0, dtype=d).element_size() for d in _DTYPES.values()}
 
-# Largest body a receiver accepts; the length prefix is read before anything authenticates the
-# frame, so a larger claim is refused before the body is read (env M25_MAX_FRAME, bytes).
-MAX_FRAME = int(os.environ.get("M25_MAX_FRAME") or 256 * 1024 * 1024)
+
+
+def _frame_cap():
+    """Largest frame body a receiver accepts, in bytes: M25_MAX_FRAME when set (the reference's knob),
+    else 256 MiB.  The length prefix arrives before anything vouches for the sender, so a larger
+    claim is refused before a byte of the body is read or allocated."""
+    text = os.environ.get("M25_MAX_FRAME", "").strip()
+    return int(text) if text else 256 << 20
+
+
+MAX_FRAME = _frame_cap()
 SOCK_BUF = 32 << 20          # socket buffers sized for a prefill-chunk activation in flight
 CHUNK_BYTES = 4 << 20        # device <-> pinned copy granularity of the device path
 RING_SLOTS = 4               # pinned ring depth per direction
@@ -102,23 +111,60 @@ def _pack(obj) -> bytes:
 
 # ---- decode ----------------------------------------------------------------------------------------
 
+_MAX_RANK = 32
+
+
+class _FrameReader:
+    """A cursor over one frame body.  Every length field is checked against the bytes that actually
+    follow it before anything is sliced or allocated; a violation raises ValueError, which the
+    socket readers turn into a dead-edge ConnectionError."""
+
+    def __init__(self, body):
+        self.mv = memoryview(body)
+        self.pos = 0
+
+    def left(self):
+        return len(self.mv) - self.pos
+
+    def take(self, n, what):
+        if n > self.left():
+            raise ValueError(f"{what}: {n} bytes declared, {self.left()} remain in the frame")
+        out = self.mv[self.pos:self.pos + n]
+        self.pos += n
+        return out
+
+    def u32(self, what):
+        return struct.unpack("!I", self.take(4, what))[0]
+
+    def u64(self, what):
+        return struct.unpack("!Q", self.take(8, what))[0]
+
+    def header(self):
+        n = self.u32("header length field")
+        return json.loads(bytes(self.take(n, "JSON header")))
+
+    def blobs(self):
+        out = []
+        while self.left():
+            n = self.u64(f"length field of blob {len(out)}")
+            out.append(self.take(n, f"blob {len(out)}"))
+        return out
+
+
 def _tensor_spec(node, n_blobs=None):
-    """(dtype, shape, nbytes, index) of a tensor node, validated; ValueError if malformed."""
+    """Validated (dtype, shape, byte size, blob index) of a header's tensor node."""
     dt = _DTYPES.get(node.get("dtype"))
     if dt is None:
-        raise ValueError(f"unknown tensor dtype {node.get('dtype')!r}")
+        raise ValueError(f"tensor node with unsupported dtype {node.get('dtype')!r}")
     index = node["__t__"]
-    if type(index) is not int or index < 0 or (n_blobs is not None and index >= n_blobs):
-        raise ValueError("invalid tensor blob index")
+    in_range = type(index) is int and index >= 0 and (n_blobs is None or index < n_blobs)
+    if not in_range:
+        raise ValueError(f"tensor node points at blob {index!r}, frame has {n_blobs}")
     shape = node.get("shape")
-    if not isinstance(shape, list) or len(shape) > 32:
-        raise ValueError("invalid tensor shape")
-    numel = 1
-    for d in shape:
-        if type(d) is not int or d < 0:
-            raise ValueError(f"bad tensor dim {d!r}")
-        numel *= d
-    return dt, shape, numel * _ITEMSIZE[dt], index
+    if not (isinstance(shape, list) and len(shape) <= _MAX_RANK and
+            all(type(d) is int and d >= 0 for d in shape)):
+        raise ValueError(f"tensor shape {shape!r} is not a list of <= {_MAX_RANK} non-negative ints")
+    return dt, shape, math.prod(shape) * _ITEMSIZE[dt], index
 
 
 def _decode(node, make_tensor):
@@ -131,116 +177,134 @@ def _decode(node, make_tensor):
     return node
 
 
-def _split_body(mv):
-    """(header object, blob memoryviews) of a frame body."""
-    if len(mv) < 4:
-        raise ValueError("truncated frame header")
-    (hlen,) = struct.unpack_from("!I", mv, 0)
-    if hlen > len(mv) - 4:
-        raise ValueError("header length exceeds frame")
-    head = json.loads(bytes(mv[4:4 + hlen]))
-    blobs, off = [], 4 + hlen
-    while off < len(mv):
-        if len(mv) - off < 8:
-            raise ValueError("truncated blob length")
-        (blen,) = struct.unpack_from("!Q", mv, off)
-        off += 8
-        if blen > len(mv) - off:
-            raise ValueError("blob length exceeds frame")
-        blobs.append(mv[off:off + blen])
-        off += blen
-    return head, blobs
-
-
 def _unpack(buf, *, copy_tensors=True):
-    """Decode one frame body into CPU tensors; ValueError if it is malformed.  With
-    copy_tensors=False the tensors view `buf` (which must then outlive them)."""
-    head, blobs = _split_body(memoryview(buf))
+    """One frame body -> message with CPU tensors.  A tensor's declared shape must account for its
+    blob exactly, so no header can make the decoder allocate more than the frame holds.  With
+    copy_tensors=False the tensors are views of `buf`, which must outlive them."""
+    rd = _FrameReader(buf)
+    head = rd.header()
+    blobs = rd.blobs()
 
-    def make(node):
+    def tensor(node):
         dt, shape, nbytes, index = _tensor_spec(node, len(blobs))
-        blob = blobs[index]
-        if nbytes != len(blob):
-            raise ValueError(f"tensor {shape} needs {nbytes} bytes, blob has {len(blob)}")
+        raw = blobs[index]
+        if nbytes != len(raw):
+            raise ValueError(f"{dt} tensor of shape {shape} is {nbytes} bytes; blob {index} holds {len(raw)}")
         if nbytes == 0:
-            return torch.empty(shape, dtype=dt, device="cpu")
-        arr = np.frombuffer(blob, dtype=np.uint8)
-        return torch.from_numpy(arr.copy() if copy_tensors else arr).view(dt).reshape(shape)
+            return torch.empty(shape, dtype=dt)
+        u8 = np.frombuffer(raw, dtype=np.uint8)
+        return torch.from_numpy(u8.copy() if copy_tensors else u8).view(dt).reshape(shape)
 
-    return _decode(head, make)
+    return _decode(head, tensor)
 
 
 # ---- receive buffer pool ---------------------------------------------------------------------------
+# Reusable host storage for recv_msg (the reference's opt-in pool, shard/receive_buffers.py:28-86,
+# and its process-wide switch, shard/transport.py:64-82).  A frame is read straight into a slot and
+# its tensors view the slot, so no second host copy is made.  A slot is leased until the last array
+# or tensor viewing it is gone; a full pool, a budget overrun or a failed allocation makes recv_msg
+# fall back to a frame-owned buffer.  The status dict follows the "shard-receive-buffer-pool/1" schema
+# its callers read (borrowed_frames, live_slots, ...).
+
+_POOL_MIN_BUDGET, _POOL_MAX_BUDGET, _POOL_MAX_SLOTS, _SLOT_MIN = 1 << 10, 512 << 20, 64, 1 << 10
+
+
+class _Slot:
+    __slots__ = ("buf", "leased")
+
+    def __init__(self, buf):
+        self.buf, self.leased = buf, False
+
+    @property
+    def capacity(self):
+        return self.buf.numel()
+
 
 class ReceiveBufferPool:
-    """Bounded, reusable receive storage for ``recv_msg``: the frame is read straight into a pool
-    slot and its tensors view that slot, which stays busy until the last such view is gone (freed
-    by reference counting, no cyclic GC needed).  A full pool or a failed allocation falls back to
-    a frame-owned buffer.  Same limits as the reference's pool (``shard/receive_buffers.py:28-86``):
-    budget 1 KiB..512 MiB, 1..64 slots, pinning explicit."""
+    """At most `slots` host buffers (page-locked when `pinned`), each a power of two of at least
+    1 KiB, never more than `budget_bytes` in total -- counting, while a slot is regrown, both its old
+    and its new buffer."""
 
     def __init__(self, budget_bytes, *, slots=2, pinned=False):
-        if type(budget_bytes) is not int or not 1024 <= budget_bytes <= 512 * 1024 ** 2:
-            raise ValueError("receive pool budget must be 1KiB..512MiB")
-        if type(slots) is not int or not 1 <= slots <= 64 or type(pinned) is not bool:
-            raise ValueError("bounded slot count and explicit pinning required")
+        if type(budget_bytes) is not int or not _POOL_MIN_BUDGET <= budget_bytes <= _POOL_MAX_BUDGET:
+            raise ValueError(f"budget_bytes must be an int in [{_POOL_MIN_BUDGET}, {_POOL_MAX_BUDGET}], "
+                             f"got {budget_bytes!r}")
+        if type(slots) is not int or not 1 <= slots <= _POOL_MAX_SLOTS:
+            raise ValueError(f"slots must be an int in [1, {_POOL_MAX_SLOTS}], got {slots!r}")
+        if type(pinned) is not bool:
+            raise ValueError(f"pinned must be True or False, got {pinned!r}")
         if pinned and not torch.cuda.is_available():
-            raise RuntimeError("pinned receive pool requires a GPU allocator")
+            raise RuntimeError("page-locked receive slots need the GPU runtime, which is not available")
         self.budget_bytes, self.slots, self.pinned = budget_bytes, slots, pinned
         self._lock = threading.Lock()
-        self._bufs, self._busy = [], set()
-        self.hits = self.fallbacks = self.high_water = self.allocation_failures = 0
+        self._table = []                     # _Slot records, at most `slots`
+        self.stats = dict(borrowed=0, fallback=0, failed_alloc=0, peak_leased=0)
+
+    def _held(self):
+        return sum(sl.capacity for sl in self._table)
+
+    def _find(self, size):
+        """An idle slot that already holds `size` bytes (the smallest such), else a slot to (re)grow
+        to the next power of two: a new one while the table has room, else the smallest idle one.
+        None when neither the table nor the budget allows it."""
+        idle = [sl for sl in self._table if not sl.leased]
+        fits = [sl for sl in idle if sl.capacity >= size]
+        if fits:
+            return min(fits, key=lambda sl: sl.capacity)
+        want = max(_SLOT_MIN, 1 << (max(size, 2) - 1).bit_length())
+        if self._held() + want > self.budget_bytes:
+            return None
+        try:
+            buf = torch.empty(want, dtype=torch.uint8, pin_memory=self.pinned)
+        except (RuntimeError, OSError, MemoryError):
+            self.stats["failed_alloc"] += 1
+            return None
+        if len(self._table) < self.slots:
+            self._table.append(_Slot(buf))
+            return self._table[-1]
+        if idle:
+            victim = min(idle, key=lambda sl: sl.capacity)
+            victim.buf = buf
+            return victim
+        return None
 
     def borrow(self, size):
-        """A writable uint8 buffer of `size` bytes tied to a slot, or None (fall back)."""
+        """A writable uint8 array of exactly `size` bytes leased from a slot, or None."""
         if type(size) is not int or size < 0:
-            raise ValueError("nonnegative receive frame size required")
+            raise ValueError(f"frame size must be a non-negative int, got {size!r}")
         if size == 0:
             return np.empty(0, dtype=np.uint8)
         with self._lock:
-            fits = [i for i, b in enumerate(self._bufs) if i not in self._busy and b.numel() >= size]
-            if fits:
-                index = min(fits, key=lambda i: self._bufs[i].numel())
-            else:
-                idle = [i for i in range(len(self._bufs)) if i not in self._busy]
-                index = min(idle, key=lambda i: self._bufs[i].numel()) if idle else len(self._bufs)
-                capacity = max(1024, 1 << max(size - 1, 1).bit_length())
-                held = sum(b.numel() for b in self._bufs)   # a resize briefly holds old and new
-                if index >= self.slots or held + capacity > self.budget_bytes:
-                    self.fallbacks += 1
-                    return None
-                try:
-                    buf = torch.empty(capacity, dtype=torch.uint8, device="cpu", pin_memory=self.pinned)
-                except (RuntimeError, OSError, MemoryError):
-                    self.fallbacks += 1
-                    self.allocation_failures += 1
-                    return None
-                if index < len(self._bufs):
-                    self._bufs[index] = buf
-                else:
-                    self._bufs.append(buf)
-            self._busy.add(index)
-            self.hits += 1
-            self.high_water = max(self.high_water, len(self._busy))
-            # The ctypes array exports the slot's memory; every numpy array / tensor decoded from
-            # it keeps it alive, and the slot is released when it is collected.
-            exporter = (ctypes.c_uint8 * size).from_address(self._bufs[index].data_ptr())
-            weakref.finalize(exporter, self._release, index)
-            return np.frombuffer(exporter, dtype=np.uint8)
+            sl = self._find(size)
+            if sl is None:
+                self.stats["fallback"] += 1
+                return None
+            sl.leased = True
+            self.stats["borrowed"] += 1
+            self.stats["peak_leased"] = max(self.stats["peak_leased"], self.n_leased())
+            # a ctypes array owns the lease: every numpy array and tensor decoded from the slot keeps it
+            # alive, and collecting it (reference counting alone, no cyclic GC) ends the lease
+            owner = (ctypes.c_uint8 * size).from_address(sl.buf.data_ptr())
+            weakref.finalize(owner, self._end_lease, sl)
+            return np.frombuffer(owner, dtype=np.uint8)
 
-    def _release(self, index):
+    def _end_lease(self, sl):
         with self._lock:
-            self._busy.discard(index)
+            sl.leased = False
+
+    def n_leased(self):
+        return sum(sl.leased for sl in self._table)
 
     def snapshot(self):
         with self._lock:
-            held = sum(b.numel() for b in self._bufs)
+            held = self._held()
+            st = self.stats
             return {"schema": "shard-receive-buffer-pool/1", "budget_bytes": self.budget_bytes,
-                    "allocated_bytes": held, "slots": self.slots, "live_slots": len(self._busy),
-                    "high_water_slots": self.high_water, "borrowed_frames": self.hits,
-                    "fallback_frames": self.fallbacks, "allocation_failures": self.allocation_failures,
-                    "pinned_allocated_bytes": held if self.pinned else 0, "pinned": self.pinned,
-                    "scope": "process lifetime; CPU receive copies only"}
+                    "allocated_bytes": held, "slots": self.slots, "live_slots": self.n_leased(),
+                    "high_water_slots": st["peak_leased"], "borrowed_frames": st["borrowed"],
+                    "fallback_frames": st["fallback"], "allocation_failures": st["failed_alloc"],
+                    "pinned_allocated_bytes": held * self.pinned, "pinned": self.pinned,
+                    "scope": "per process; host frames of recv_msg"}
 
 
 _POOL = None
@@ -248,21 +312,23 @@ _POOL_LOCK = threading.Lock()
 
 
 def configure_receive_pool(budget_bytes=0, *, slots=2, pinned=False):
-    """Process-wide opt-in to pooled receive buffers (0 turns it off); refused while a pooled
-    frame still has live tensors."""
+    """Turn pooled receive buffers on for this process (budget_bytes > 0) or off (0).  Refused while
+    tensors of a pooled frame are still alive.  Returns the new status."""
     global _POOL
-    if type(budget_bytes) is not int or budget_bytes < 0 or type(pinned) is not bool:
-        raise ValueError("explicit receive buffer budget/pinning required")
+    if type(budget_bytes) is not int or budget_bytes < 0:
+        raise ValueError(f"budget_bytes must be a non-negative int, got {budget_bytes!r}")
+    if type(pinned) is not bool:
+        raise ValueError(f"pinned must be True or False, got {pinned!r}")
     with _POOL_LOCK:
         if _POOL is not None and _POOL.snapshot()["live_slots"]:
-            raise RuntimeError("cannot replace a receive pool while tensor views are live")
+            raise RuntimeError("the receive pool still has leased slots: tensor views of pooled frames are live")
         _POOL = ReceiveBufferPool(budget_bytes, slots=slots, pinned=pinned) if budget_bytes else None
     return receive_pool_status()
 
 
 def receive_pool_status():
     pool = _POOL
-    return pool.snapshot() if pool is not None else {"enabled": False, "scope": "process lifetime"}
+    return pool.snapshot() if pool is not None else {"enabled": False, "scope": "per process"}
 
 
 # ---- sockets ---------------------------------------------------------------------------------------
@@ -276,16 +342,13 @@ def tune_socket(sock, buf_bytes=SOCK_BUF):
 
 
 def _recv_into(sock, view):
-    got, n = 0, len(view)
-    while got < n:
-        r = sock.recv_into(view[got:], n - got)
-        if not r:
-            try:
-                peer = sock.getpeername()
-            except (OSError, AttributeError):
-                peer = "unknown"
-            raise ConnectionError(f"peer {peer} closed the connection while reading a frame ({got}/{n} bytes)")
-        got += r
+    """Fill `view` from the socket; a peer that hangs up first is a ConnectionError."""
+    filled = 0
+    while filled < len(view):
+        r = sock.recv_into(view[filled:])
+        if r == 0:
+            raise ConnectionError(f"socket closed by the peer after {filled} of {len(view)} expected bytes")
+        filled += r
 
 
 def _recv_exact(sock, n):
@@ -460,10 +523,10 @@ def recv_activation(sock, device="cuda"):
     n = _read_length(sock)
     try:
         if n < 4:
-            raise ValueError("truncated frame header")
+            raise ValueError(f"header length field: 4 bytes declared, {n} remain in the frame")
         (hlen,) = struct.unpack("!I", _recv_exact(sock, 4))
         if hlen > n - 4:
-            raise ValueError("header length exceeds frame")
+            raise ValueError(f"JSON header: {hlen} bytes declared, {n - 4} remain in the frame")
         head = json.loads(bytes(_recv_exact(sock, hlen)))
         specs = {}
         _collect_specs(head, specs)
@@ -471,14 +534,14 @@ def recv_activation(sock, device="cuda"):
         with ring.lock:
             while left:
                 if left < 8:
-                    raise ValueError("truncated blob length")
+                    raise ValueError(f"length field of blob {index}: 8 bytes declared, {left} remain in the frame")
                 (blen,) = struct.unpack("!Q", _recv_exact(sock, 8))
                 left -= 8
                 if blen > left:
-                    raise ValueError("blob length exceeds frame")
+                    raise ValueError(f"blob {index}: {blen} bytes declared, {left} remain in the frame")
                 spec = specs.get(index)
                 if spec is not None and spec[2] != blen:
-                    raise ValueError(f"tensor {spec[1]} needs {spec[2]} bytes, blob has {blen}")
+                    raise ValueError(f"{spec[0]} tensor of shape {spec[1]} is {spec[2]} bytes; blob {index} holds {blen}")
                 dst = (torch.empty(blen, dtype=torch.uint8, device=device) if spec is not None else None)
                 for j, c0 in enumerate(range(0, blen, ring.chunk)):
                     s, c1 = j % k, min(blen, c0 + ring.chunk)
@@ -494,8 +557,9 @@ def recv_activation(sock, device="cuda"):
                 left -= blen
                 index += 1
             torch.cuda.current_stream(device).wait_stream(ring.stream)
-        if any(i >= index for i in specs):
-            raise ValueError("invalid tensor blob index")
+        missing = [i for i in specs if i >= index]
+        if missing:
+            raise ValueError(f"tensor node points at blob {missing[0]}, frame has {index}")
 
         def make(node):
             dt, shape, _, i = _tensor_spec(node)

@@ -296,6 +296,15 @@ int flyai_lm_head_argmax(const uint16_t* x, const int32_t* rows, int32_t n_rows,
                          const uint8_t* w_packed, int32_t V, int32_t* ids, uint16_t* logits_out,
                          void* workspace, flyai_stream_t stream);
 
+/* ---- measurement -------------------------------------------------------------------------------
+ * HBM read-streaming probe (no counterpart in the reference: it measures the bandwidth ceiling the
+ * weight-streaming kernels are held against).  Reads every byte of src once, 16 bytes per lane per
+ * load: `grid` workgroups of 256 take contiguous 32 KiB chunks round-robin, 8 loads in flight per
+ * thread; nontemporal selects nontemporal loads.  sink (device, 4 bytes) is written only in a 1-in-2^32 case.  bytes % 16
+ * == 0, src 16-byte aligned, grid in [1, 65536]. */
+int flyai_hbm_read_probe(const void* src, size_t bytes, int32_t nontemporal, int32_t grid, uint32_t* sink,
+                         flyai_stream_t stream);
+
 /* ---- a10: stage step driver ----------------------------------------------------------------------
  * The per-layer loop of FastVerify._layers / BatchedFastVerify._layers (phase0/fastverify.py:116-122,
  * phase0/batchverify.py:132-138) over GptOssDecoderLayer.forward (modeling_gpt_oss.py:347-376), for

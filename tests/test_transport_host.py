@@ -189,7 +189,7 @@ def test_pooled_frames_have_independent_storage_and_slots_are_reused():
 def test_reconfigure_refused_while_views_live():
     W.configure_receive_pool(8192)
     held = exchange({"h": torch.ones(32)})
-    with pytest.raises(RuntimeError, match="views are live"):
+    with pytest.raises(RuntimeError, match="views of pooled frames are live"):
         W.configure_receive_pool(0)
     del held
 

@@ -12,6 +12,24 @@ import torch
 
 
 class YarnRotary:
+    @classmethod
+    def from_inv_freq(cls, inv_freq, attention_scaling, n_positions, device="cuda"):
+        """The table of a rotary module that already holds its fp32 inv_freq and attention_scaling
+        (transformers' GptOssRotaryEmbedding): the same product, cos/sin, scaling and bf16 rounding."""
+        self = cls.__new__(cls)
+        self.inv_freq = inv_freq.detach().float().cpu()
+        self.attention_scaling = float(attention_scaling)
+        self.head_dim = 2 * self.inv_freq.numel()
+        self._tables(n_positions, device)
+        return self
+
+    def _tables(self, n_positions, device):
+        self.n_positions = n_positions
+        pos = torch.arange(n_positions, dtype=torch.float32)
+        freqs = (self.inv_freq[None, :, None] @ pos[None, None, :]).transpose(1, 2)[0]
+        self.cos = (freqs.cos() * self.attention_scaling).to(torch.bfloat16).contiguous().to(device)
+        self.sin = (freqs.sin() * self.attention_scaling).to(torch.bfloat16).contiguous().to(device)
+
     def __init__(self, n_positions, head_dim=64, base=150000.0, factor=32.0, beta_fast=32.0,
                  beta_slow=1.0, original_max=4096, truncate=False, device="cuda"):
         dim = head_dim
@@ -31,9 +49,5 @@ class YarnRotary:
         extra = 1 - ramp
         self.inv_freq = (1.0 / (factor * pos_freqs)) * (1 - extra) + (1.0 / pos_freqs) * extra
         self.attention_scaling = att
-        self.n_positions = n_positions
         self.head_dim = head_dim
-        pos = torch.arange(n_positions, dtype=torch.float32)
-        freqs = (self.inv_freq[None, :, None] @ pos[None, None, :]).transpose(1, 2)[0]
-        self.cos = (freqs.cos() * att).to(torch.bfloat16).contiguous().to(device)
-        self.sin = (freqs.sin() * att).to(torch.bfloat16).contiguous().to(device)
+        self._tables(n_positions, device)

@@ -18,7 +18,7 @@ import ctypes as C
 import numpy as np
 import torch
 
-from . import _lib, kvlayout, ops
+from . import _lib, kvlayout, ops, stage_parts
 from ._lib import ContextOverflow, check, lib
 from .weights import GptOssShape
 
@@ -235,22 +235,21 @@ def validate_tree(M, par, dep):
             raise ValueError(f"tree node {i}: depth {dep[i]} != {want} (parent {par[i]}; cycle or bad depth)")
 
 
-def _parts_shape(parts):
-    return parts.get("shape") or GptOssShape()
-
-
 class FastVerifyStage:
     """Drop-in for ``FastVerify(parts, maxlen, dev)`` (phase0/fastverify.py:80-309), B = 1.
 
-    ``parts`` keys read: ``layers`` (LayerWeights), ``rotary`` (YarnRotary), ``shape`` (GptOssShape);
-    ``sliding``/``window`` are carried by the layers and the shape.  ``decode`` returns a buffer the
-    runtime owns and reuses on the next call (as the graph output is in the reference)."""
+    ``parts`` is the reference's dict: either what ``flyai_amd.stage_parts.load_stage`` returns or the
+    reference's own (transformers modules, converted by ``stage_parts.parts_from_reference``).  Keys
+    read: ``layers``, ``rotary``, ``sliding`` (carried by each layer), ``_model.config`` or ``shape``.
+    ``decode`` returns a buffer the runtime owns and reuses on the next call (as the graph output is
+    in the reference)."""
 
     DECODE_BUCKETS = (2048, 4096, 8192, 16384, 32768, 65536, 131072)
 
     def __init__(self, parts, maxlen=2048, dev="cuda", max_tokens=4096):
+        parts = stage_parts.as_stage_parts(parts, dev)
         self.parts, self.maxlen, self.dev = parts, maxlen, dev
-        self.shape = _parts_shape(parts)
+        self.shape = stage_parts.stage_shape(parts)
         self.layers = parts["layers"]
         self.n_layers = len(self.layers)
         self.hidden = self.shape.hidden
@@ -314,8 +313,9 @@ class BatchedFastVerifyStage:
     DECODE_BUCKETS = FastVerifyStage.DECODE_BUCKETS
 
     def __init__(self, parts, B, maxlen=2048, dev="cuda", lossless=False, max_tokens=None):
+        parts = stage_parts.as_stage_parts(parts, dev)
         self.parts, self.B, self.maxlen, self.dev = parts, B, maxlen, dev
-        self.shape = _parts_shape(parts)
+        self.shape = stage_parts.stage_shape(parts)
         self.layers = parts["layers"]
         self.n_layers = len(self.layers)
         self.hidden = self.shape.hidden

@@ -67,6 +67,10 @@ _PROTOS = {
     "flyai_mxfp4_repack": (C.c_int, [P, P, I32, I32, I32, P, P]),
     "flyai_moe_gate_up_mxfp4": (C.c_int, [P, P, P, I32, I32, P, P, I32, I32, I32, P, P]),
     "flyai_moe_down_mxfp4": (C.c_int, [P, P, I32, P, P, I32, I32, I32, P, P]),
+    "flyai_mx_act_scale_bytes": (SZ, [I32, I32]),
+    "flyai_mx_act_quant": (C.c_int, [P, I32, I32, P, P, P]),
+    "flyai_moe_gate_up_mxfp4_fp8act": (C.c_int, [P, P, P, P, P, I32, I32, P, P, I32, I32, I32, P, P]),
+    "flyai_moe_down_mxfp4_fp8act": (C.c_int, [P, P, P, P, I32, P, P, I32, I32, I32, P, P]),
     "flyai_rmsnorm": (C.c_int, [P, P, I32, I32, F32, P, P]),
     "flyai_linear_workspace_bytes": (SZ, [I32, I32, I32]),
     "flyai_linear_bf16": (C.c_int, [P, P, P, I32, I32, I32, P, P, P, P]),

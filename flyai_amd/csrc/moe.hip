@@ -582,6 +582,307 @@ __global__ __launch_bounds__(512) void moe_mxfp4_gemm_kernel(
   }
 }
 
+// ---- dense groups on the scaled MFMA: fp8 activations x MXFP4 weights -------------------------------
+// v_mfma_scale_f32_16x16x128_f8f6f4 takes A = 16 activation rows x 128 K as fp8 e4m3 and B = 128 K x 16
+// weight rows as fp4 e2m1.  Measured on gfx950 (one-hot operands): an fp4 B lane (r, g) holds the 32
+// K values 32g .. 32g+31 of its row r; an fp8 A lane (r, g) holds K 16g .. 16g+15 in bytes 0..15 and
+// K 64+16g .. 64+16g+15 in bytes 16..31; and the E8M0 scale of 32-block b (K 32b .. 32b+31) is the
+// scale byte of lane group b, for A and B alike, whichever lanes hold the block's values.  The packed
+// MXFP4 tiles already hold exactly B's lane layout (lane 16g + r = row r, block 4kg + g of group kg,
+// 16 bytes) and the block scales of the format, so the weights go from the load straight into the
+// MFMA: no conversion and no scaling instruction.  The
+// activations are quantised once per row to fp8 with one power-of-two scale per 32 values
+// (mx_act_quant_kernel), whose scale bytes are stored in the same order as the weights': dword
+// (kg4, g) of a row holds the scales of blocks 4(4kg4 + i) + g in bytes i = 0..3, so lane (r, g)
+// finds the scale of its block of group kg in byte kg % 4 of one dword per 4 groups.  One MFMA covers
+// what four bf16 MFMAs and eight conversions covered, and the activation stages carry half the bytes.
+typedef int mx_v8i_t __attribute__((ext_vector_type(8)));
+
+// bytes of one row's activation scales: 16 per 4 groups of 128 K (blocks past K read 127 = 2^0)
+__host__ __device__ inline int mx_act_scale_row_bytes(int K) { return 16 * mx_geom(1, 16, K).KG4; }
+
+// One wave per (row, group of 128 K), two elements per lane, 16 lanes per 32-block: the block's amax
+// by xor shuffles, s = 2^ceil(log2(max(amax, 1e-4) / 448)), q = e4m3 RNE of clamp(x / s, +-448)
+// (v_cvt_pk_fp8_f32), scale byte e + 127.  Groups past K (up to 4 * KG4) only write scale bytes 127.
+__global__ __launch_bounds__(256) void mx_act_quant_kernel(const uint16_t* __restrict__ x, int M, int K,
+                                                           uint8_t* __restrict__ q, uint8_t* __restrict__ s) {
+  const MxGeom gm = mx_geom(1, 16, K);
+  const int KGP = 4 * gm.KG4;
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= M * KGP) return;  // uniform per wave
+  const int lane = threadIdx.x & 63;
+  const int row = item / KGP, kg = item % KGP, g = lane >> 4;
+  const int k0 = kg * 128 + 2 * lane;
+  const bool in = k0 < K;  // K % 32 == 0: a 32-block is wholly inside or wholly past the row
+  float x0 = 0.f, x1 = 0.f;
+  if (in) {
+    const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (size_t)row * K + k0);
+    x0 = bf2f(xv & 0xffff);
+    x1 = bf2f(xv >> 16);
+  }
+  float amax = fmaxf(fabsf(x0), fabsf(x1));
+#pragma unroll
+  for (int o = 8; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  amax = fmaxf(amax, 1e-4f);
+  // ceil(log2(amax / 448)) from the bits of amax * (1/448), a normal number since amax >= 1e-4
+  const uint32_t bits = __float_as_uint(amax * (1.0f / 448.0f));
+  const int e = (int)((bits >> 23) & 0xff) - 127 + ((bits & 0x7fffffu) ? 1 : 0);
+  if (in) {
+    const float y0 = fminf(fmaxf(ldexpf(x0, -e), -448.0f), 448.0f);
+    const float y1 = fminf(fmaxf(ldexpf(x1, -e), -448.0f), 448.0f);
+    const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
+    *reinterpret_cast<uint16_t*>(q + (size_t)row * K + k0) = (uint16_t)(packed & 0xffff);
+  }
+  if ((lane & 15) == 0)
+    s[(size_t)row * mx_act_scale_row_bytes(K) + ((kg >> 2) * 4 + g) * 4 + (kg & 3)] = in ? (uint8_t)(e + 127) : 127;
+}
+
+constexpr int kMxStage = 8 * 2048 + 8 * 256 + kGemmTiles * 256;  // activations, their scales, weight scales
+
+// what one workgroup of the scaled GEMM works on
+struct MxCtx {
+  const uint8_t* act;     // fp8 activation rows [*, K]
+  const uint8_t* ascale;  // their scale rows, mx_act_scale_row_bytes(K) each
+  const int32_t* perm;
+  const float* bias;
+  void* out;
+  const uint8_t* wbase;  // the expert's packed tiles, + lane * 16
+  const uint8_t* sbase;  // the expert's weight scale rows, + lane * 4
+  MxGeom gm;
+  size_t tile_bytes;
+  int as_row, k_top, N, K, e, nb0, nbn, row_lo, lane, wave, r, g;
+};
+
+// One pass over MT row tiles (16 * MT rows from m0) and every weight block of the chunk.  The pipeline
+// is the bf16 dense kernel's: per group of 128 K, each wave loads its 2 weight tiles into a 4-deep
+// register ring and DMAs its share of the activation fragments, their scale dwords and its tiles'
+// scale dwords into one of 4 LDS stages, 3 groups ahead; a stage is waited for with an explicit vmcnt
+// that leaves the 2 younger groups in flight, then a bare s_barrier.  The activation stage holds, for
+// row tile m, two 1-KiB blocks (h = 0, 1): lane (g, r) at 16 * lane has bytes 64h + 16g .. +15 of the
+// group of row 16m + r (the A operand's lane layout above), so a lane's A operand is two contiguous,
+// conflict-free ds_read_b128.
+template <bool GATE_UP, int MT>
+__device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStage], char (&st1)[kMxStage],
+                                             char (&st2)[kMxStage], char (&st3)[kMxStage], int m0, int rows) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  static_assert(MT == 4 || MT == 8, "row tiles per pass");
+  constexpr int ASOFF = MT * 2048;             // activation scale dwords: MT x 256 B
+  constexpr int WSOFF = ASOFF + MT * 256;      // weight scale dwords: 16 tiles x 256 B
+  constexpr int AJ = MT / 4;                   // activation fragment blocks per wave per group
+  constexpr int LOADS = 2 + 2 + AJ + 1;        // weight tiles, weight scales, activations, their scales
+  constexpr int WAIT = (kGemmStages - 2) * LOADS;
+  const MxGeom& gm = c.gm;
+  const int lane = c.lane, wave = c.wave, r = c.r, g = c.g;
+  auto tile_of = [&](int nb, int n) __attribute__((always_inline)) {
+    return min((c.nb0 + nb) * kGemmTiles + 2 * wave + n, gm.NT - 1);
+  };
+  auto src_row = [&](int row) __attribute__((always_inline)) {
+    const int p = c.row_lo + m0 + (row < rows ? row : 0);  // rows past the pass read row 0, never stored
+    return GATE_UP ? c.perm[p] / c.k_top : p;
+  };
+  const int KGP = (gm.KG + kGemmStages - 1) / kGemmStages * kGemmStages;  // groups per block, padded
+  // DMA sources: fragment block b = J*8 + wave is row tile b/2, half b%2; scale block wave % MT
+  const uint8_t* arow[AJ];
+  int akl[AJ];  // the lane's K offset within a group, for the half its block holds
+#pragma unroll
+  for (int J = 0; J < AJ; ++J) {
+    const int b = J * 8 + wave;
+    akl[J] = 64 * (b & 1) + 16 * g;
+    arow[J] = c.act + (size_t)src_row((b >> 1) * 16 + r) * c.K + akl[J];
+  }
+  const uint8_t* asrow = c.ascale + (size_t)src_row((wave % MT) * 16 + r) * c.as_row + 4 * g;
+  int i_nb = 0, i_kg = 0;
+  auto issue = [&](u32x4 (&bq)[2], char* stage) __attribute__((always_inline)) {
+    const int nb = min(i_nb, c.nbn - 1), kg = i_kg;
+    const bool blk = 4 * kg + g < gm.G;  // the lane's block of the group exists
+    const size_t woff = blk ? (size_t)kg * 1024 : 0;
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+      bq[n] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(c.wbase + (size_t)tile_of(nb, n) * c.tile_bytes + woff));
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+      __builtin_amdgcn_global_load_lds((const void*)(c.sbase + ((size_t)tile_of(nb, n) * gm.KG4 + min(kg / 4, gm.KG4 - 1)) * 256),
+                                       (lds_ptr)(stage + WSOFF + (2 * wave + n) * 256), 4, 0, 0);
+    // lanes whose 16 K values lie past the row read its first group instead (finite, and paired with
+    // zeroed weights)
+#pragma unroll
+    for (int J = 0; J < AJ; ++J)
+      __builtin_amdgcn_global_load_lds((const void*)(arow[J] + (kg * 128 + akl[J] < c.K ? kg * 128 : 0)),
+                                       (lds_ptr)(stage + (J * 8 + wave) * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(asrow + min(kg / 4, gm.KG4 - 1) * 16),
+                                     (lds_ptr)(stage + ASOFF + (wave % MT) * 256), 4, 0, 0);
+    if (++i_kg == KGP) {
+      i_kg = 0;
+      ++i_nb;
+    }
+  };
+  f32x4_t acc[MT][2];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < MT; ++m)
+#pragma unroll
+      for (int n = 0; n < 2; ++n) acc[m][n] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  };
+  zero_acc();
+  u32x4 w0[2], w1[2], w2[2], w3[2];
+  // group kg from stage `cur` and weight slot `wq`: A fragments and scales from LDS, B straight from
+  // the ring (lanes past the row's last block zeroed), MT x 2 scaled MFMAs
+  auto compute = [&](const char* cur, const u32x4 (&wq)[2], int kg) __attribute__((always_inline)) {
+    const int sh = 8 * (kg & 3);
+    const bool bok = 4 * kg + g < gm.G;
+    int sw[2];
+    mx_v8i_t b[2];
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      sw[n] = (int)((*reinterpret_cast<const uint32_t*>(cur + WSOFF + (2 * wave + n) * 256 + lane * 4) >> sh) & 0xffu);
+      const u32x4 wv = bok ? wq[n] : u32x4{0u, 0u, 0u, 0u};
+      b[n] = mx_v8i_t{(int)wv.x, (int)wv.y, (int)wv.z, (int)wv.w, 0, 0, 0, 0};
+    }
+    // row tile m's operand is read while tile m-1's two MFMAs run (two operand sets live, not MT)
+    u32x4 lo[2], hi[2];
+    uint32_t sdw[2];
+    auto read_a = [&](auto m) __attribute__((always_inline)) {
+      constexpr int q = decltype(m)::value & 1;
+      lo[q] = *reinterpret_cast<const u32x4*>(cur + (2 * m) * 1024 + lane * 16);
+      hi[q] = *reinterpret_cast<const u32x4*>(cur + (2 * m + 1) * 1024 + lane * 16);
+      sdw[q] = *reinterpret_cast<const uint32_t*>(cur + ASOFF + m * 256 + lane * 4);
+    };
+    read_a(std::integral_constant<int, 0>{});
+    mx_static_for<0, MT>([&](auto m) {
+      constexpr int q = decltype(m)::value & 1;
+      if constexpr (decltype(m)::value + 1 < MT) read_a(std::integral_constant<int, decltype(m)::value + 1>{});
+      const int sa = (int)((sdw[q] >> sh) & 0xffu);
+      const mx_v8i_t a = mx_v8i_t{(int)lo[q].x, (int)lo[q].y, (int)lo[q].z, (int)lo[q].w,
+                                  (int)hi[q].x, (int)hi[q].y, (int)hi[q].z, (int)hi[q].w};
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+        acc[m][n] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b[n], acc[m][n], 0, 4, 0, sa, 0, sw[n]);
+    });
+    // the order above, kept by the scheduler: weight scales and tile 0's reads, then per tile the next
+    // tile's 3 reads and this tile's 2 MFMAs
+    __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 5, 0);
+    mx_static_for<0, MT - 1>([&](auto) {
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 3, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+    });
+    __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  float bsum[2];
+  auto load_bias = [&](int nb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) bsum[n] = c.bias[(size_t)c.e * c.N + tile_of(min(nb, c.nbn - 1), n) * 16 + r];
+  };
+  // acc[m][n][v] = D[group row 16m + 4g + v][feature (block tile 2*wave + n) * 16 + r]
+  auto epilogue = [&](int nb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int n = 0; n < 2; ++n) {
+      const int tile = (c.nb0 + nb) * kGemmTiles + 2 * wave + n;
+      const bool nval = tile < gm.NT;
+      const int feat = tile * 16 + r;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int orow = 16 * m + 4 * g + v;
+          const float val = acc[m][n][v] + bsum[n];
+          if (GATE_UP) {
+            const float partner = lane_xor1(val);
+            if (nval && (r & 1) == 0 && orow < rows)
+              reinterpret_cast<uint16_t*>(c.out)[(size_t)(c.row_lo + m0 + orow) * (c.N / 2) + feat / 2] =
+                  f2bf(swiglu_gptoss(val, partner));
+          } else {
+            if (nval && orow < rows)
+              reinterpret_cast<float*>(c.out)[(size_t)(c.row_lo + m0 + orow) * c.N + feat] = val;
+          }
+        }
+      }
+    }
+  };
+  auto group = [&](char* cur, u32x4 (&wq)[2], int kg) __attribute__((always_inline)) {
+    compute(cur, wq, kg);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(WAIT));  // this wave's loads of the next group are done
+    lds_barrier();  // every wave's part of the next stage is in LDS; every wave is done with `cur`
+    issue(wq, cur);  // refill `cur` and the weight slot 4 groups ahead
+  };
+
+  lds_barrier();  // every wave is done with the previous pass's stages
+  load_bias(0);
+  // the stage waits count loads per group in issue order: no load may move across a group
+  asm volatile("" ::: "memory");
+  issue(w0, st0);
+  asm volatile("" ::: "memory");
+  issue(w1, st1);
+  asm volatile("" ::: "memory");
+  issue(w2, st2);
+  asm volatile("" ::: "memory");
+  issue(w3, st3);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm((kGemmStages - 1) * LOADS));
+  lds_barrier();  // stage 0 is in LDS
+  for (int nb = 0; nb < c.nbn; ++nb) {
+    for (int kg = 0; kg < KGP; kg += kGemmStages) {
+      group(st0, w0, kg);
+      group(st1, w1, kg + 1);
+      group(st2, w2, kg + 2);
+      group(st3, w3, kg + 3);
+    }
+    epilogue(nb);
+    load_bias(nb + 1);
+    zero_acc();
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the loads past the chunk's end have landed
+}
+
+template <bool GATE_UP>
+__global__ __launch_bounds__(512) void moe_mx_gemm_kernel(
+    const uint8_t* __restrict__ act, const uint8_t* __restrict__ ascale, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ offsets, int k_top, const uint8_t* __restrict__ packed,
+    const float* __restrict__ bias, int E, int N, int K, int min_rows, int chunk, void* __restrict__ out) {
+  __shared__ __align__(16) char st0[kMxStage];
+  __shared__ __align__(16) char st1[kMxStage];
+  __shared__ __align__(16) char st2[kMxStage];
+  __shared__ __align__(16) char st3[kMxStage];
+  MxCtx c;
+  c.gm = mx_geom(E, N, K);
+  const int blocks_per_e = (c.gm.NT + kGemmTiles - 1) / kGemmTiles;
+  const int chunks_per_e = (blocks_per_e + chunk - 1) / chunk;
+  // consecutive work units on one XCD (workgroups are dealt to the 8 XCDs round-robin)
+  const int per_xcd = (int)(gridDim.x / 8);
+  const int unit = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (unit >= E * chunks_per_e) return;
+  c.e = unit / chunks_per_e;
+  c.nb0 = (unit % chunks_per_e) * chunk;
+  c.nbn = min(chunk, blocks_per_e - c.nb0);
+  c.row_lo = offsets[c.e];
+  const int n_e = offsets[c.e + 1] - c.row_lo;
+  if (n_e <= 0 || n_e < min_rows) return;  // uniform over the workgroup
+  c.act = act;
+  c.ascale = ascale;
+  c.perm = perm;
+  c.bias = bias;
+  c.out = out;
+  c.k_top = k_top;
+  c.N = N;
+  c.K = K;
+  c.as_row = mx_act_scale_row_bytes(K);
+  const int tid = threadIdx.x;
+  c.lane = tid & 63;
+  c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  c.r = c.lane & 15;
+  c.g = c.lane >> 4;
+  c.tile_bytes = (size_t)c.gm.G * 256;
+  c.wbase = packed + (size_t)c.e * c.gm.NT * c.tile_bytes + c.lane * 16;
+  c.sbase = packed + c.gm.data_bytes + (size_t)c.e * c.gm.NT * c.gm.KG4 * 256 + c.lane * 4;
+  // passes of 128 rows; the last takes 64 when they suffice
+  for (int m0 = 0; m0 < n_e; m0 += 128) {
+    const int rows = min(128, n_e - m0);
+    if (rows > 64) mx_gemm_pass<GATE_UP, 8>(c, st0, st1, st2, st3, m0, rows);
+    else mx_gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, m0, rows);
+  }
+}
+
 // Chunk of weight blocks per workgroup: the largest chunk that still gives at least 3 rounds of
 // workgroups over the CUs, so that workgroups of unequal length (experts with different row
 // counts take different row tiles) balance, while each start-up is shared by several blocks.
@@ -657,6 +958,60 @@ int launch_moe_down(const uint16_t* h, const int32_t* offsets, const uint8_t* w2
   return FLYAI_OK;
 }
 
+int launch_mx_act_quant(const uint16_t* x, int M, int K, uint8_t* q, uint8_t* s, hipStream_t st) {
+  if (M == 0) return FLYAI_OK;
+  const int items = M * 4 * mx_geom(1, 16, K).KG4;
+  hipLaunchKernelGGL(mx_act_quant_kernel, dim3(ceil_div(items, 4)), dim3(256), 0, st, x, M, K, q, s);
+  return check_launch("mx_act_quant");
+}
+
+// The fp8-activation variants: groups the bf16 kernels would give the dense tiled GEMM take the
+// scaled-MFMA GEMM on the quantised rows instead; decode-sized groups keep the row-pass kernel on the
+// bf16 rows.
+int launch_moe_gate_up_fp8act(const uint16_t* x, const uint8_t* xq, const uint8_t* xs, const int32_t* perm,
+                              const int32_t* offsets, int k_top, const uint8_t* w13, const float* b13, int T,
+                              int E, int H, int I, uint16_t* h, hipStream_t s) {
+  const MxGeom gm = mx_geom(E, 2 * I, H);
+  const bool dense = use_dense(T * k_top, E) && H >= 128;
+  if (H <= 4064) {
+    const int wg_per_e = ceil_div(gm.NT, 4 * kNTWGateUp);
+    hipLaunchKernelGGL((moe_mxfp4_kernel<true, kNTWGateUp, kDepthGateUp>), dim3(E * wg_per_e), dim3(256),
+                       kRowsPerPass * mx_lds_row_bytes(H), s, x, perm, offsets, k_top, w13, b13, E,
+                       2 * I, H, 1, dense ? kDenseFrom : (1 << 30), (void*)h);
+    const int rc = check_launch("moe_gate_up_mxfp4");
+    if (rc) return rc;
+  }
+  if (dense || H > 4064) {
+    const int chunk = gemm_chunk(gm, E);
+    hipLaunchKernelGGL((moe_mx_gemm_kernel<true>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s, xq, xs, perm,
+                       offsets, k_top, w13, b13, E, 2 * I, H, H > 4064 ? 1 : kDenseFrom + 1, chunk, (void*)h);
+    return check_launch("moe_gate_up_mxfp4(scaled mfma)");
+  }
+  return FLYAI_OK;
+}
+
+int launch_moe_down_fp8act(const uint16_t* h, const uint8_t* hq, const uint8_t* hs, const int32_t* offsets,
+                           const uint8_t* w2, const float* b2, int rows_total, int E, int H, int I, float* y,
+                           hipStream_t s) {
+  const MxGeom gm = mx_geom(E, H, I);
+  const bool dense = use_dense(rows_total, E) && I >= 128;
+  if (I <= 4064) {
+    const int wg_per_e = ceil_div(gm.NT, 4 * kNTWDown);
+    hipLaunchKernelGGL((moe_mxfp4_kernel<false, kNTWDown, kDepthDown>), dim3(E * wg_per_e), dim3(256),
+                       kRowsPerPass * mx_lds_row_bytes(I), s, h, nullptr, offsets, 1, w2, b2, E, H, I, 1,
+                       dense ? kDenseFrom : (1 << 30), (void*)y);
+    const int rc = check_launch("moe_down_mxfp4");
+    if (rc) return rc;
+  }
+  if (dense || I > 4064) {
+    const int chunk = gemm_chunk(gm, E);
+    hipLaunchKernelGGL((moe_mx_gemm_kernel<false>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s, hq, hs, nullptr,
+                       offsets, 1, w2, b2, E, H, I, I > 4064 ? 1 : kDenseFrom + 1, chunk, (void*)y);
+    return check_launch("moe_down_mxfp4(scaled mfma)");
+  }
+  return FLYAI_OK;
+}
+
 }  // namespace flyai
 
 using namespace flyai;
@@ -696,4 +1051,36 @@ extern "C" int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, i
                 "down: need I %% 32 == 0, H %% 16 == 0");
   FLYAI_REQUIRE(h && offsets && w2_packed && b2 && y_perm, "down: null pointer");
   return launch_moe_down(h, offsets, w2_packed, b2, rows, E, H, I, y_perm, as_stream(stream));
+}
+
+extern "C" size_t flyai_mx_act_scale_bytes(int32_t M, int32_t K) {
+  if (M < 0 || K <= 0 || K % 32) return 0;
+  return (size_t)M * mx_act_scale_row_bytes(K);
+}
+
+extern "C" int flyai_mx_act_quant(const uint16_t* x, int32_t M, int32_t K, uint8_t* q, uint8_t* s,
+                                  flyai_stream_t stream) {
+  FLYAI_REQUIRE(M >= 0 && K > 0 && K % 32 == 0, "mx_act_quant: need K %% 32 == 0");
+  FLYAI_REQUIRE(x && q && s, "mx_act_quant: null pointer");
+  return launch_mx_act_quant(x, M, K, q, s, as_stream(stream));
+}
+
+extern "C" int flyai_moe_gate_up_mxfp4_fp8act(const uint16_t* x, const uint8_t* xq, const uint8_t* xs,
+                                              const int32_t* perm, const int32_t* offsets, int32_t T, int32_t k,
+                                              const uint8_t* w13_packed, const float* b13, int32_t E, int32_t H,
+                                              int32_t I, uint16_t* h, flyai_stream_t stream) {
+  FLYAI_REQUIRE(T >= 0 && E > 0 && H > 0 && I > 0 && H % 32 == 0 && (2 * I) % 16 == 0 && k >= 1,
+                "gate_up: need H %% 32 == 0, 2I %% 16 == 0");
+  FLYAI_REQUIRE(x && xq && xs && perm && offsets && w13_packed && b13 && h, "gate_up: null pointer");
+  return launch_moe_gate_up_fp8act(x, xq, xs, perm, offsets, k, w13_packed, b13, T, E, H, I, h, as_stream(stream));
+}
+
+extern "C" int flyai_moe_down_mxfp4_fp8act(const uint16_t* h, const uint8_t* hq, const uint8_t* hs,
+                                           const int32_t* offsets, int32_t rows, const uint8_t* w2_packed,
+                                           const float* b2, int32_t E, int32_t H, int32_t I, float* y_perm,
+                                           flyai_stream_t stream) {
+  FLYAI_REQUIRE(rows >= 0 && E > 0 && H > 0 && I > 0 && I % 32 == 0 && H % 16 == 0,
+                "down: need I %% 32 == 0, H %% 16 == 0");
+  FLYAI_REQUIRE(h && hq && hs && offsets && w2_packed && b2 && y_perm, "down: null pointer");
+  return launch_moe_down_fp8act(h, hq, hs, offsets, w2_packed, b2, rows, E, H, I, y_perm, as_stream(stream));
 }

@@ -123,6 +123,32 @@ int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, int32_t rows
                          const uint8_t* w2_packed, const float* b2, int32_t E, int32_t H, int32_t I,
                          float* y_perm, flyai_stream_t stream);
 
+/* ---- a6, dense groups on the scaled MFMA (fp8 activations x MXFP4 weights) -----------------------
+ * The dense-group path of flyai_moe_gate_up_mxfp4 / flyai_moe_down_mxfp4 with the activation operand in
+ * fp8: groups the bf16 entry points give the dense tiled GEMM run v_mfma_scale_f32_16x16x128_f8f6f4 on
+ * fp8 e4m3 activations and the packed E2M1 weights, each with its E8M0 per-32 scales applied inside the
+ * MFMA (the reference's fp8-activation x fp4-weight GEMM, vendor/deepseek_v4_ref/inference/kernel.py:
+ * 441-449, with the activations on 32-blocks); decode-sized groups take the bf16 row-pass kernel on x
+ * (h) as before.  flyai_mx_act_quant quantises bf16 rows x [M, K] (K % 32 == 0): per row per 32-block
+ * s = 2^ceil(log2(max(amax, 1e-4) / 448)), q[M, K] = e4m3 RNE of clamp(x / s, -448, 448); the scale
+ * bytes s_e8m0 (flyai_mx_act_scale_bytes(M, K) bytes) are stored per row as 16 * ceil(ceil(K/128)/4)
+ * bytes in MFMA order: byte 4 * (4 * kg4 + g) + i holds the scale of block 4 * (4 * kg4 + i) + g, 127
+ * past K.  gate_up reads x (bf16) and xq/xs = flyai_mx_act_quant(x) for the same rows; down reads h and
+ * hq/hs = flyai_mx_act_quant(h).  Results differ from the bf16 path by the fp8 rounding of the dense
+ * groups' activations (per-32 relative error <= 2^-4), so a row's result depends on whether its expert's
+ * group is dense. */
+size_t flyai_mx_act_scale_bytes(int32_t M, int32_t K);
+int flyai_mx_act_quant(const uint16_t* x, int32_t M, int32_t K, uint8_t* q, uint8_t* s_e8m0,
+                       flyai_stream_t stream);
+int flyai_moe_gate_up_mxfp4_fp8act(const uint16_t* x, const uint8_t* xq, const uint8_t* xs,
+                                   const int32_t* perm, const int32_t* offsets, int32_t T, int32_t k,
+                                   const uint8_t* w13_packed, const float* b13, int32_t E, int32_t H,
+                                   int32_t I, uint16_t* h, flyai_stream_t stream);
+int flyai_moe_down_mxfp4_fp8act(const uint16_t* h, const uint8_t* hq, const uint8_t* hs,
+                                const int32_t* offsets, int32_t rows, const uint8_t* w2_packed,
+                                const float* b2, int32_t E, int32_t H, int32_t I, float* y_perm,
+                                flyai_stream_t stream);
+
 /* ---- a2 (DeepSeek-V3 shape): grouped sigmoid router ---------------------------------------------
  * Replaces KimiMoEGate.forward (vendor/kimi_k3_ref/modeling_kimi_linear.py:703-759) / the V4 Gate
  * (vendor/deepseek_v4_ref/inference/model.py:560-589) for score_func sigmoid with group limits.

@@ -108,16 +108,59 @@ def e4m3_round(v):
     return torch.as_tensor(np.asarray(v, dtype=np.float32)).to(torch.float8_e4m3fn).float().numpy()
 
 
-def act_quant_128(x):
-    """Per-row per-128 e4m3 quantisation with power-of-two scales (v4_kernels_cpu.py:89-104).
-    x fp32 [M, K] -> (q fp32 [M, K] holding e4m3 values, s fp32 [M, K/128])."""
+def act_quant_blocks(x, block):
+    """Per-row per-`block` e4m3 quantisation with power-of-two scales: the act_quant rule of
+    v4_kernels_cpu.py:89-104 (s = 2**ceil(log2(max(amax, 1e-4) / 448)), q = e4m3(clamp(x / s))) at any
+    block size dividing K.  x fp32 [M, K] -> (q fp32 [M, K] holding e4m3 values, s fp32 [M, K/block])."""
     x = np.asarray(x, dtype=np.float32)
     M, K = x.shape
-    z = x.reshape(M, K // 128, 128)
+    assert K % block == 0
+    z = x.reshape(M, K // block, block)
     amax = np.maximum(np.abs(z).max(axis=2, keepdims=True), np.float32(1e-4)).astype(np.float32)
     s = round_scale_pow2(amax, 1.0 / FP8_MAX)
     q = np.clip((z / s).astype(np.float32), -FP8_MAX, FP8_MAX)
-    return e4m3_round(q).reshape(M, K), s.reshape(M, K // 128)
+    return e4m3_round(q).reshape(M, K), s.reshape(M, K // block)
+
+
+def act_quant_128(x):
+    """Per-row per-128 e4m3 quantisation with power-of-two scales (v4_kernels_cpu.py:89-104).
+    x fp32 [M, K] -> (q fp32 [M, K] holding e4m3 values, s fp32 [M, K/128])."""
+    return act_quant_blocks(x, 128)
+
+
+def mx_fp8_roundtrip(x):
+    """x fp32 [M, K] (K % 32 == 0) -> the fp32 values an fp8 e4m3 activation operand with one E8M0
+    scale per 32 values carries: q * s from act_quant_blocks(x, 32) (exact in fp32)."""
+    q, s = act_quant_blocks(x, 32)
+    M, K = q.shape
+    return (q.reshape(M, K // 32, 32) * s[:, :, None]).reshape(M, K).astype(np.float32)
+
+
+def experts_mxfp4_fp8act(x, perm, offsets, k, wts: MxExpertWeights, return_h=False):
+    """experts_mxfp4 with both activation operands carried as fp8 e4m3 + per-32 E8M0 scales (the
+    dense groups' scaled-MFMA path): the gathered x rows and the bf16 intermediate h each pass through
+    mx_fp8_roundtrip before their product with the MXFP4 weights, the precedent being the
+    reference's fp8-activation x fp4-weight GEMM (vendor/deepseek_v4_ref/inference/kernel.py:441-449,
+    activations quantised per block on K with power-of-two scales).  Everything else as
+    experts_mxfp4: fp32 bias, SwiGLU, bf16 h, fp32 y."""
+    xq = torch.from_numpy(mx_fp8_roundtrip(np.asarray(torch.as_tensor(x).float())))
+    perm = np.asarray(perm, dtype=np.int64)
+    offsets = np.asarray(offsets, dtype=np.int64)
+    H = wts.b2.shape[1]
+    inter = wts.b13.shape[1] // 2
+    y = torch.zeros(perm.size, H, dtype=torch.float32)
+    hbuf = torch.zeros(perm.size, inter, dtype=torch.float32)
+    for e in range(wts.n_experts):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi == lo:
+            continue
+        w13, w2 = wts.dense(e)
+        gu = xq[torch.from_numpy(perm[lo:hi] // k)] @ w13.T + torch.from_numpy(wts.b13[e])[None, :]
+        h = bf16(swiglu(gu[:, 0::2], gu[:, 1::2]))
+        hbuf[lo:hi] = h
+        hq = torch.from_numpy(mx_fp8_roundtrip(h.numpy()))
+        y[lo:hi] = hq @ w2.T + torch.from_numpy(wts.b2[e])[None, :]
+    return (y, hbuf) if return_h else y
 
 
 def fp8_block_gemm(aq, sa, wq, sw):

@@ -455,3 +455,89 @@ def test_lm_head_logits_exact_on_small_integers():
     want = (h * norm_w) @ lm_w.T
     assert np.array_equal(got.numpy(), want)
     assert not np.array_equal(got.numpy(), (h * norm_w) @ lm_w[::-1].T)
+
+
+# ---- fp8 activation operands of the dense MXFP4 groups (per-32 E8M0 scales) -----------------------
+
+def _e4m3_grid():
+    """Every finite e4m3fn value with its code (sign, 4 exponent bits, 3 mantissa bits; bias 7;
+    exponent 0 subnormal; code 0x7f/0xff NaN), enumerated from the format's definition."""
+    vals = []
+    for code in range(256):
+        s, e, m = code >> 7, (code >> 3) & 15, code & 7
+        if e == 15 and m == 7:
+            continue
+        mag = (m / 8.0) * 2.0 ** -6 if e == 0 else (1 + m / 8.0) * 2.0 ** (e - 7)
+        vals.append(((-1) ** s * mag, code))
+    return vals
+
+
+def _e4m3_rne_brute(v, grid):
+    """Nearest grid value; a tie goes to the code with an even mantissa."""
+    best = min(abs(v - g) for g, _ in grid)
+    cands = [(g, c) for g, c in grid if abs(v - g) == best]
+    even = [g for g, c in cands if (c & 1) == 0]
+    return (even or [cands[0][0]])[0]
+
+
+def test_act_quant_blocks_brute_force():
+    import math
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((3, 96)).astype(np.float32) * np.array([1.0, 300.0, 1e-3], dtype=np.float32)[:, None]
+    x[1, 32:64] = 0.0                                     # an all-zero block: amax floor 1e-4
+    q, s = experts.act_quant_blocks(x, 32)
+    grid = _e4m3_grid()
+    for r in range(3):
+        for b in range(3):
+            blk = x[r, 32 * b:32 * (b + 1)].astype(np.float64)
+            amax = max(float(np.float32(np.abs(blk).max())), 1e-4)
+            a = float(np.float32(np.float32(amax) * np.float32(1.0 / 448.0)))
+            want_s = 2.0 ** math.ceil(math.log2(a))
+            assert s[r, b] == want_s, (r, b)
+            for i in range(32):
+                y = float(np.float32(np.float32(blk[i]) / np.float32(want_s)))
+                y = min(max(y, -448.0), 448.0)
+                assert q[r, 32 * b + i] == _e4m3_rne_brute(y, grid), (r, b, i)
+    assert np.abs(q).max() <= 448.0
+
+
+def test_mx_fp8_roundtrip_is_identity_on_the_grid_with_unit_scales():
+    grid = np.array(sorted({g for g, _ in _e4m3_grid()}), dtype=np.float32)
+    rng = np.random.default_rng(42)
+    x = rng.choice(grid, size=(4, 64)).astype(np.float32)
+    x[:, ::32] = 448.0 * np.where(rng.random((4, 2)) < 0.5, -1, 1)   # amax 448 in every block: s = 1
+    assert np.array_equal(experts.mx_fp8_roundtrip(x), x)
+    y = x * np.float32(2.0 ** -5)                                   # s = 2^-5, still exact
+    assert np.array_equal(experts.mx_fp8_roundtrip(y), y)
+
+
+def test_experts_fp8act_gate_up_exact_on_grid_inputs_and_down_recomputed():
+    """gate_up: inputs already on the fp8 grid with unit scales give exactly experts_mxfp4's h.
+    down: y is recomputed in fp64 from that h quantised by mx_fp8_roundtrip and the down weights
+    dequantised directly -- a dropped quantisation of h, or a bias on the wrong side, fails."""
+    E, H, I, k, T = 3, 64, 64, 2, 5
+    rng = np.random.default_rng(43)
+    grid = np.array(sorted({g for g, _ in _e4m3_grid()}), dtype=np.float32)
+    x = rng.choice(grid[np.abs(grid) <= 8], size=(T, H)).astype(np.float32)
+    x[:, ::32] = 448.0
+    w = experts.MxExpertWeights(rng.integers(0, 256, (E, 2 * I, H // 32, 16), dtype=np.uint8),
+                                rng.integers(118, 122, (E, 2 * I, H // 32), dtype=np.uint8),
+                                rng.standard_normal((E, 2 * I)).astype(np.float32),
+                                rng.integers(0, 256, (E, H, I // 32, 16), dtype=np.uint8),
+                                rng.integers(118, 122, (E, H, I // 32), dtype=np.uint8),
+                                rng.standard_normal((E, H)).astype(np.float32))
+    ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    ids.sort(axis=1)
+    _, offsets, perm, _ = routing.permute(ids, E)
+    y8, h8 = experts.experts_mxfp4_fp8act(torch.from_numpy(x), perm, offsets, k, w, return_h=True)
+    y16, h16 = experts.experts_mxfp4(torch.from_numpy(x), perm, offsets, k, w, return_h=True)
+    assert torch.equal(h8, h16)
+    assert not torch.equal(y8, y16)                                 # h itself is re-quantised
+    for e in range(E):
+        lo, hi = int(offsets[e]), int(offsets[e + 1])
+        if hi == lo:
+            continue
+        w2 = mxfp4.dequant(w.w2_blocks[e], w.w2_scales[e]).astype(np.float64)
+        hq = experts.mx_fp8_roundtrip(h16[lo:hi].numpy()).astype(np.float64)
+        want = hq @ w2.T + w.b2[e][None, :].astype(np.float64)
+        np.testing.assert_allclose(y8[lo:hi].numpy(), want, rtol=1e-5, atol=1e-4)

@@ -107,6 +107,9 @@ def main():
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     ap.add_argument("--workload", choices=("c1", "c2", "c3", "wire"), default="c1")
     ap.add_argument("--frames", type=int, default=20, help="--workload wire: frames per path")
+    ap.add_argument("--dense", choices=("fp8", "bf16"), default="fp8",
+                    help="--workload c2: dense expert groups on the scaled MFMA with fp8 activations (fp8) or "
+                         "on the bf16-activation tiled GEMM (bf16)")
     ap.add_argument("--graphs", action="store_true",
                     help="replay the stage step as a HIP graph (measured slower than direct launches "
                          "on this stack, so off by default)")
@@ -234,7 +237,9 @@ def run_gptoss(args, chunked_prefill=False):
     cpu_inputs = None
     if with_cpu:   # the oracle's copies of layers 0-1 and their KV, taken before any step writes
         cpu_inputs = cpu_layer_inputs(layers[:2], kv, hidden0, S)
-    stage = RaggedStage(shape, layers, rot, kv, max_tokens=max(64, T), max_seqs=S, use_graphs=args.graphs)
+    fp8 = chunked_prefill and args.dense == "fp8"
+    stage = RaggedStage(shape, layers, rot, kv, max_tokens=max(64, T), max_seqs=S, use_graphs=args.graphs,
+                        dense_fp8=fp8)
     slots = list(range(S))
     torch.cuda.synchronize()
     print("[bench] warmup", file=sys.stderr, flush=True)
@@ -258,20 +263,36 @@ def run_gptoss(args, chunked_prefill=False):
     lw = layers[1]
     xn = stage.debug_buffer(0, torch.bfloat16, (T, shape.hidden)).clone()
     resid = hidden0.clone()
+    I, H = shape.intermediate, shape.hidden
     ids, wts, hist, off, perm, inv = ops.moe_route_permute(xn, lw.router_w, lw.router_b, k)
-    hmoe = ops.moe_gate_up(xn, perm, off, k, lw.w13_packed, lw.b13, E, shape.intermediate)
-    y = ops.moe_down(hmoe, off, lw.w2_packed, lw.b2, E, shape.hidden)
+    hmoe = ops.moe_gate_up(xn, perm, off, k, lw.w13_packed, lw.b13, E, I)
     torch.cuda.synchronize()
     hist_np = hist.cpu().numpy()
     reps = args.kernel_reps
-    gu_us = hip_event_us(lambda: ops.moe_gate_up(xn, perm, off, k, lw.w13_packed, lw.b13, E, shape.intermediate),
-                         reps, warmup=10)
-    dn_us = hip_event_us(lambda: ops.moe_down(hmoe, off, lw.w2_packed, lw.b2, E, shape.hidden), reps, warmup=10)
+    if fp8:   # the dense groups' path in this stage: fp8 activation operands, scaled MFMA
+        xq, xs = ops.mx_act_quant(xn)
+        hq, hs = ops.mx_act_quant(hmoe)
+        gate_up = lambda: ops.moe_gate_up_fp8act(xn, xq, xs, perm, off, k, lw.w13_packed, lw.b13, E, I)
+        down = lambda: ops.moe_down_fp8act(hmoe, hq, hs, off, lw.w2_packed, lw.b2, E, H)
+        quant_us = hip_event_us(lambda: ops.mx_act_quant(xn), reps, warmup=5) + \
+            hip_event_us(lambda: ops.mx_act_quant(hmoe), reps, warmup=5)
+    else:
+        gate_up = lambda: ops.moe_gate_up(xn, perm, off, k, lw.w13_packed, lw.b13, E, I)
+        down = lambda: ops.moe_down(hmoe, off, lw.w2_packed, lw.b2, E, H)
+        quant_us = 0.0
+    gu_us = hip_event_us(gate_up, reps, warmup=10)
+    dn_us = hip_event_us(down, reps, warmup=10)
 
     def moe_block():
         i_, w_, _, o_, p_, v_ = ops.moe_route_permute(xn, lw.router_w, lw.router_b, k)
-        h_ = ops.moe_gate_up(xn, p_, o_, k, lw.w13_packed, lw.b13, E, shape.intermediate)
-        y_ = ops.moe_down(h_, o_, lw.w2_packed, lw.b2, E, shape.hidden)
+        if fp8:
+            xq_, xs_ = ops.mx_act_quant(xn)
+            h_ = ops.moe_gate_up_fp8act(xn, xq_, xs_, p_, o_, k, lw.w13_packed, lw.b13, E, I)
+            hq_, hs_ = ops.mx_act_quant(h_)
+            y_ = ops.moe_down_fp8act(h_, hq_, hs_, o_, lw.w2_packed, lw.b2, E, H)
+        else:
+            h_ = ops.moe_gate_up(xn, p_, o_, k, lw.w13_packed, lw.b13, E, I)
+            y_ = ops.moe_down(h_, o_, lw.w2_packed, lw.b2, E, H)
         ops.moe_combine(y_, v_, w_, residual=resid, out=resid)
 
     moe_us = hip_event_us(moe_block, args.moe_reps, warmup=20)
@@ -288,29 +309,36 @@ def run_gptoss(args, chunked_prefill=False):
     ceiling = hbm_read_ceiling(args.read_probe_mib, dev)
     copy_probe(args.copy_probe_mib, dev)
     step_launch = "hip graph replay" if args.graphs else "direct launches"
-    moe = {"us": round(moe_us, 2), "ops": "route+top-k/permute, gate_up, down, combine",
+    moe = {"us": round(moe_us, 2),
+           "ops": "route+top-k/permute, " + ("fp8 act quant x2, " if fp8 else "") + "gate_up, down, combine",
            "GB/s": round(moe_bytes / (moe_us * 1e-6) / 1e9, 1),
            "frac": round(moe_bytes / (moe_us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
            "algorithmic_bytes": moe_bytes, "experts_us": round(gu_us + dn_us, 2)}
+    if fp8:
+        moe["act_quant_us"] = round(quant_us, 2)
 
     if chunked_prefill:
         # dense groups (~65 rows per expert): the gate_up GEMM against the MFMA peak of its dtype
         P = T * k
         flops = 2.0 * P * shape.hidden * 2 * shape.intermediate
         tflops = flops / (gu_us * 1e-6) / 1e12
-        peak = MFMA_PEAK_TFLOPS["bf16"]
+        peak = MFMA_PEAK_TFLOPS["fp8" if fp8 else "bf16"]
+        dtype = ("mxfp4-e2m1 weights x fp8-e4m3 activations (E8M0 per-32 scales, scaled MFMA) in the dense "
+                 "expert groups, bf16 elsewhere; fp32 accumulate") if fp8 else "mxfp4-e2m1/bf16 (fp32 accumulate)"
+        kname = "moe_mx_gemm_kernel<gate_up> (scaled f8f6f4 MFMA)" if fp8 else "moe_mxfp4_gemm_kernel<gate_up>"
         line = {
             "metric": "stage tokens/sec at a chunked-prefill mixed batch; MoE layer us; % MFMA roofline",
             "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
-            "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4-e2m1/bf16 (fp32 accumulate)",
+            "scaling": "weak", "vs_baseline": None, "dtype": dtype,
             "data": "synthetic (seeded random-init weights, N(0,1) KV and activations)",
             "config": {"workload": "gpt-oss-120b-shaped 9-layer MXFP4 stage, one 2048-token prefill chunk "
                                    "(prior KV 4096) + 48 decode rows (KV 512-8192)",
                        "layers": args.layers, "tokens": T, "sequences": S, "experts": E,
-                       "top_k": k, "hidden": shape.hidden, "parallelism": "single GPU", "step_launch": step_launch},
+                       "top_k": k, "hidden": shape.hidden, "parallelism": "single GPU", "step_launch": step_launch,
+                       "dense_path": args.dense},
             "moe_layer_us": moe["us"], "moe_layer": moe,
-            "roofline": {"bound": "mfma", "kernel": "moe_mxfp4_gemm_kernel<gate_up>", "achieved": round(tflops, 1),
+            "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(tflops, 1),
                          "peak": peak, "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": None,
                          "algorithmic_flops": flops, "avg_us": round(gu_us, 2), "hbm_GB/s": round(gu_gbs, 1)},
             "kernels": {"moe_down": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),

@@ -35,7 +35,8 @@ class StageConfig(C.Structure):
     _fields_ = [(n, C.c_int32) for n in (
         "n_layers", "hidden", "n_q_heads", "n_kv_heads", "head_dim", "n_experts", "top_k",
         "intermediate", "window", "max_tokens", "max_seqs", "max_attn_items", "rope_positions",
-        "attn_split_keys")] + [("rms_eps", C.c_float), ("attn_prefill_min", C.c_int32)]
+        "attn_split_keys")] + [("rms_eps", C.c_float), ("attn_prefill_min", C.c_int32),
+                               ("moe_dense_fp8", C.c_int32)]
 
 
 class LayerDesc(C.Structure):

@@ -40,6 +40,12 @@ int launch_moe_gate_up(const uint16_t*, const int32_t*, const int32_t*, int, con
                        const float*, int, int, int, int, uint16_t*, hipStream_t);
 int launch_moe_down(const uint16_t*, const int32_t*, const uint8_t*, const float*, int, int, int, int,
                     float*, hipStream_t);
+int launch_mx_act_quant(const uint16_t*, int, int, uint8_t*, uint8_t*, hipStream_t);
+int launch_moe_gate_up_fp8act(const uint16_t*, const uint8_t*, const uint8_t*, const int32_t*, const int32_t*, int,
+                              const uint8_t*, const float*, int, int, int, int, uint16_t*, hipStream_t);
+int launch_moe_down_fp8act(const uint16_t*, const uint8_t*, const uint8_t*, const int32_t*, const uint8_t*,
+                           const float*, int, int, int, int, float*, hipStream_t);
+bool moe_batch_is_dense(int rows_total, int E, int K);
 int launch_rmsnorm(const uint16_t*, const float*, int, int, float, uint16_t*, hipStream_t);
 int launch_linear_residual_rmsnorm(const uint16_t*, const uint16_t*, const uint16_t*, int, int, int,
                                    uint16_t*, const float*, float, uint16_t*, float*, hipStream_t);
@@ -95,6 +101,7 @@ struct flyai_stage {
   size_t o_xn, o_gemm, o_qrot, o_attn, o_parts;
   size_t o_ids, o_w, o_logits, o_hist, o_off, o_perm, o_inv, o_hmoe, o_y;
   size_t o_h2;  // the post-attention residual stream of the decode-sized path
+  size_t o_xq, o_xs, o_hq, o_hs;  // fp8 activation operands of the dense groups (moe_dense_fp8)
   size_t o_hidden;  // stage-owned hidden rows the replayed graphs read and update
   size_t dev_bytes = 0;
   size_t host_half = 0;  // bytes of one pinned staging half (== blob_max)
@@ -165,6 +172,12 @@ static void layout(flyai_stage* st) {
   st->o_y = d.take(P * c.hidden * 4);
   st->o_h2 = d.take(T * c.hidden * 2);
   st->o_hidden = d.take(T * c.hidden * 2);
+  if (c.moe_dense_fp8) {
+    st->o_xq = d.take(T * c.hidden);
+    st->o_xs = d.take(flyai_mx_act_scale_bytes(c.max_tokens, c.hidden));
+    st->o_hq = d.take(P * c.intermediate);
+    st->o_hs = d.take(flyai_mx_act_scale_bytes((int32_t)P, c.intermediate));
+  }
   st->dev_bytes = d.off;
   st->host_half = st->blob_max;
 }
@@ -189,6 +202,7 @@ extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** o
   FLYAI_REQUIRE(c.max_attn_items > 0 && c.rope_positions > 0, "stage: bad capacities");
   FLYAI_REQUIRE(c.attn_split_keys >= 64 && c.attn_split_keys % 64 == 0, "stage: attn_split_keys % 64");
   FLYAI_REQUIRE(c.attn_prefill_min >= 0, "stage: attn_prefill_min must be >= 0");
+  FLYAI_REQUIRE(c.moe_dense_fp8 == 0 || c.moe_dense_fp8 == 1, "stage: moe_dense_fp8 must be 0 or 1");
   flyai_stage* st = new (std::nothrow) flyai_stage();
   if (!st) return set_error(FLYAI_EINVAL, "stage_create: out of host memory");
   st->cfg = c;
@@ -368,10 +382,24 @@ static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* count
                                F32(st->o_w), F32(st->o_logits), I32(st->o_hist), I32(st->o_off),
                                I32(st->o_perm), I32(st->o_inv), s));
     }
-    RUN(launch_moe_gate_up(B16(st->o_xn), I32(st->o_perm), I32(st->o_off), k, L.w13_packed, L.b13,
-                           Tn, E, H, I, B16(st->o_hmoe), s));
-    RUN(launch_moe_down(B16(st->o_hmoe), I32(st->o_off), L.w2_packed, L.b2, Tn * k, E, H, I,
-                        F32(st->o_y), s));
+    if (c.moe_dense_fp8 && moe_batch_is_dense(Tn * k, E, H < I ? H : I)) {
+      // dense groups on the scaled MFMA: the activation operands quantised to fp8 first
+      uint8_t* xq = reinterpret_cast<uint8_t*>(d + st->o_xq);
+      uint8_t* xs = reinterpret_cast<uint8_t*>(d + st->o_xs);
+      uint8_t* hq = reinterpret_cast<uint8_t*>(d + st->o_hq);
+      uint8_t* hs = reinterpret_cast<uint8_t*>(d + st->o_hs);
+      RUN(launch_mx_act_quant(B16(st->o_xn), Tn, H, xq, xs, s));
+      RUN(launch_moe_gate_up_fp8act(B16(st->o_xn), xq, xs, I32(st->o_perm), I32(st->o_off), k, L.w13_packed, L.b13,
+                                    Tn, E, H, I, B16(st->o_hmoe), s));
+      RUN(launch_mx_act_quant(B16(st->o_hmoe), Tn * k, I, hq, hs, s));
+      RUN(launch_moe_down_fp8act(B16(st->o_hmoe), hq, hs, I32(st->o_off), L.w2_packed, L.b2, Tn * k, E, H, I,
+                                 F32(st->o_y), s));
+    } else {
+      RUN(launch_moe_gate_up(B16(st->o_xn), I32(st->o_perm), I32(st->o_off), k, L.w13_packed, L.b13,
+                             Tn, E, H, I, B16(st->o_hmoe), s));
+      RUN(launch_moe_down(B16(st->o_hmoe), I32(st->o_off), L.w2_packed, L.b2, Tn * k, E, H, I,
+                          F32(st->o_y), s));
+    }
     const float* next_ln1 = (l + 1 < c.n_layers) ? st->layers[l + 1].ln1 : nullptr;
     // the fused path left the post-attention residual in o_h2; the other path updated hidden in place
     const uint16_t* resid = fused_route ? B16(st->o_h2) : hidden;

@@ -601,40 +601,53 @@ typedef int mx_v8i_t __attribute__((ext_vector_type(8)));
 // bytes of one row's activation scales: 16 per 4 groups of 128 K (blocks past K read 127 = 2^0)
 __host__ __device__ inline int mx_act_scale_row_bytes(int K) { return 16 * mx_geom(1, 16, K).KG4; }
 
-// One wave per (row, group of 128 K), two elements per lane, 16 lanes per 32-block: the block's amax
-// by xor shuffles, s = 2^ceil(log2(max(amax, 1e-4) / 448)), q = e4m3 RNE of clamp(x / s, +-448)
-// (v_cvt_pk_fp8_f32), scale byte e + 127.  Groups past K (up to 4 * KG4) only write scale bytes 127.
+// One wave per (row, 4 groups of 128 K): 8 elements per lane from one 16-byte load, 4 lanes per
+// 32-block; the block's amax by xor shuffles, s = 2^ceil(log2(max(amax, 1e-4) / 448)), q = e4m3 RNE of
+// clamp(x / s, +-448) (v_cvt_pk_fp8_f32), scale byte e + 127.  Blocks past K (up to 16 * KG4 per row)
+// only write their scale byte, 127.
 __global__ __launch_bounds__(256) void mx_act_quant_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                            uint8_t* __restrict__ q, uint8_t* __restrict__ s) {
   const MxGeom gm = mx_geom(1, 16, K);
-  const int KGP = 4 * gm.KG4;
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (item >= M * KGP) return;  // uniform per wave
+  if (item >= M * gm.KG4) return;  // uniform per wave
   const int lane = threadIdx.x & 63;
-  const int row = item / KGP, kg = item % KGP, g = lane >> 4;
-  const int k0 = kg * 128 + 2 * lane;
-  const bool in = k0 < K;  // K % 32 == 0: a 32-block is wholly inside or wholly past the row
-  float x0 = 0.f, x1 = 0.f;
-  if (in) {
-    const uint32_t xv = *reinterpret_cast<const uint32_t*>(x + (size_t)row * K + k0);
-    x0 = bf2f(xv & 0xffff);
-    x1 = bf2f(xv >> 16);
-  }
-  float amax = fmaxf(fabsf(x0), fabsf(x1));
+  const int row = item / gm.KG4, kg4 = item % gm.KG4;
+  const int k0 = kg4 * 512 + 8 * lane;
+  const bool in = k0 < K;  // K % 32 == 0: a 32-block (4 lanes) is wholly inside or wholly past the row
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 xv = in ? *reinterpret_cast<const u32x4*>(x + (size_t)row * K + k0) : u32x4{0u, 0u, 0u, 0u};
+  float v[8];
 #pragma unroll
-  for (int o = 8; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf2f(xv[i] & 0xffff);
+    v[2 * i + 1] = bf2f(xv[i] >> 16);
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
   amax = fmaxf(amax, 1e-4f);
   // ceil(log2(amax / 448)) from the bits of amax * (1/448), a normal number since amax >= 1e-4
   const uint32_t bits = __float_as_uint(amax * (1.0f / 448.0f));
   const int e = (int)((bits >> 23) & 0xff) - 127 + ((bits & 0x7fffffu) ? 1 : 0);
   if (in) {
-    const float y0 = fminf(fmaxf(ldexpf(x0, -e), -448.0f), 448.0f);
-    const float y1 = fminf(fmaxf(ldexpf(x1, -e), -448.0f), 448.0f);
-    const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(y0, y1, 0, false);
-    *reinterpret_cast<uint16_t*>(q + (size_t)row * K + k0) = (uint16_t)(packed & 0xffff);
+    uint32_t w[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      float y[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(ldexpf(v[4 * i + j], -e), -448.0f), 448.0f);
+      const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+      w[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], lo, true);
+    }
+    *reinterpret_cast<uint2*>(q + (size_t)row * K + k0) = make_uint2(w[0], w[1]);
   }
-  if ((lane & 15) == 0)
+  if ((lane & 3) == 0) {
+    const int blk = kg4 * 16 + lane / 4;  // block index within the row
+    const int kg = blk / 4, g = blk % 4;
     s[(size_t)row * mx_act_scale_row_bytes(K) + ((kg >> 2) * 4 + g) * 4 + (kg & 3)] = in ? (uint8_t)(e + 127) : 127;
+  }
 }
 
 constexpr int kMxStage = 8 * 2048 + 8 * 256 + kGemmTiles * 256;  // activations, their scales, weight scales
@@ -914,6 +927,9 @@ constexpr int kDenseFrom = 8;
 
 inline bool use_dense(int rows_total, int E) { return (int64_t)rows_total >= (int64_t)kDenseFrom * E; }
 
+// whether a batch of rows_total permuted rows gives any expert group to the dense kernels
+bool moe_batch_is_dense(int rows_total, int E, int K) { return use_dense(rows_total, E) && K >= 128; }
+
 int launch_moe_gate_up(const uint16_t* x, const int32_t* perm, const int32_t* offsets, int k_top,
                        const uint8_t* w13, const float* b13, int T, int E, int H, int I, uint16_t* h,
                        hipStream_t s) {
@@ -960,7 +976,7 @@ int launch_moe_down(const uint16_t* h, const int32_t* offsets, const uint8_t* w2
 
 int launch_mx_act_quant(const uint16_t* x, int M, int K, uint8_t* q, uint8_t* s, hipStream_t st) {
   if (M == 0) return FLYAI_OK;
-  const int items = M * 4 * mx_geom(1, 16, K).KG4;
+  const int items = M * mx_geom(1, 16, K).KG4;
   hipLaunchKernelGGL(mx_act_quant_kernel, dim3(ceil_div(items, 4)), dim3(256), 0, st, x, M, K, q, s);
   return check_launch("mx_act_quant");
 }

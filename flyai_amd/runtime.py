@@ -83,7 +83,11 @@ class RaggedStage:
     """One pipeline stage of GPT-OSS decoder layers on libflyai_stage."""
 
     def __init__(self, shape: GptOssShape, layers, rotary, kv: KVWorkspace, max_tokens, max_seqs,
-                 max_attn_items=None, split_keys=1024, device="cuda", use_graphs=False, prefill_min=32):
+                 max_attn_items=None, split_keys=1024, device="cuda", use_graphs=False, prefill_min=32,
+                 dense_fp8=False):
+        """dense_fp8: expert groups large enough for the dense kernels run on the scaled f8f6f4 MFMA with
+        fp8 activation operands (faster on prefill-sized batches, within the fp8 rounding of the
+        activations); the default keeps them on bf16 activations, bit-identical to the decode path."""
         self.shape, self.layers, self.rotary, self.kv = shape, layers, rotary, kv
         self.device = torch.device(device)
         self.max_tokens, self.max_seqs = max_tokens, max_seqs
@@ -96,7 +100,8 @@ class RaggedStage:
             top_k=shape.top_k, intermediate=shape.intermediate, window=shape.window,
             max_tokens=max_tokens, max_seqs=max_seqs, max_attn_items=max_attn_items,
             rope_positions=rotary.n_positions, attn_split_keys=split_keys, rms_eps=shape.rms_eps,
-            attn_prefill_min=prefill_min)
+            attn_prefill_min=prefill_min, moe_dense_fp8=int(bool(dense_fp8)))
+        self.dense_fp8 = bool(dense_fp8)
         handle = C.c_void_p()
         check(lib().flyai_stage_create(C.byref(cfg), C.byref(handle)))
         self._h = handle

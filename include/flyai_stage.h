@@ -342,6 +342,8 @@ typedef struct {
   int32_t max_tokens, max_seqs, max_attn_items, rope_positions, attn_split_keys;
   float rms_eps;
   int32_t attn_prefill_min;   /* sequences with q_len >= this take the prefill attention items (0: never) */
+  int32_t moe_dense_fp8;      /* 1: dense expert groups take the fp8-activation scaled-MFMA path
+                                 (flyai_moe_gate_up_mxfp4_fp8act); 0: the bf16 dense kernel */
 } flyai_stage_config;
 
 typedef struct {

@@ -32,7 +32,8 @@ def _batch(seed=4, S=256):
     return [int(v) for v in q], [int(v) for v in starts], [int(v) for v in prefill]
 
 
-def test_stress_batch_layers_vs_oracle():
+@pytest.mark.parametrize("dense_fp8", [False, True], ids=["bf16-dense", "fp8-dense"])
+def test_stress_batch_layers_vs_oracle(dense_fp8):
     from flyai_amd import ops
     from flyai_amd.rope import YarnRotary
     from flyai_amd.runtime import KVWorkspace, RaggedStage
@@ -72,7 +73,7 @@ def test_stress_batch_layers_vs_oracle():
     cos, sin = olayer.rope_table(MAXLEN + 64)
 
     for l, lw in enumerate(layers):
-        st = RaggedStage(shape, [lw], rot, _SingleLayerKV(kv, l), max_tokens=T, max_seqs=S)
+        st = RaggedStage(shape, [lw], rot, _SingleLayerKV(kv, l), max_tokens=T, max_seqs=S, dense_fp8=dense_fp8)
         hin = h
         h = st.forward(hin.clone(), q_lens, starts, list(range(S)))
         torch.cuda.synchronize()
@@ -95,5 +96,8 @@ def test_stress_batch_layers_vs_oracle():
         ref = olayer.decoder_layer(cpu_f32(hin)[rows], oracle_layer_params(lw, lw.sliding), (ks, vs),
                                    sub_q, sub_starts, cos, sin)
         mar, cos_ = metrics(cpu_f32(h)[rows].numpy(), ref.numpy())
-        assert mar <= MAR and cos_ >= COS, f"layer {l}: {mar:.3g} {cos_:.6f}"
+        # the opt-in fp8 dense path carries the fp8 rounding of the hot experts' activations
+        bar_mar, bar_cos = (0.08, 0.998) if dense_fp8 else (MAR, COS)
+        print(f"C4 {'fp8' if dense_fp8 else 'bf16'} dense, layer {l}: max-abs-rel {mar:.4g} cos {cos_:.6f}")
+        assert mar <= bar_mar and cos_ >= bar_cos, f"layer {l}: {mar:.3g} {cos_:.6f}"
         del st

@@ -89,6 +89,8 @@ _PROTOS = {
     "flyai_lm_head_workspace_bytes": (SZ, [I32, I32]),
     "flyai_lm_head_argmax": (C.c_int, [P, P, I32, I32, P, I32, P, P, P, P]),
     "flyai_hbm_read_probe": (C.c_int, [P, SZ, I32, I32, P, P]),
+    "flyai_sample_rows": (C.c_int, [P, I32, I32, F32, I32, F32, P, P, P, P, P, P]),
+    "flyai_sample_probs": (C.c_int, [P, I32, C.c_double, P, P]),
     "flyai_stage_create": (C.c_int, [P, P]),
     "flyai_stage_destroy": (None, [P]),
     "flyai_stage_set_layer": (C.c_int, [P, I32, P]),

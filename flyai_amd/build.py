@@ -10,7 +10,7 @@ CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "libflyai_stage.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
-SOURCES = ("capi.hip", "pack.hip", "route.hip", "moe.hip", "fp8.hip", "linear.hip", "attn.hip", "tail.hip", "probe.hip")
+SOURCES = ("capi.hip", "pack.hip", "route.hip", "moe.hip", "fp8.hip", "linear.hip", "attn.hip", "tail.hip", "probe.hip", "sample.hip")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]

@@ -461,3 +461,39 @@ def lm_head_argmax(x, w_packed, vocab, rows=None, want_logits=False, workspace=N
     check(lib().flyai_lm_head_argmax(_ptr(x), _ptr(rows), n, H, _ptr(w_packed), vocab, _ptr(ids),
                                      _ptr(logits), _ptr(workspace), _stream()))
     return (ids, logits) if want_logits else ids
+
+
+def sample_rows(logits, temp, top_k=0, top_p=1.0, draft=None, u=None, want_p_draft=False, want_draw=False,
+                want_probs=False):
+    """Temperature / top-k / top-p over bf16 logits rows [R, V] (one workgroup per row).  draft int32 [R]
+    (device, -1 = none) and u float64 [R] (device uniforms in [0, 1)) are optional; returns a dict with
+    the requested outputs: p_draft fp32 [R], draw int32 [R] (needs u unless temp <= 0), probs fp32 [R, V]."""
+    R, V = logits.shape
+    _need(logits, torch.bfloat16, (R, V), "logits")
+    if draft is not None:
+        _need(draft, torch.int32, (R,), "draft")
+    if u is not None:
+        _need(u, torch.float64, (R,), "u")
+    if want_draw and u is None and temp > 0:
+        raise ValueError("a sampled draw needs uniforms u")
+    dev = logits.device
+    out = {}
+    if want_p_draft:
+        out["p_draft"] = torch.empty(R, dtype=torch.float32, device=dev)
+    if want_draw:
+        out["draw"] = torch.empty(R, dtype=torch.int32, device=dev)
+    if want_probs:
+        out["probs"] = torch.empty(R, V, dtype=torch.float32, device=dev)
+    check(lib().flyai_sample_rows(_ptr(logits), R, V, float(temp), int(top_k), float(top_p), _ptr(draft), _ptr(u),
+                                  _ptr(out.get("p_draft")), _ptr(out.get("draw")), _ptr(out.get("probs")),
+                                  _stream()))
+    return out
+
+
+def sample_probs(probs, u):
+    """One draw from a fp32 probability vector [V] (device) at uniform u in [0, 1): int32 [1] on device."""
+    V = probs.numel()
+    _need(probs, torch.float32, (V,), "probs")
+    out = torch.empty(1, dtype=torch.int32, device=probs.device)
+    check(lib().flyai_sample_probs(_ptr(probs), V, float(u), _ptr(out), _stream()))
+    return out

@@ -331,6 +331,24 @@ int flyai_lm_head_argmax(const uint16_t* x, const int32_t* rows, int32_t n_rows,
 int flyai_hbm_read_probe(const void* src, size_t bytes, int32_t nontemporal, int32_t grid, uint32_t* sink,
                          flyai_stream_t stream);
 
+/* ---- token sampling (the tail's Sampler: phase0/specsample.py:36-107) -------------------------------
+ * Per logits row x[V] (bf16, R rows, one workgroup each): z = x / max(temp, 1e-6) in fp32; top-k
+ * (0 < top_k < V) keeps z >= the k-th largest z; weights w = floor(2^40 e^(z - max z)) as exact integers
+ * (a fixed fp64 exp); top-p (0 < top_p < 1) keeps, in (z desc, id asc) order, each token whose preceding
+ * weight is <= floor(top_p * W); the distribution is w / W over what is kept.  Outputs (each nullable):
+ * p_draft[r] = the kept probability of token draft[r] (draft nullable; -1 = none); probs [R, V] fp32 the
+ * distribution; draw[r] = the first id (ascending) whose inclusive prefix of w exceeds floor(u[r] * W'')
+ * where w has the drafted token removed (the speculative-sampling residual) -- the first id of maximal w
+ * when nothing is left; a sampled draw needs u (fp64 in [0, 1)).  temp <= 0 is greedy: draw is the first
+ * id of maximal x (u unused) and p_draft is 1 for that id, else 0.  Logits must be finite.  Sums are
+ * integer, so results do not depend on the launch. */
+int flyai_sample_rows(const uint16_t* logits, int32_t R, int32_t V, float temp, int32_t top_k, float top_p,
+                      const int32_t* draft, const double* u, float* p_draft, int32_t* draw, float* probs,
+                      flyai_stream_t stream);
+/* A draw from a probability vector p[V] (fp32, device; Sampler.sample): weights floor(p * 2^40), then the
+ * same inverse-CDF rule with uniform u in [0, 1); out (device int32) gets the id (0 when all are 0). */
+int flyai_sample_probs(const float* probs, int32_t V, double u, int32_t* out, flyai_stream_t stream);
+
 /* ---- a10: stage step driver ----------------------------------------------------------------------
  * The per-layer loop of FastVerify._layers / BatchedFastVerify._layers (phase0/fastverify.py:116-122,
  * phase0/batchverify.py:132-138) over GptOssDecoderLayer.forward (modeling_gpt_oss.py:347-376), for

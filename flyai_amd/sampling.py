@@ -58,6 +58,15 @@ class Sampler:
         u = None if self.greedy else torch.tensor([self.uniform()], dtype=torch.float64, device=self.device)
         return int(ops.sample_rows(x, self.temp, self.top_k, self.top_p, u=u, want_draw=True)["draw"].item())
 
+    def sample_logits_rows(self, logits):
+        """``sample_logits`` of every row of logits [n, V] in one launch, consuming one uniform per row in
+        row order (the same tokens as n calls of ``sample_logits``)."""
+        x = self._rows(logits)
+        if self.greedy:
+            return ops.sample_rows(x, 0.0, want_draw=True)["draw"].tolist()
+        u = torch.tensor([self.uniform() for _ in range(x.shape[0])], dtype=torch.float64, device=self.device)
+        return ops.sample_rows(x, self.temp, self.top_k, self.top_p, u=u, want_draw=True)["draw"].tolist()
+
     def _draw_row(self, x, exclude):
         d = torch.tensor([exclude], dtype=torch.int32, device=self.device)
         u = torch.tensor([self.uniform()], dtype=torch.float64, device=self.device)
@@ -88,3 +97,21 @@ class Sampler:
             return r
         r[K] = self._draw_row(x[K:K + 1], -1)
         return r
+
+
+def tail_tokens(parts, h, sampler, prefill=False, draft=None):
+    """The tail's reply for one verify message (``phase0/specpipe.py:790-803``): h [1, n, H] is the last
+    stage's output rows, ``parts`` holds ``norm`` and ``lm_head`` callables.  Prefill -> [one token from
+    the last row]; no draft -> one token per row (greedy: the fused lm_head argmax when the head has one,
+    so no logits are written); a draft of n - 1 ids -> ``sampler.accept`` over the n logits rows."""
+    if prefill:
+        h = h[:, -1:]
+    x = parts["norm"](h)
+    head = parts["lm_head"]
+    if prefill:
+        return [sampler.sample_logits(head(x)[0, -1])]
+    if draft is None:
+        if sampler.greedy and hasattr(head, "argmax"):
+            return head.argmax(x)[0].tolist()
+        return sampler.sample_logits_rows(head(x)[0])
+    return sampler.accept(head(x)[0], list(draft))

@@ -128,3 +128,36 @@ def test_sampler_api():
         sm.accept(_logits(2, 5000, seed=1).to(DEV), [1, 2])           # K=2 needs 3 rows
     with pytest.raises(TypeError):
         sm.dist(x.float().to(DEV))
+
+
+def test_tail_tokens_over_the_lm_head():
+    """tail_tokens on the stage parts (final norm + lm_head over the 201088-token vocabulary): greedy
+    replies are bit-identical to the fused lm_head argmax; sampled replies (prefill, per-row, accept over
+    K+1 rows) equal the oracle's for the same uniforms over the same bf16 logits."""
+    from flyai_amd.sampling import Sampler, tail_tokens
+    from flyai_amd.stage_parts import FinalNorm, LmHead
+    H = 2880
+    g = torch.Generator(device="cpu")
+    g.manual_seed(21)
+    parts = {"norm": FinalNorm((1 + 0.1 * torch.randn(H, generator=g)).to(DEV)),
+             "lm_head": LmHead((torch.randn(V_GPTOSS, H, generator=g) * 0.03).to(torch.bfloat16).to(DEV))}
+    h = (torch.randn(1, 5, H, generator=g) * 2).to(torch.bfloat16).to(DEV)
+    logits = parts["lm_head"](parts["norm"](h))[0].float().cpu().numpy()
+    greedy = Sampler(device=DEV)
+    want = [S.greedy(r) for r in logits]
+    assert tail_tokens(parts, h, greedy) == want
+    assert tail_tokens(parts, h, greedy, draft=[want[0], 3, want[2], 4]) == want
+    assert tail_tokens(parts, h, greedy, prefill=True) == [want[-1]]
+    temp, top_k, top_p, seed = 0.9, 0, 0.95, 77
+    ws = [S.weights(r, temp, top_k, top_p) for r in logits]
+
+    def uni():
+        u = np.random.Generator(np.random.PCG64(seed))
+        return iter(lambda: float(u.random()), None)
+    sm = lambda: Sampler(temp=temp, top_p=top_p, top_k=top_k, seed=seed, device=DEV)  # noqa: E731
+    u = uni()
+    assert tail_tokens(parts, h, sm(), prefill=True) == [S.draw(ws[-1], next(u))]
+    u = uni()
+    assert tail_tokens(parts, h, sm()) == [S.draw(w, next(u)) for w in ws]
+    draft = [int(np.argmax(ws[0])), int(np.argmax(ws[1])), 5, 6]
+    assert tail_tokens(parts, h, sm(), draft=draft) == S.accept(list(logits), draft, temp, top_k, top_p, uni())

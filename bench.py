@@ -177,6 +177,26 @@ def hbm_read_ceiling(mib, dev, reps=20, grid_per_cu=None):
     return out
 
 
+def committed_traffic(profile, kernels):
+    """HBM bytes of one launch of each named kernel (FETCH_SIZE + WRITE_SIZE per dispatch, calibrated
+    against a plain copy: flyai_amd.profiling), summed, from a counters profile committed under
+    profiles/; None when the profile or a kernel is missing.  A kernel name matches by prefix; of
+    several launch shapes of it, the one with the most dispatches is taken."""
+    path = os.path.join(ROOT, "profiles", profile)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        ents = json.load(f)
+    total = 0
+    for name in kernels:
+        hits = [e for e in ents if e["kernel"].startswith(name) and "FETCH_SIZE_bytes" in e]
+        if not hits:
+            return None
+        e = max(hits, key=lambda x: x.get("calls") or 0)
+        total += e["FETCH_SIZE_bytes"] + e.get("WRITE_SIZE_bytes", 0.0)
+    return int(round(total))
+
+
 def cpu_threads():
     """Intra-op threads for the CPU oracle: every CPU this process may run on (its affinity mask,
     which is the box's CPU share), unless OMP_NUM_THREADS narrows it."""
@@ -301,11 +321,12 @@ def run_gptoss(args, chunked_prefill=False):
     moe_bytes = moe_layer_algorithmic_bytes(shape, hist_np, T, k)
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
     dn_gbs = dn_bytes / (dn_us * 1e-6) / 1e9
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "moe_gate_up_c1_traffic.json")
-    if os.path.exists(tpath) and not chunked_prefill:
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    if chunked_prefill:
+        traffic = committed_traffic("stage_step_c2_fp8_counters.json" if fp8 else "stage_step_c2_counters.json",
+                                    ("moe_mx_gemm_kernel<true>", "moe_mxfp4_kernel<true") if fp8 else
+                                    ("moe_mxfp4_gemm_kernel<true>", "moe_mxfp4_kernel<true"))
+    else:
+        traffic = committed_traffic("stage_step_c1_counters.json", ("moe_mxfp4_kernel<true",))
     ceiling = hbm_read_ceiling(args.read_probe_mib, dev)
     copy_probe(args.copy_probe_mib, dev)
     step_launch = "hip graph replay" if args.graphs else "direct launches"
@@ -339,7 +360,7 @@ def run_gptoss(args, chunked_prefill=False):
                        "dense_path": args.dense},
             "moe_layer_us": moe["us"], "moe_layer": moe,
             "roofline": {"bound": "mfma", "kernel": kname, "achieved": round(tflops, 1),
-                         "peak": peak, "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": None,
+                         "peak": peak, "unit": "TFLOP/s", "frac": round(tflops / peak, 4), "traffic": traffic,
                          "algorithmic_flops": flops, "avg_us": round(gu_us, 2), "hbm_GB/s": round(gu_gbs, 1)},
             "kernels": {"moe_down": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),
                                      "TFLOP/s": round(flops / 2 / (dn_us * 1e-6) / 1e12, 1)}},
@@ -503,8 +524,10 @@ def run_c3(args):
                       "experts_us": round(gu_us + dn_us, 2)},
         "roofline": {"bound": "hbm", "kernel": "moe_fp8_kernel<gate_up> (tail + dense launches)",
                      "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None, "algorithmic_bytes": gu_bytes,
-                     "avg_us": round(gu_us, 2), "groups_touched": groups},
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": committed_traffic("stage_step_c3_counters.json",
+                                                  ("moe_fp8_kernel<true, 1", "moe_fp8_kernel<true, 8")),
+                     "algorithmic_bytes": gu_bytes, "avg_us": round(gu_us, 2), "groups_touched": groups},
         "kernels": {"moe_down_fp8": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),
                                      "frac": round(dn_gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": dn_bytes}},
         "hbm_read_ceiling": ceiling,

@@ -9,7 +9,15 @@ Two reports, both plain text for committing beside the numbers they support:
   ``WRITE_SIZE``, KiB per dispatch).  Each reading is scaled by the reading of a plain device copy
   of known size in the same run (``bench.py --copy-probe-mib M``): factor = M MiB / copy reading.
 
-Usage (after the rocprofv3 runs, on any machine)::
+* ``collect``: runs the kernel trace and the counter passes (PMC_PASSES) of one ``bench.py``
+  workload under rocprofv3, as child processes, and writes both reports for it;
+* ``counters``: per (kernel, grid size) the mean of every counter of one or more ``--pmc`` runs
+  (HBM bytes through the same copy calibration, unit busy/stall cycles as a fraction of the CUs'
+  cycles, MFMA ops as TFLOP/s) beside the mean duration from a ``--kernel-trace`` run.
+
+Usage::
+
+    python -m flyai_amd.profiling collect --name c2 OUT -- --workload c2     (on the GPU machine)
 
     python -m flyai_amd.profiling stats DIR --kernel moe_mxfp4_kernel<true --reps 50 --command "..."
     python -m flyai_amd.profiling traffic FETCH_DIR WRITE_DIR --kernel moe_mxfp4_kernel<true \\
@@ -104,6 +112,177 @@ def traffic(fetch_dir, write_dir, kernel, reps, copy_mib):
     return res
 
 
+def _grid(r):
+    if r.get("Grid_Size"):
+        return int(float(r["Grid_Size"]))
+    return (int(float(r.get("Grid_Size_X") or 0)) * int(float(r.get("Grid_Size_Y") or 1)) *
+            int(float(r.get("Grid_Size_Z") or 1)))
+
+
+def dispatch_counters(dirname):
+    """{Dispatch_Id: (short kernel name, grid size, {counter: (sum, max) over its instance rows})} of
+    one ``--pmc`` run."""
+    out = {}
+    for r in _rows(_find(dirname, "counter_collection.csv")):
+        d = int(r["Dispatch_Id"])
+        if d not in out:
+            out[d] = (short_name(r["Kernel_Name"]), _grid(r), {})
+        vals = out[d][2]
+        v = float(r["Counter_Value"])
+        s, m = vals.get(r["Counter_Name"], (0.0, float("-inf")))
+        vals[r["Counter_Name"]] = (s + v, max(m, v))
+    return out
+
+
+def trace_durations(dirname):
+    """{(short kernel name, grid size): [duration ns, ...]} of a ``--kernel-trace`` run."""
+    out = {}
+    for r in _rows(_find(dirname, "kernel_trace.csv")):
+        key = (short_name(r["Kernel_Name"]), _grid(r))
+        out.setdefault(key, []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    return out
+
+
+def _copy_factor(disp, counter, copy_mib):
+    """Bytes per counter KiB: the last 3 plain-copy dispatches of the run moved copy_mib MiB each."""
+    ds = sorted(d for d, (n, _, v) in disp.items() if "copyBuffer" in n and counter in v)[-3:]
+    if not ds or copy_mib <= 0:
+        return None
+    kib = sum(disp[d][2][counter][0] for d in ds) / len(ds)
+    return copy_mib * 1024.0 / kib * 1024.0
+
+
+def counter_table(pmc_dirs, trace_dir, match, copy_mib, n_cu):
+    """Per (kernel, grid) whose name contains one of ``match``: dispatch count and mean duration from
+    the trace run, and the mean per-dispatch value of every counter of the pmc runs.  FETCH_SIZE and
+    WRITE_SIZE become bytes through the copy calibration; *_sum cycle counters become a fraction of
+    n_cu x the dispatch's GRBM_GUI_ACTIVE (its busy cycles, the max over XCDs) when that counter was
+    read in the same pass; MFMA op counters become TFLOP/s over the trace duration."""
+    durs = trace_durations(trace_dir)
+    rows = {}
+    for d in pmc_dirs:
+        disp = dispatch_counters(d)
+        factors = {c: _copy_factor(disp, c, copy_mib) for c in ("FETCH_SIZE", "WRITE_SIZE")}
+        for _, (name, grid, vals) in disp.items():
+            if not any(m in name for m in match):
+                continue
+            row = rows.setdefault((name, grid), {})
+            gui = vals.get("GRBM_GUI_ACTIVE", (0.0, 0.0))[1]
+            for c, (s, _) in vals.items():
+                if c in factors and factors[c]:
+                    row.setdefault(c + "_bytes", []).append(s * factors[c])
+                elif c.endswith("_sum") and ("CYCLES" in c or "BUSY" in c) and gui > 0:
+                    row.setdefault(c + "_frac", []).append(s / (n_cu * gui))
+                elif c.startswith("SQ_INSTS_VALU_MFMA_MOPS"):
+                    row.setdefault(c, []).append(s * 512.0)
+                elif c != "GRBM_GUI_ACTIVE":
+                    row.setdefault(c, []).append(s)
+    out = []
+    for (name, grid), row in sorted(rows.items()):
+        ds = durs.get((name, grid), [])
+        ent = {"kernel": name, "grid": grid, "calls": len(ds),
+               "avg_us": (sum(ds) / len(ds) / 1e3) if ds else None}
+        for c, v in row.items():
+            ent[c] = sum(v) / len(v)
+        if ent["avg_us"]:
+            by = ent.get("FETCH_SIZE_bytes", 0.0) + ent.get("WRITE_SIZE_bytes", 0.0)
+            if by:
+                ent["hbm_GBps"] = by / (ent["avg_us"] * 1e-6) / 1e9
+            fl = sum(v for c, v in ent.items() if c.startswith("SQ_INSTS_VALU_MFMA_MOPS"))
+            if fl:
+                ent["mfma_TFLOPs"] = fl / (ent["avg_us"] * 1e-6) / 1e12
+        out.append(ent)
+    return out
+
+
+def counter_markdown(ents, title, commands):
+    cols = [("calls", "calls", "{:.0f}"), ("avg_us", "avg us", "{:.2f}"),
+            ("FETCH_SIZE_bytes", "HBM read MB", "{:.2f}"), ("WRITE_SIZE_bytes", "HBM write MB", "{:.2f}"),
+            ("hbm_GBps", "HBM GB/s", "{:.0f}"), ("TA_TA_BUSY_sum_frac", "TA busy", "{:.0%}"),
+            ("TCP_PENDING_STALL_CYCLES_sum_frac", "L1 pending stall", "{:.0%}"),
+            ("TCP_TCC_READ_REQ_sum", "L1->L2 reads", "{:.3g}"), ("MfmaUtil", "MfmaUtil %", "{:.1f}"),
+            ("mfma_TFLOPs", "MFMA TFLOP/s", "{:.0f}"), ("SQ_LDS_BANK_CONFLICT", "LDS conflict cyc", "{:.3g}")]
+    cols = [c for c in cols if any(c[0] in e and e[c[0]] is not None for e in ents)]
+    scale = {"FETCH_SIZE_bytes": 1e-6, "WRITE_SIZE_bytes": 1e-6}
+    lines = [f"# {title}", "", "Commands (repo root, ``cd /tmp && export TMPDIR=/tmp`` first):", ""]
+    lines += ["    " + c for c in commands]
+    lines += ["", "| kernel | grid | " + " | ".join(h for _, h, _ in cols) + " |",
+              "|---|---:|" + "---:|" * len(cols)]
+    for e in ents:
+        cells = []
+        for k, _, f in cols:
+            v = e.get(k)
+            cells.append("" if v is None else f.format(v * scale.get(k, 1.0)))
+        lines.append(f"| `{e['kernel']}` | {e['grid']} | " + " | ".join(cells) + " |")
+    return lines
+
+
+# Counter passes of ``collect``: each pass stays within one rocprofv3 run's hardware limits (at most
+# 8 SQ, 4 TCC, 4 TCP, 2 TA and 2 GRBM counters).
+PMC_PASSES = (
+    ("FETCH_SIZE",),
+    ("WRITE_SIZE",),
+    ("TA_TA_BUSY_sum", "TCP_PENDING_STALL_CYCLES_sum", "TCP_TCC_READ_REQ_sum", "GRBM_GUI_ACTIVE"),
+    ("MfmaUtil", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_INSTS_VALU_MFMA_MOPS_F6F4"),
+)
+STAGE_KERNELS = ("moe_", "attn_", "gemm_", "rmsnorm", "qkv_", "pack_", "act_quant", "route", "router",
+                 "combine", "mx_", "fp8", "linear_", "grouped_")
+# bench.py arguments of the counter passes: few steps, a 256 MiB copy for the byte calibration
+PMC_BENCH = ("--no-cpu", "--steps", "2", "--warmup", "1", "--kernel-reps", "5", "--moe-reps", "5",
+             "--read-probe-mib", "0", "--copy-probe-mib", "256")
+
+
+def _run(cmd, log, timeout):
+    import subprocess
+    with open(log, "w") as f:
+        f.write(" ".join(cmd) + "\n")
+        f.flush()
+        subprocess.run(cmd, stdout=f, stderr=subprocess.STDOUT, timeout=timeout, check=True)
+
+
+def collect(out, name, bench_args, python="python3", timeout=300):
+    """Kernel trace + the PMC_PASSES counter passes of ``bench.py bench_args`` under rocprofv3, each a
+    child process (this process never touches the GPU), then the counter table (``name_counters.md``
+    and ``.json``) and the kernel table (``name_kernel_stats.md``).  Raw rocprofv3 output is removed;
+    the kernel trace is kept gzipped."""
+    import gzip
+    import shutil
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    bench = [python, os.path.join(root, "bench.py")]
+    os.makedirs(out, exist_ok=True)
+    trace = os.path.join(out, name + "_trace")
+    cmds = [["rocprofv3", "--kernel-trace", "--stats", "-f", "csv", "-d", trace, "-o", "run", "--", *bench,
+             "--no-cpu", "--read-probe-mib", "0", *bench_args]]
+    pmc_dirs = []
+    for i, ctrs in enumerate(PMC_PASSES):
+        d = os.path.join(out, f"{name}_pmc{i + 1}")
+        pmc_dirs.append(d)
+        cmds.append(["rocprofv3", "--kernel-trace", "--pmc", *ctrs, "-f", "csv", "-d", d, "-o", "run", "--",
+                     *bench, *PMC_BENCH, *bench_args])
+    for i, cmd in enumerate(cmds):
+        print(f"[profiling] {name} pass {i + 1}/{len(cmds)}", flush=True)
+        _run(cmd, os.path.join(out, f"{name}_pass{i + 1}.log"), timeout)
+    shown = [" ".join(["python3 -m flyai_amd.profiling collect --name", name, out, "--", *bench_args]),
+             "which runs:"] + [" ".join(c) for c in cmds]
+    shown = [c.replace(root + os.sep, "") for c in shown]
+    ents = counter_table(pmc_dirs, trace, STAGE_KERNELS, 256, 256)
+    with open(os.path.join(out, name + "_counters.json"), "w") as f:
+        json.dump(ents, f, indent=1)
+    with open(os.path.join(out, name + "_counters.md"), "w") as f:
+        f.write("\n".join(counter_markdown(ents, f"{name}: per-kernel counters", shown)) + "\n")
+    lines, total = kernel_table(trace)
+    with open(os.path.join(out, name + "_kernel_stats.md"), "w") as f:
+        f.write(f"# {name}: kernel time\n\nCommand (the trace pass of ``{shown[0]}``):\n\n    {shown[2]}\n\n"
+                f"All dispatches of the run, total "
+                f"{total / 1e6:.3f} ms of kernel time.\n\n" + "\n".join(lines) + "\n")
+    with open(_find(trace, "kernel_trace.csv"), "rb") as src, \
+            gzip.open(os.path.join(out, name + "_kernel_trace.csv.gz"), "wb") as dst:
+        shutil.copyfileobj(src, dst)
+    for d in [trace, *pmc_dirs]:
+        shutil.rmtree(d, ignore_errors=True)
+    return ents
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -122,7 +301,33 @@ def main(argv=None):
     t.add_argument("--json", required=True)
     t.add_argument("--command-fetch", required=True)
     t.add_argument("--command-write", required=True)
+    c = sub.add_parser("counters")
+    c.add_argument("trace_dir")
+    c.add_argument("pmc_dirs", nargs="+")
+    c.add_argument("--match", action="append", required=True)
+    c.add_argument("--copy-mib", type=int, default=0)
+    c.add_argument("--cus", type=int, default=256)
+    c.add_argument("--title", required=True)
+    c.add_argument("--command", action="append", required=True)
+    c.add_argument("--json")
+    k = sub.add_parser("collect")
+    k.add_argument("out")
+    k.add_argument("--name", required=True)
+    k.add_argument("--timeout", type=int, default=300)
+    k.add_argument("bench_args", nargs=argparse.REMAINDER)
     a = ap.parse_args(argv)
+
+    if a.cmd == "collect":
+        extra = [x for x in a.bench_args if x != "--"]
+        collect(a.out, a.name, extra, timeout=a.timeout)
+        return 0
+    if a.cmd == "counters":
+        ents = counter_table(a.pmc_dirs, a.trace_dir, a.match, a.copy_mib, a.cus)
+        if a.json:
+            with open(a.json, "w") as f:
+                json.dump(ents, f, indent=1)
+        print("\n".join(counter_markdown(ents, a.title, a.command)))
+        return 0
 
     if a.cmd == "stats":
         lines, total = kernel_table(a.dir)

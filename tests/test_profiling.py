@@ -58,3 +58,33 @@ def test_kernel_table_and_last_dispatches(tmp_path):
     lines, total = profiling.kernel_table(d)
     assert total == 4000 and lines[2].startswith("| `a` | 2 | 1.50")
     assert profiling.last_dispatches(d, "a", 1) == [(3, 2000)]
+
+
+def test_counter_table_groups_by_kernel_and_grid(tmp_path):
+    d = str(tmp_path)
+    trace = os.path.join(d, "trace")
+    os.makedirs(trace)
+    _write(os.path.join(trace, "c1_kernel_trace.csv"),
+           ["Dispatch_Id", "Kernel_Name", "Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z", "Start_Timestamp",
+            "End_Timestamp"],
+           [[1, "attn(int)", 64, 1, 1, 0, 2000], [2, "attn(int)", 128, 1, 1, 0, 4000],
+            [3, "attn(int)", 64, 1, 1, 0, 4000]])
+    pmc = os.path.join(d, "pmc")
+    os.makedirs(pmc)
+    hdr = ["Dispatch_Id", "Kernel_Name", "Grid_Size", "Counter_Name", "Counter_Value"]
+    rows = [[1, "attn(int)", 64, "FETCH_SIZE", 50.0], [1, "attn(int)", 64, "FETCH_SIZE", 50.0],
+            [1, "attn(int)", 64, "TA_TA_BUSY_sum", 1000.0], [1, "attn(int)", 64, "GRBM_GUI_ACTIVE", 10.0],
+            [1, "attn(int)", 64, "GRBM_GUI_ACTIVE", 5.0],
+            [2, "attn(int)", 128, "FETCH_SIZE", 300.0], [2, "attn(int)", 128, "SQ_INSTS_VALU_MFMA_MOPS_BF16", 2.0],
+            [3, "__amd_rocclr_copyBuffer", 4096, "FETCH_SIZE", 512.0]]
+    _write(os.path.join(pmc, "c1_counter_collection.csv"), hdr, rows)
+    ents = profiling.counter_table([pmc], trace, ["attn"], copy_mib=1, n_cu=200)
+    by = {e["grid"]: e for e in ents}
+    # a 1 MiB copy reads as 512 KiB -> 2 bytes per counter byte; instance rows of a dispatch add up
+    assert by[64]["FETCH_SIZE_bytes"] == 100.0 * 2 * 1024
+    assert by[64]["calls"] == 2 and by[64]["avg_us"] == 3.0
+    # busy cycles over n_cu x the dispatch's GRBM_GUI_ACTIVE (max over its instances)
+    assert by[64]["TA_TA_BUSY_sum_frac"] == 1000.0 / (200 * 10.0)
+    assert by[128]["mfma_TFLOPs"] == 2.0 * 512 / 4e-6 / 1e12
+    md = profiling.counter_markdown(ents, "t", ["cmd"])
+    assert md[0] == "# t" and any(line.startswith("| `attn` | 64 |") for line in md)

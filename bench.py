@@ -44,6 +44,8 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp8": 5000.0}
 READ_PROBE_WG_PER_CU = 8   # workgroups per CU of the read-streaming probe
+# sizes of the read probe's shorter runs: about one projection weight, one down and one gate_up launch
+READ_PROBE_SIZES_MIB = (30, 454, 903)
 
 
 # ---- workloads -----------------------------------------------------------------------------------
@@ -173,6 +175,26 @@ def hbm_read_ceiling(mib, dev, reps=20, grid_per_cu=None):
                                              C.c_void_p(torch.cuda.current_stream().cuda_stream)))
         us = hip_event_us(run, reps, warmup=3)
         out[name] = round(buf.numel() / (us * 1e-6) / 1e9, 1)
+    # smaller reads, each launch on the next slice of the buffer (a slice is not re-read before the
+    # others, so its bytes are gone from the 256 MiB memory-side cache): the time a kernel that only
+    # streams that many bytes takes, launch included -- the floor for a kernel of the same bytes
+    by_size = {}
+    for smib in READ_PROBE_SIZES_MIB:
+        nslice = mib // smib
+        if nslice < 2:
+            continue
+        nbytes = smib << 20
+        turn = [0]
+
+        def run_slice():
+            off = (turn[0] % nslice) * nbytes
+            turn[0] += 1
+            check(lib().flyai_hbm_read_probe(C.c_void_p(buf.data_ptr() + off), nbytes, 1, grid,
+                                             C.c_void_p(sink.data_ptr()),
+                                             C.c_void_p(torch.cuda.current_stream().cuda_stream)))
+        us = hip_event_us(run_slice, max(reps, 2 * nslice), warmup=3)
+        by_size[f"{smib}MiB"] = {"us": round(us, 2), "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    out["nontemporal_by_size"] = by_size
     del buf
     return out
 

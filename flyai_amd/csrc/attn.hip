@@ -232,10 +232,14 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
                                           const int64_t* __restrict__ kv_base,
                                           const int32_t* __restrict__ kv_cap, int window, int Hq,
                                           float* __restrict__ partials,
+                                          const flyai_attn_group* __restrict__ groups, int n_groups,
+                                          const float* __restrict__ sinks, uint16_t* __restrict__ out,
                                           const flyai_attn_tree* __restrict__ tree,
                                           const int* __restrict__ dep_s) {
   const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
+  // the item is its rows' whole key range (a group index outside the plan reads as "not single")
+  const bool single = it.group >= 0 && it.group < n_groups && groups[it.group].n_splits == 1;
   const int cap = kv_cap[it.seq];
   const int64_t base = kv_base[it.seq] + (int64_t)it.kv_head * cap * 64;
   const uint16_t* K = k_pool + base;
@@ -280,7 +284,9 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
       }
     }
   }
-  // partial record per query row: [m, l, O[64]]; O^T layout: lane holds dims 16dt + 4g + v of qrow n
+  // partial record per query row: [m, l, O[64]]; O^T layout: lane holds dims 16dt + 4g + v of qrow n.
+  // A row whose whole key range is this item is finished here with the merge's arithmetic for one
+  // split (the same operations in the same order, so the same bits), and the merge skips its group.
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     float l = R.l_run[qt];
@@ -288,6 +294,26 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
     l += __shfl_xor(l, 32, 64);
     const int rq = 16 * qt + n;
     if (!R.qval[qt]) continue;
+    if (single) {
+      const int h = it.kv_head * 8 + (rq & 7);
+      const float sink = sinks[h] * kLog2e;
+      const float M = fmaxf(sink, R.m_run[qt]);
+      float L = exp2f(sink - M);
+      const float wgt = exp2f(R.m_run[qt] - M);
+      L += l * wgt;
+      const float inv = 1.0f / L;
+      uint16_t* o = out + ((size_t)(it.tok + (rq >> 3)) * Hq + h) * 64;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        float a[4];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) a[v] = 0.f + R.O[qt][dt][v] * wgt;
+        const uint32_t lo = (uint32_t)f2bf(a[0] * inv) | ((uint32_t)f2bf(a[1] * inv) << 16);
+        const uint32_t hi = (uint32_t)f2bf(a[2] * inv) | ((uint32_t)f2bf(a[3] * inv) << 16);
+        *reinterpret_cast<uint2*>(o + 16 * dt + 4 * g) = make_uint2(lo, hi);
+      }
+      continue;
+    }
     float* rec = partials + ((size_t)item_idx * kAttnRows + rq) * kPartFloats;
     if (g == 0) {
       rec[0] = R.m_run[qt];
@@ -307,7 +333,8 @@ __global__ __launch_bounds__(64, 2) void attn_partial_kernel(
     const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
     const int32_t* __restrict__ kv_cap, int window, int Hq,
     const flyai_attn_item* __restrict__ items, const int32_t* __restrict__ n_live,
-    float* __restrict__ partials, const flyai_attn_tree* __restrict__ tree) {
+    float* __restrict__ partials, const flyai_attn_group* __restrict__ groups, int n_groups,
+    const float* __restrict__ sinks, uint16_t* __restrict__ out, const flyai_attn_tree* __restrict__ tree) {
   __shared__ int dep_s[64];
   // a graph-replayed step launches the plan's capacity; items past this step's count exit
   if (n_live && (int)blockIdx.x >= *n_live) return;
@@ -316,15 +343,19 @@ __global__ __launch_bounds__(64, 2) void attn_partial_kernel(
     dep_s[threadIdx.x] = (int)threadIdx.x < tree->n_nodes ? tree->depth[threadIdx.x] : 0;
     __syncthreads();
     if (it.ntok <= 2)
-      attn_item<1, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, tree, dep_s);
+      attn_item<1, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
+                         tree, dep_s);
     else
-      attn_item<2, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, tree, dep_s);
+      attn_item<2, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
+                         tree, dep_s);
     return;
   }
   if (it.ntok <= 2)
-    attn_item<1, false>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, nullptr, nullptr);
+    attn_item<1, false>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
+                         nullptr, nullptr);
   else
-    attn_item<2, false>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, nullptr, nullptr);
+    attn_item<2, false>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
+                         nullptr, nullptr);
 }
 
 // ---- chunked-prefill rows -------------------------------------------------------------------------
@@ -449,6 +480,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(const float* __restrict
                                                          uint16_t* __restrict__ out) {
   if (n_live && (int)blockIdx.x >= *n_live) return;  // as in attn_partial_kernel
   const flyai_attn_group gr = groups[blockIdx.x];
+  if (gr.n_splits == 1) return;  // finished by its only item (attn_item)
   const int rq = threadIdx.x >> 3, part = threadIdx.x & 7;
   const int ti = rq >> 3;
   if (ti >= gr.ntok) return;
@@ -506,13 +538,14 @@ int launch_attn(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_poo
                 const int64_t* kv_base, const int32_t* kv_cap, const float* sinks, int window,
                 int Hq, const flyai_attn_item* items, int n_items, int n_small,
                 const flyai_attn_group* groups, int n_groups, const int32_t* counts, float* partials,
-                uint16_t* out, const flyai_attn_tree* tree, hipStream_t s) {
+                uint16_t* out, const flyai_attn_tree* tree, bool merge, hipStream_t s) {
   if (n_items == 0) return FLYAI_OK;
   (void)n_small;  // the plan's two ranges share one launch
   hipLaunchKernelGGL(attn_partial_kernel, dim3(n_items), dim3(64), 0, s, q, k_pool, v_pool, kv_base,
-                     kv_cap, window, Hq, items, counts, partials, tree);
+                     kv_cap, window, Hq, items, counts, partials, groups, n_groups, sinks, out, tree);
   int rc = check_launch("attn_partial");
   if (rc) return rc;
+  if (!merge) return FLYAI_OK;  // every group has one split: the items wrote the output
   hipLaunchKernelGGL(attn_merge_kernel, dim3(n_groups), dim3(256), 0, s, partials, groups, sinks,
                      Hq, counts ? counts + 1 : nullptr, out);
   return check_launch("attn_merge");
@@ -728,6 +761,6 @@ extern "C" int flyai_attn_ragged(const uint16_t* q, const uint16_t* k_pool, cons
                     (n_items == 0 || (items_dev && groups_dev && partials)),
                 "attn: null pointer");
   return launch_attn(q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, items_dev, n_items,
-                     n_items_small, groups_dev, n_groups, nullptr, partials, out, nullptr,
+                     n_items_small, groups_dev, n_groups, nullptr, partials, out, nullptr, true,
                      as_stream(stream));
 }

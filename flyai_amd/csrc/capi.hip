@@ -61,7 +61,7 @@ int launch_qkv_rope_kv(const uint16_t*, const uint16_t*, const uint16_t*, float*
 size_t linear_partials_bytes(int M, int N, int K);
 int launch_attn(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
                 const float*, int, int, const flyai_attn_item*, int, int, const flyai_attn_group*, int,
-                const int32_t*, float*, uint16_t*, const flyai_attn_tree*, hipStream_t);
+                const int32_t*, float*, uint16_t*, const flyai_attn_tree*, bool, hipStream_t);
 int attn_plan(const int32_t*, const int32_t*, int, int, int, int, flyai_attn_item*, int,
               flyai_attn_group*, int, int*, int*, int*, int, flyai_attn_item*, int, int*);
 int launch_attn_prefill(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
@@ -119,7 +119,7 @@ struct flyai_stage {
   bool graphs = false;
   hipStream_t capture_stream = nullptr;
   struct Graph {
-    int64_t key[8];
+    int64_t key[10];
     hipGraphExec_t exec;
     uint64_t last_use;
   };
@@ -320,6 +320,7 @@ struct StepPlan {
   int grid_items[2], grid_groups[2];  // launch sizes: exact counts, or the plan capacities (graphs)
   int n_small[2];
   int n_pitems[2];  // chunked-prefill attention items (exact counts, part of the graph key)
+  int merge[2];     // some group has more than one split: the merge kernel runs (part of the graph key)
   size_t off_counts, off_q, off_st, off_cap, off_base, off_items[2], off_groups[2], off_pitems[2];
   bool tree = false;  // a tree-verify step: the blob carries the flyai_attn_tree at off_tree
   size_t off_tree = 0;
@@ -363,7 +364,7 @@ static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* count
                     reinterpret_cast<const flyai_attn_item*>(blob + sp.off_items[p]), sp.grid_items[p],
                     sp.n_small[p], reinterpret_cast<const flyai_attn_group*>(blob + sp.off_groups[p]),
                     sp.grid_groups[p], counts ? counts + 2 * p : nullptr, F32(st->o_parts),
-                    B16(st->o_attn), tree_d, s));
+                    B16(st->o_attn), tree_d, sp.merge[p] != 0, s));
     RUN(launch_attn_prefill(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks, L.sliding ? c.window : 0,
                             c.n_q_heads, reinterpret_cast<const flyai_attn_item*>(blob + sp.off_pitems[p]),
                             sp.n_pitems[p], B16(st->o_attn), s));
@@ -415,8 +416,8 @@ static int hip_fail(const char* what, hipError_t e) {
 
 // The executable graph for this step's key, captured on first use (least recently used evicted).
 static int step_graph(flyai_stage* st, const StepPlan& sp, hipGraphExec_t* out) {
-  const int64_t key[8] = {sp.Tn, sp.S, sp.grid_items[0], sp.grid_items[1], sp.grid_groups[0], sp.grid_groups[1],
-                          sp.n_pitems[0], sp.n_pitems[1]};
+  const int64_t key[10] = {sp.Tn, sp.S, sp.grid_items[0], sp.grid_items[1], sp.grid_groups[0], sp.grid_groups[1],
+                           sp.n_pitems[0], sp.n_pitems[1], sp.merge[0], sp.merge[1]};
   ++st->use_clock;
   for (auto& g : st->graph_cache)
     if (memcmp(g.key, key, sizeof(key)) == 0) {
@@ -468,6 +469,13 @@ extern "C" int flyai_stage_set_graphs(flyai_stage* st, int32_t enable) {
 }
 
 extern "C" int32_t flyai_stage_graphs_captured(const flyai_stage* st) { return st ? st->graphs_captured : 0; }
+
+// A group of one split is finished by its item; the merge kernel is needed only past that.
+static int plan_needs_merge(const flyai_attn_group* groups, int n) {
+  for (int i = 0; i < n; ++i)
+    if (groups[i].n_splits > 1) return 1;
+  return 0;
+}
 
 // One compact blob per step: live counts | q_lens | starts | kv_cap | kv_base | items x2 | groups x2
 // [| tree], staged through the double-buffered pinned halves and copied with one H2D copy.
@@ -583,6 +591,7 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
     auto bucket = [](int n, int cap) { const int b = (n + kPlanBucket - 1) / kPlanBucket * kPlanBucket; return b < cap ? b : cap; };
     sp.grid_items[p] = st->graphs ? bucket(n_items[p], c.max_attn_items) : n_items[p];
     sp.grid_groups[p] = st->graphs ? bucket(n_groups[p], st->max_groups) : n_groups[p];
+    sp.merge[p] = plan_needs_merge(st->plan_groups[p].data(), n_groups[p]);
   }
   RUN(stage_blob(st, sp, q_lens, starts, kv_base, kv_cap, n_items, n_groups, nullptr, s));
   if (!st->graphs) return record_step(st, sp, nullptr, hidden, s);
@@ -656,6 +665,7 @@ extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t 
     sp.grid_items[p] = n_items[p];
     sp.grid_groups[p] = n_groups[p];
     sp.n_pitems[p] = 0;
+    sp.merge[p] = plan_needs_merge(st->plan_groups[p].data(), n_groups[p]);
   }
   const int32_t q_len = n, st0 = start;
   RUN(stage_blob(st, sp, &q_len, &st0, &kv_base, &kv_cap, n_items, n_groups, &tree, s));

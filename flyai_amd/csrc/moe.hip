@@ -13,6 +13,7 @@
 // in a dot product, lane (r, g) supplies, at MFMA step j of group kg, the 8 K values
 // 32*(4kg+g) + 8j .. +7 for BOTH operands: the lane's 16 weight bytes feed four MFMA steps and
 // its activation bytes are the matching 64 contiguous bytes of the activation row.
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -240,29 +241,16 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
   }
 }
 
-constexpr int kNTW = 2;  // weight tiles per wave
 // Weight tiles per wave and weight-ring depth (128-K groups) of the decode-sized kernels.  Two tiles
 // and an 8-deep ring keep 14 KiB in flight per wave at 3 waves per SIMD (166 registers), against
 // 9 KiB for 3 tiles and a 4-deep ring (162 registers); the workgroups are also a third smaller, so
 // the end of the launch, where the last workgroups run alone, is shorter.  Measured on the C1 step
 // (9 layers, A/B on one box): 3 tiles x 4 deep 3.13 ms; 2 x 8 3.04 ms; 1 x 8, 2 x 4 and 2 x 12 for
-// gate_up and 1 x 8, 1 x 16 and 2 x 12 for down all slower.  The macros allow such sweeps.
-#ifndef FLYAI_MOE_NTW_GATE_UP
-#define FLYAI_MOE_NTW_GATE_UP 2
-#endif
-#ifndef FLYAI_MOE_NTW_DOWN
-#define FLYAI_MOE_NTW_DOWN 2
-#endif
-#ifndef FLYAI_MOE_DEPTH_GATE_UP
-#define FLYAI_MOE_DEPTH_GATE_UP 8
-#endif
-#ifndef FLYAI_MOE_DEPTH_DOWN
-#define FLYAI_MOE_DEPTH_DOWN 8
-#endif
-constexpr int kNTWGateUp = FLYAI_MOE_NTW_GATE_UP;
-constexpr int kNTWDown = FLYAI_MOE_NTW_DOWN;
-constexpr int kDepthGateUp = FLYAI_MOE_DEPTH_GATE_UP;
-constexpr int kDepthDown = FLYAI_MOE_DEPTH_DOWN;
+// gate_up and 1 x 8, 1 x 16 and 2 x 12 for down all slower.
+constexpr int kNTWGateUp = 2;
+constexpr int kNTWDown = 2;
+constexpr int kDepthGateUp = 8;
+constexpr int kDepthDown = 8;
 
 // ---- dense groups as a tiled GEMM ----------------------------------------------------------------
 // For groups of many rows the weights are still read once from HBM, but each weight byte now feeds
@@ -899,13 +887,21 @@ __global__ __launch_bounds__(512) void moe_mx_gemm_kernel(
 // Chunk of weight blocks per workgroup: the largest chunk that still gives at least 3 rounds of
 // workgroups over the CUs, so that workgroups of unequal length (experts with different row
 // counts take different row tiles) balance, while each start-up is shared by several blocks.
+// The CU count is read per device (once each) for the device current at the call.
+inline int device_cus() {
+  constexpr int kDevices = 64;
+  static std::atomic<int> cached[kDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevices) return 256;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v > 0) return v;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+  cached[dev].store(v, std::memory_order_relaxed);
+  return v;
+}
+
 inline int gemm_chunk(const MxGeom& gm, int E) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, v = 0;
-    cus = (hipGetDevice(&dev) == hipSuccess &&
-           hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) ? v : 256;
-  }
+  const int cus = device_cus();
   const int W = (gm.NT + kGemmTiles - 1) / kGemmTiles;
   int best = 1;
   for (int c = 1; c <= W; ++c)

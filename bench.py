@@ -109,9 +109,9 @@ def main():
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     ap.add_argument("--workload", choices=("c1", "c2", "c3", "wire"), default="c1")
     ap.add_argument("--frames", type=int, default=20, help="--workload wire: frames per path")
-    ap.add_argument("--dense", choices=("fp8", "bf16"), default="fp8",
-                    help="--workload c2: dense expert groups on the scaled MFMA with fp8 activations (fp8) or "
-                         "on the bf16-activation tiled GEMM (bf16)")
+    ap.add_argument("--dense", choices=("fp8", "bf16"), default="bf16",
+                    help="--workload c2: dense expert groups on the scaled MFMA with two-term fp8 activations "
+                         "(fp8) or on the bf16-activation tiled GEMM (bf16)")
     ap.add_argument("--graphs", action="store_true",
                     help="replay the stage step as a HIP graph (measured slower than direct launches "
                          "on this stack, so off by default)")
@@ -366,8 +366,9 @@ def run_gptoss(args, chunked_prefill=False):
         flops = 2.0 * P * shape.hidden * 2 * shape.intermediate
         tflops = flops / (gu_us * 1e-6) / 1e12
         peak = MFMA_PEAK_TFLOPS["fp8" if fp8 else "bf16"]
-        dtype = ("mxfp4-e2m1 weights x fp8-e4m3 activations (E8M0 per-32 scales, scaled MFMA) in the dense "
-                 "expert groups, bf16 elsewhere; fp32 accumulate") if fp8 else "mxfp4-e2m1/bf16 (fp32 accumulate)"
+        dtype = ("mxfp4-e2m1 weights x two-term fp8-e4m3 activations (high + low term, E8M0 per-32 scales, "
+                 "scaled MFMA) in the dense expert groups, bf16 elsewhere; fp32 accumulate") if fp8 \
+            else "mxfp4-e2m1/bf16 (fp32 accumulate)"
         kname = "moe_mx_gemm_kernel<gate_up> (scaled f8f6f4 MFMA)" if fp8 else "moe_mxfp4_gemm_kernel<gate_up>"
         line = {
             "metric": "stage tokens/sec at a chunked-prefill mixed batch; MoE layer us; % MFMA roofline",

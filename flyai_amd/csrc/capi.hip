@@ -173,10 +173,11 @@ static void layout(flyai_stage* st) {
   st->o_h2 = d.take(T * c.hidden * 2);
   st->o_hidden = d.take(T * c.hidden * 2);
   if (c.moe_dense_fp8) {
-    st->o_xq = d.take(T * c.hidden);
-    st->o_xs = d.take(flyai_mx_act_scale_bytes(c.max_tokens, c.hidden));
-    st->o_hq = d.take(P * c.intermediate);
-    st->o_hs = d.take(flyai_mx_act_scale_bytes((int32_t)P, c.intermediate));
+    // two e4m3 terms per row (high, then low): 2 rows of bytes and scales per activation row
+    st->o_xq = d.take(2 * T * c.hidden);
+    st->o_xs = d.take(flyai_mx_act_scale_bytes(2 * c.max_tokens, c.hidden));
+    st->o_hq = d.take(2 * P * c.intermediate);
+    st->o_hs = d.take(flyai_mx_act_scale_bytes((int32_t)(2 * P), c.intermediate));
   }
   st->dev_bytes = d.off;
   st->host_half = st->blob_max;

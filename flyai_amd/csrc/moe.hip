@@ -590,9 +590,40 @@ typedef int mx_v8i_t __attribute__((ext_vector_type(8)));
 __host__ __device__ inline int mx_act_scale_row_bytes(int K) { return 16 * mx_geom(1, 16, K).KG4; }
 
 // One wave per (row, 4 groups of 128 K): 8 elements per lane from one 16-byte load, 4 lanes per
-// 32-block; the block's amax by xor shuffles, s = 2^ceil(log2(max(amax, 1e-4) / 448)), q = e4m3 RNE of
-// clamp(x / s, +-448) (v_cvt_pk_fp8_f32), scale byte e + 127.  Blocks past K (up to 16 * KG4 per row)
-// only write their scale byte, 127.
+// 32-block.  Each row is carried as two e4m3 terms, x = s1 q1 + s2 q2 + (rounding of the second term):
+// the high term per block is s1 = 2^ceil(log2(max(amax, 1e-4) / 448)) (amax by xor shuffles), q1 = e4m3
+// RNE of clamp(x / s1, +-448) (v_cvt_pk_fp8_f32); the residual x - s1 q1 is exact in fp32 (q1 s1 is x
+// rounded to 4 significant bits), and the low term is the same rule applied to it.  Together they hold
+// the 8 significant bits of a bf16 x, so the scaled-MFMA products carry the bf16 operand's precision.
+// Row r's high term is row r of q and s, its low term row M + r.  Scale byte e + 127; blocks past K (up
+// to 16 * KG4 per row) only write their scale byte, 127.
+__device__ __forceinline__ int mx_block_scale_exp(float amax) {
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  amax = fmaxf(amax, 1e-4f);
+  // ceil(log2(amax / 448)) from the bits of amax * (1/448), a normal number since amax >= 1e-4
+  const uint32_t bits = __float_as_uint(amax * (1.0f / 448.0f));
+  return (int)((bits >> 23) & 0xff) - 127 + ((bits & 0x7fffffu) ? 1 : 0);
+}
+
+// e4m3 bytes of v * 2^-e (clamped to +-448), two dwords; dec receives the values the bytes hold
+__device__ __forceinline__ uint2 mx_fp8_pack(const float (&v)[8], int e, float (&dec)[8]) {
+  uint32_t w[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float y[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(ldexpf(v[4 * i + j], -e), -448.0f), 448.0f);
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
+    w[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], lo, true);
+    dec[4 * i + 0] = __builtin_amdgcn_cvt_f32_fp8((int)w[i], 0);
+    dec[4 * i + 1] = __builtin_amdgcn_cvt_f32_fp8((int)w[i], 1);
+    dec[4 * i + 2] = __builtin_amdgcn_cvt_f32_fp8((int)w[i], 2);
+    dec[4 * i + 3] = __builtin_amdgcn_cvt_f32_fp8((int)w[i], 3);
+  }
+  return make_uint2(w[0], w[1]);
+}
+
 __global__ __launch_bounds__(256) void mx_act_quant_kernel(const uint16_t* __restrict__ x, int M, int K,
                                                            uint8_t* __restrict__ q, uint8_t* __restrict__ s) {
   const MxGeom gm = mx_geom(1, 16, K);
@@ -613,36 +644,37 @@ __global__ __launch_bounds__(256) void mx_act_quant_kernel(const uint16_t* __res
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-  amax = fmaxf(amax, 1e-4f);
-  // ceil(log2(amax / 448)) from the bits of amax * (1/448), a normal number since amax >= 1e-4
-  const uint32_t bits = __float_as_uint(amax * (1.0f / 448.0f));
-  const int e = (int)((bits >> 23) & 0xff) - 127 + ((bits & 0x7fffffu) ? 1 : 0);
+  const int e1 = mx_block_scale_exp(amax);
+  float d1[8], r[8], d2[8];
+  const uint2 w1 = mx_fp8_pack(v, e1, d1);
+  float ramax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    r[i] = v[i] - ldexpf(d1[i], e1);  // exact: the high term is v rounded to 4 significant bits
+    ramax = fmaxf(ramax, fabsf(r[i]));
+  }
+  const int e2 = mx_block_scale_exp(ramax);
+  const uint2 w2 = mx_fp8_pack(r, e2, d2);
   if (in) {
-    uint32_t w[2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      float y[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) y[j] = fminf(fmaxf(ldexpf(v[4 * i + j], -e), -448.0f), 448.0f);
-      const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(y[0], y[1], 0, false);
-      w[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(y[2], y[3], lo, true);
-    }
-    *reinterpret_cast<uint2*>(q + (size_t)row * K + k0) = make_uint2(w[0], w[1]);
+    *reinterpret_cast<uint2*>(q + (size_t)row * K + k0) = w1;
+    *reinterpret_cast<uint2*>(q + (size_t)(M + row) * K + k0) = w2;
   }
   if ((lane & 3) == 0) {
     const int blk = kg4 * 16 + lane / 4;  // block index within the row
     const int kg = blk / 4, g = blk % 4;
-    s[(size_t)row * mx_act_scale_row_bytes(K) + ((kg >> 2) * 4 + g) * 4 + (kg & 3)] = in ? (uint8_t)(e + 127) : 127;
+    const size_t at = ((kg >> 2) * 4 + g) * 4 + (kg & 3);
+    const size_t rb = mx_act_scale_row_bytes(K);
+    s[(size_t)row * rb + at] = in ? (uint8_t)(e1 + 127) : 127;
+    s[(size_t)(M + row) * rb + at] = in ? (uint8_t)(e2 + 127) : 127;
   }
 }
 
-constexpr int kMxStage = 8 * 2048 + 8 * 256 + kGemmTiles * 256;  // activations, their scales, weight scales
+constexpr int kMxMaxMT = 12;  // row tiles per pass: up to 6 real row tiles, each as a high and a low tile
+constexpr int kMxStage = kMxMaxMT * 2048 + kMxMaxMT * 256 + kGemmTiles * 256;  // activations, their scales, weight scales
 
 // what one workgroup of the scaled GEMM works on
 struct MxCtx {
-  const uint8_t* act;     // fp8 activation rows [*, K]
+  const uint8_t* act;     // fp8 activation rows [*, K]: high terms, then low terms from row lo_off
   const uint8_t* ascale;  // their scale rows, mx_act_scale_row_bytes(K) each
   const int32_t* perm;
   const float* bias;
@@ -651,7 +683,7 @@ struct MxCtx {
   const uint8_t* sbase;  // the expert's weight scale rows, + lane * 4
   MxGeom gm;
   size_t tile_bytes;
-  int as_row, k_top, N, K, e, nb0, nbn, row_lo, lane, wave, r, g;
+  int as_row, k_top, N, K, e, nb0, nbn, row_lo, lo_off, lane, wave, r, g;
 };
 
 // One pass over MT row tiles (16 * MT rows from m0) and every weight block of the chunk.  The pipeline
@@ -667,32 +699,43 @@ __device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStag
                                              char (&st2)[kMxStage], char (&st3)[kMxStage], int m0, int rows) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) void* lds_ptr;
-  static_assert(MT == 4 || MT == 8, "row tiles per pass");
+  static_assert(MT == 4 || MT == 8 || MT == 12, "row tiles per pass");
+  constexpr int MR = MT / 2;                   // real row tiles: tile m < MR is the high term, m + MR the low
   constexpr int ASOFF = MT * 2048;             // activation scale dwords: MT x 256 B
   constexpr int WSOFF = ASOFF + MT * 256;      // weight scale dwords: 16 tiles x 256 B
   constexpr int AJ = MT / 4;                   // activation fragment blocks per wave per group
-  constexpr int LOADS = 2 + 2 + AJ + 1;        // weight tiles, weight scales, activations, their scales
+  constexpr int SJ = (MT + 7) / 8;             // activation scale blocks per wave per group
+  constexpr int LOADS = 2 + 2 + AJ + SJ;       // weight tiles, weight scales, activations, their scales
   constexpr int WAIT = (kGemmStages - 2) * LOADS;
   const MxGeom& gm = c.gm;
   const int lane = c.lane, wave = c.wave, r = c.r, g = c.g;
   auto tile_of = [&](int nb, int n) __attribute__((always_inline)) {
     return min((c.nb0 + nb) * kGemmTiles + 2 * wave + n, gm.NT - 1);
   };
-  auto src_row = [&](int row) __attribute__((always_inline)) {
+  // activation row of lane r of row tile t (t >= MR: the low term of tile t - MR)
+  auto src_row = [&](int t) __attribute__((always_inline)) {
+    const int row = (t % MR) * 16 + r;
     const int p = c.row_lo + m0 + (row < rows ? row : 0);  // rows past the pass read row 0, never stored
-    return GATE_UP ? c.perm[p] / c.k_top : p;
+    return (GATE_UP ? c.perm[p] / c.k_top : p) + (t >= MR ? c.lo_off : 0);
   };
   const int KGP = (gm.KG + kGemmStages - 1) / kGemmStages * kGemmStages;  // groups per block, padded
-  // DMA sources: fragment block b = J*8 + wave is row tile b/2, half b%2; scale block wave % MT
+  // DMA sources: fragment block b = J*8 + wave is row tile b/2, half b%2; scale blocks wave + 8 j
+  // (clamped: waves past the last tile load a copy of an earlier one, so every wave issues SJ loads)
   const uint8_t* arow[AJ];
   int akl[AJ];  // the lane's K offset within a group, for the half its block holds
 #pragma unroll
   for (int J = 0; J < AJ; ++J) {
     const int b = J * 8 + wave;
     akl[J] = 64 * (b & 1) + 16 * g;
-    arow[J] = c.act + (size_t)src_row((b >> 1) * 16 + r) * c.K + akl[J];
+    arow[J] = c.act + (size_t)src_row(b >> 1) * c.K + akl[J];
   }
-  const uint8_t* asrow = c.ascale + (size_t)src_row((wave % MT) * 16 + r) * c.as_row + 4 * g;
+  const uint8_t* asrow[SJ];
+  int astile[SJ];
+#pragma unroll
+  for (int j = 0; j < SJ; ++j) {
+    astile[j] = (wave + 8 * j) < MT ? wave + 8 * j : wave % MT;
+    asrow[j] = c.ascale + (size_t)src_row(astile[j]) * c.as_row + 4 * g;
+  }
   int i_nb = 0, i_kg = 0;
   auto issue = [&](u32x4 (&bq)[2], char* stage) __attribute__((always_inline)) {
     const int nb = min(i_nb, c.nbn - 1), kg = i_kg;
@@ -711,8 +754,10 @@ __device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStag
     for (int J = 0; J < AJ; ++J)
       __builtin_amdgcn_global_load_lds((const void*)(arow[J] + (kg * 128 + akl[J] < c.K ? kg * 128 : 0)),
                                        (lds_ptr)(stage + (J * 8 + wave) * 1024), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds((const void*)(asrow + min(kg / 4, gm.KG4 - 1) * 16),
-                                     (lds_ptr)(stage + ASOFF + (wave % MT) * 256), 4, 0, 0);
+#pragma unroll
+    for (int j = 0; j < SJ; ++j)
+      __builtin_amdgcn_global_load_lds((const void*)(asrow[j] + min(kg / 4, gm.KG4 - 1) * 16),
+                                       (lds_ptr)(stage + ASOFF + astile[j] * 256), 4, 0, 0);
     if (++i_kg == KGP) {
       i_kg = 0;
       ++i_nb;
@@ -775,7 +820,8 @@ __device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStag
 #pragma unroll
     for (int n = 0; n < 2; ++n) bsum[n] = c.bias[(size_t)c.e * c.N + tile_of(min(nb, c.nbn - 1), n) * 16 + r];
   };
-  // acc[m][n][v] = D[group row 16m + 4g + v][feature (block tile 2*wave + n) * 16 + r]
+  // acc[m][n][v] = D[group row 16m + 4g + v][feature (block tile 2*wave + n) * 16 + r] of the high term
+  // (m < MR) or the low term (m >= MR, row 16(m - MR) + 4g + v)
   auto epilogue = [&](int nb) __attribute__((always_inline)) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
@@ -783,11 +829,11 @@ __device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStag
       const bool nval = tile < gm.NT;
       const int feat = tile * 16 + r;
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
+      for (int m = 0; m < MR; ++m) {
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int orow = 16 * m + 4 * g + v;
-          const float val = acc[m][n][v] + bsum[n];
+          const float val = (acc[m][n][v] + acc[m + MR][n][v]) + bsum[n];
           if (GATE_UP) {
             const float partner = lane_xor1(val);
             if (nval && (r & 1) == 0 && orow < rows)
@@ -840,7 +886,8 @@ template <bool GATE_UP>
 __global__ __launch_bounds__(512) void moe_mx_gemm_kernel(
     const uint8_t* __restrict__ act, const uint8_t* __restrict__ ascale, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, int k_top, const uint8_t* __restrict__ packed,
-    const float* __restrict__ bias, int E, int N, int K, int min_rows, int chunk, void* __restrict__ out) {
+    const float* __restrict__ bias, int E, int N, int K, int min_rows, int chunk, int lo_off,
+    void* __restrict__ out) {
   __shared__ __align__(16) char st0[kMxStage];
   __shared__ __align__(16) char st1[kMxStage];
   __shared__ __align__(16) char st2[kMxStage];
@@ -868,6 +915,7 @@ __global__ __launch_bounds__(512) void moe_mx_gemm_kernel(
   c.N = N;
   c.K = K;
   c.as_row = mx_act_scale_row_bytes(K);
+  c.lo_off = lo_off;
   const int tid = threadIdx.x;
   c.lane = tid & 63;
   c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -876,10 +924,12 @@ __global__ __launch_bounds__(512) void moe_mx_gemm_kernel(
   c.tile_bytes = (size_t)c.gm.G * 256;
   c.wbase = packed + (size_t)c.e * c.gm.NT * c.tile_bytes + c.lane * 16;
   c.sbase = packed + c.gm.data_bytes + (size_t)c.e * c.gm.NT * c.gm.KG4 * 256 + c.lane * 4;
-  // passes of 128 rows; the last takes 64 when they suffice
-  for (int m0 = 0; m0 < n_e; m0 += 128) {
-    const int rows = min(128, n_e - m0);
-    if (rows > 64) mx_gemm_pass<GATE_UP, 8>(c, st0, st1, st2, st3, m0, rows);
+  // passes of 96 rows (6 row tiles, each with its high and low term); the last takes the fewest 32-row
+  // multiples that hold its rows
+  for (int m0 = 0; m0 < n_e; m0 += 96) {
+    const int rows = min(96, n_e - m0);
+    if (rows > 64) mx_gemm_pass<GATE_UP, 12>(c, st0, st1, st2, st3, m0, rows);
+    else if (rows > 32) mx_gemm_pass<GATE_UP, 8>(c, st0, st1, st2, st3, m0, rows);
     else mx_gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, m0, rows);
   }
 }
@@ -996,7 +1046,7 @@ int launch_moe_gate_up_fp8act(const uint16_t* x, const uint8_t* xq, const uint8_
   if (dense || H > 4064) {
     const int chunk = gemm_chunk(gm, E);
     hipLaunchKernelGGL((moe_mx_gemm_kernel<true>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s, xq, xs, perm,
-                       offsets, k_top, w13, b13, E, 2 * I, H, H > 4064 ? 1 : kDenseFrom + 1, chunk, (void*)h);
+                       offsets, k_top, w13, b13, E, 2 * I, H, H > 4064 ? 1 : kDenseFrom + 1, chunk, T, (void*)h);
     return check_launch("moe_gate_up_mxfp4(scaled mfma)");
   }
   return FLYAI_OK;
@@ -1018,7 +1068,7 @@ int launch_moe_down_fp8act(const uint16_t* h, const uint8_t* hq, const uint8_t* 
   if (dense || I > 4064) {
     const int chunk = gemm_chunk(gm, E);
     hipLaunchKernelGGL((moe_mx_gemm_kernel<false>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s, hq, hs, nullptr,
-                       offsets, 1, w2, b2, E, H, I, I > 4064 ? 1 : kDenseFrom + 1, chunk, (void*)y);
+                       offsets, 1, w2, b2, E, H, I, I > 4064 ? 1 : kDenseFrom + 1, chunk, rows_total, (void*)y);
     return check_launch("moe_down_mxfp4(scaled mfma)");
   }
   return FLYAI_OK;

@@ -156,21 +156,22 @@ def moe_down(h, offsets, w2_packed, b2, n_experts, hidden):
 
 
 def mx_act_quant(x):
-    """bf16 [M, K] -> (fp8 e4m3 bytes u8 [M, K], E8M0 scale bytes u8 [M, row bytes] in MFMA order)."""
+    """bf16 [M, K] -> the two-term e4m3 form: (bytes u8 [2M, K], E8M0 scale bytes u8 [2M, row bytes] in
+    MFMA order); row r holds the high term of x[r], row M + r its low term."""
     M, K = x.shape
     _need(x, torch.bfloat16, (M, K), "x")
-    q = torch.empty(M, K, dtype=torch.uint8, device=x.device)
-    s = torch.empty(int(lib().flyai_mx_act_scale_bytes(M, K)), dtype=torch.uint8, device=x.device)
+    q = torch.empty(2 * M, K, dtype=torch.uint8, device=x.device)
+    s = torch.empty(int(lib().flyai_mx_act_scale_bytes(2 * M, K)), dtype=torch.uint8, device=x.device)
     check(lib().flyai_mx_act_quant(_ptr(x), M, K, _ptr(q), _ptr(s), _stream()))
-    return q, s.view(M, -1) if M else s.view(0, 0)
+    return q, s.view(2 * M, -1) if M else s.view(0, 0)
 
 
 def moe_gate_up_fp8act(x, xq, xs, perm, offsets, k, w13_packed, b13, n_experts, inter):
-    """gate_up with the dense groups on the scaled MFMA (fp8 activations xq/xs = mx_act_quant(x))."""
+    """gate_up with the dense groups on the scaled MFMA (two-term fp8 activations xq/xs = mx_act_quant(x))."""
     T, H = x.shape
     _need(x, torch.bfloat16, (T, H), "x")
-    _need(xq, torch.uint8, (T, H), "xq")
-    _need(xs, torch.uint8, (T, int(lib().flyai_mx_act_scale_bytes(1, H))), "xs")
+    _need(xq, torch.uint8, (2 * T, H), "xq")
+    _need(xs, torch.uint8, (2 * T, int(lib().flyai_mx_act_scale_bytes(1, H))), "xs")
     _need(perm, torch.int32, (T * k,), "perm")
     _need(offsets, torch.int32, (n_experts + 1,), "offsets")
     _need(b13, torch.float32, (n_experts, 2 * inter), "b13")
@@ -183,11 +184,11 @@ def moe_gate_up_fp8act(x, xq, xs, perm, offsets, k, w13_packed, b13, n_experts, 
 
 
 def moe_down_fp8act(h, hq, hs, offsets, w2_packed, b2, n_experts, hidden):
-    """down with the dense groups on the scaled MFMA (fp8 activations hq/hs = mx_act_quant(h))."""
+    """down with the dense groups on the scaled MFMA (two-term fp8 activations hq/hs = mx_act_quant(h))."""
     P, I = h.shape
     _need(h, torch.bfloat16, (P, I), "h")
-    _need(hq, torch.uint8, (P, I), "hq")
-    _need(hs, torch.uint8, (P, int(lib().flyai_mx_act_scale_bytes(1, I))), "hs")
+    _need(hq, torch.uint8, (2 * P, I), "hq")
+    _need(hs, torch.uint8, (2 * P, int(lib().flyai_mx_act_scale_bytes(1, I))), "hs")
     _need(offsets, torch.int32, (n_experts + 1,), "offsets")
     _need(b2, torch.float32, (n_experts, hidden), "b2")
     _need(w2_packed, torch.uint8, (mxfp4_packed_bytes(n_experts, hidden, I),), "w2_packed")

@@ -129,14 +129,16 @@ int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, int32_t rows
  * fp8 e4m3 activations and the packed E2M1 weights, each with its E8M0 per-32 scales applied inside the
  * MFMA (the reference's fp8-activation x fp4-weight GEMM, vendor/deepseek_v4_ref/inference/kernel.py:
  * 441-449, with the activations on 32-blocks); decode-sized groups take the bf16 row-pass kernel on x
- * (h) as before.  flyai_mx_act_quant quantises bf16 rows x [M, K] (K % 32 == 0): per row per 32-block
- * s = 2^ceil(log2(max(amax, 1e-4) / 448)), q[M, K] = e4m3 RNE of clamp(x / s, -448, 448); the scale
- * bytes s_e8m0 (flyai_mx_act_scale_bytes(M, K) bytes) are stored per row as 16 * ceil(ceil(K/128)/4)
- * bytes in MFMA order: byte 4 * (4 * kg4 + g) + i holds the scale of block 4 * (4 * kg4 + i) + g, 127
- * past K.  gate_up reads x (bf16) and xq/xs = flyai_mx_act_quant(x) for the same rows; down reads h and
- * hq/hs = flyai_mx_act_quant(h).  Results differ from the bf16 path by the fp8 rounding of the dense
- * groups' activations (per-32 relative error <= 2^-4), so a row's result depends on whether its expert's
- * group is dense. */
+ * (h) as before.  Each activation row is carried as two e4m3 terms, so the products keep the bf16
+ * operand's 8 significant bits: flyai_mx_act_quant quantises bf16 rows x [M, K] (K % 32 == 0) into
+ * q [2M, K] and scale rows s_e8m0 [2M] (flyai_mx_act_scale_bytes(2M, K) bytes).  Row r is the high term:
+ * per 32-block s1 = 2^ceil(log2(max(amax, 1e-4) / 448)), q1 = e4m3 RNE of clamp(x / s1, -448, 448);
+ * row M + r is the low term, the same rule on the exact residual x - s1 q1.  Scale bytes are stored per
+ * row as 16 * ceil(ceil(K/128)/4) bytes in MFMA order: byte 4 * (4 * kg4 + g) + i holds the scale of
+ * block 4 * (4 * kg4 + i) + g, 127 past K.  gate_up reads x (bf16) and xq/xs = flyai_mx_act_quant(x)
+ * for the same T rows (2T rows of xq and xs); down reads h and hq/hs = flyai_mx_act_quant(h) (2 * rows).
+ * Each dense product is the sum of the two terms' products in fp32, so results match the bf16 path to
+ * fp32 accumulation order, not bit for bit. */
 size_t flyai_mx_act_scale_bytes(int32_t M, int32_t K);
 int flyai_mx_act_quant(const uint16_t* x, int32_t M, int32_t K, uint8_t* q, uint8_t* s_e8m0,
                        flyai_stream_t stream);

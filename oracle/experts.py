@@ -128,18 +128,34 @@ def act_quant_128(x):
     return act_quant_blocks(x, 128)
 
 
-def mx_fp8_roundtrip(x):
-    """x fp32 [M, K] (K % 32 == 0) -> the fp32 values an fp8 e4m3 activation operand with one E8M0
-    scale per 32 values carries: q * s from act_quant_blocks(x, 32) (exact in fp32)."""
-    q, s = act_quant_blocks(x, 32)
+def _dequant_blocks(q, s, block=32):
     M, K = q.shape
-    return (q.reshape(M, K // 32, 32) * s[:, :, None]).reshape(M, K).astype(np.float32)
+    return (q.reshape(M, K // block, block) * s[:, :, None]).reshape(M, K).astype(np.float32)
+
+
+def mx_act_quant_two_term(x):
+    """x fp32 [M, K] (K % 32 == 0) -> the two-term e4m3 form of the dense groups' activation operand:
+    (q1, s1, q2, s2), the high term act_quant_blocks(x, 32) and the low term the same rule on the
+    residual x - q1 s1 (exact in fp32: q1 s1 is x rounded to 4 significant bits).  q* hold e4m3 values
+    as fp32, s* the power-of-two scales per 32-block."""
+    x = np.asarray(x, dtype=np.float32)
+    q1, s1 = act_quant_blocks(x, 32)
+    r = (x - _dequant_blocks(q1, s1)).astype(np.float32)
+    q2, s2 = act_quant_blocks(r, 32)
+    return q1, s1, q2, s2
+
+
+def mx_fp8_roundtrip(x):
+    """x fp32 [M, K] (K % 32 == 0) -> the fp32 values the two-term e4m3 activation operand (one E8M0 scale
+    per 32 values per term) carries: q1 s1 + q2 s2 from mx_act_quant_two_term (exact in fp32)."""
+    q1, s1, q2, s2 = mx_act_quant_two_term(x)
+    return (_dequant_blocks(q1, s1) + _dequant_blocks(q2, s2)).astype(np.float32)
 
 
 def experts_mxfp4_fp8act(x, perm, offsets, k, wts: MxExpertWeights, return_h=False):
-    """experts_mxfp4 with both activation operands carried as fp8 e4m3 + per-32 E8M0 scales (the
-    dense groups' scaled-MFMA path): the gathered x rows and the bf16 intermediate h each pass through
-    mx_fp8_roundtrip before their product with the MXFP4 weights, the precedent being the
+    """experts_mxfp4 with both activation operands carried in the two-term e4m3 form with per-32 E8M0
+    scales (the dense groups' scaled-MFMA path): the gathered x rows and the bf16 intermediate h each
+    pass through mx_fp8_roundtrip before their product with the MXFP4 weights, the precedent being the
     reference's fp8-activation x fp4-weight GEMM (vendor/deepseek_v4_ref/inference/kernel.py:441-449,
     activations quantised per block on K with power-of-two scales).  Everything else as
     experts_mxfp4: fp32 bias, SwiGLU, bf16 h, fp32 y."""

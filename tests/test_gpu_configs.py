@@ -126,12 +126,9 @@ def test_c1_workload_layers_vs_oracle_and_batch_invariance():
 
 @pytest.mark.parametrize("dense_fp8", [False, True], ids=["bf16-dense", "fp8-dense"])
 def test_c2_workload_layers_vs_oracle(dense_fp8):
-    """With dense_fp8 the dense expert groups run on the scaled MFMA with fp8 activation operands.  On
-    these synthetic weights the MoE output dominates the layer output, so the fp8 rounding of the
-    activations (up to 2^-4 relative per value) shows in it: measured max-abs-rel ~0.05 and cos ~0.9988
-    per layer, outside the north_star bar of 2e-2 / 0.999.  That is why the path is opt-in; the test
-    holds it to max-abs-rel 0.08 and cos 0.998 against the bf16 model math.  The default (bf16) path is
-    held to the north_star bar."""
+    """With dense_fp8 the dense expert groups run on the scaled MFMA with two-term fp8 activation
+    operands (which hold the bf16 activations to 2^-6 of each 32-block's largest value); without it on
+    the bf16 tiled GEMM.  Both are held to the north_star bar against the bf16 model math."""
     from gpu_harness import _SingleLayerKV, cpu_f32, metrics, oracle_layer_params, tokens_with_same_routing
     from flyai_amd.runtime import RaggedStage
     q_lens, starts = bench.c2_batch(0)
@@ -173,11 +170,10 @@ def test_c2_workload_layers_vs_oracle(dense_fp8):
         out = cpu_f32(h).numpy()[rows]
         good = tokens_with_same_routing(ids[rows], tr["ids"], tr["logits"], k)
         mar, c = metrics(out[good], ref.numpy()[good])
-        bar_mar, bar_cos = (0.08, 0.998) if dense_fp8 else (MAR, COS)
         print(f"C2 {'fp8' if dense_fp8 else 'bf16'} dense, layer {l}: max-abs-rel {mar:.4g} cos {c:.6f}")
-        assert mar <= bar_mar and c >= bar_cos, f"C2 layer {l}: max-abs-rel {mar:.3g} cos {c:.6f}"
+        assert mar <= MAR and c >= COS, f"C2 layer {l}: max-abs-rel {mar:.3g} cos {c:.6f}"
         _, c = metrics((out - hin_sub.numpy())[good], (ref.numpy() - hin_sub.numpy())[good])
-        assert c >= (0.997 if dense_fp8 else COS), f"C2 layer {l}: increment cos {c:.6f}"
+        assert c >= COS, f"C2 layer {l}: increment cos {c:.6f}"
         attn = cpu_f32(st.debug_buffer(3, torch.bfloat16, (T, shape.n_q_heads * shape.head_dim))).numpy()[rows]
         mar, c = metrics(attn, tr["attn"].reshape(len(rows), -1).numpy())
         assert mar <= 1e-2 and c >= 0.9999, f"C2 layer {l} attention: {mar:.3g} {c:.6f}"

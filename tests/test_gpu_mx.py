@@ -1,13 +1,14 @@
-"""Dense MXFP4 expert groups on the CDNA4 scaled MFMA (fp8 activations x E2M1 weights).
+"""Dense MXFP4 expert groups on the CDNA4 scaled MFMA (two-term fp8 activations x E2M1 weights).
 
-* flyai_mx_act_quant: bit-exact against the oracle's act_quant_blocks(x, 32) -- every e4m3 byte and
-  every E8M0 scale byte, in the MFMA-ordered scale layout, padding bytes 127.
+* flyai_mx_act_quant: bit-exact against the oracle's mx_act_quant_two_term -- every e4m3 byte and every
+  E8M0 scale byte of both terms (rows 0..M-1 the high term, M..2M-1 the low term), in the MFMA-ordered
+  scale layout, padding bytes 127.
 * gate_up / down with the fp8 activation operand: against oracle.experts_mxfp4_fp8act, which carries
-  the same quantised operands through an fp32 product (the bar: fp32 accumulation order and bf16
-  rounding of h only), and against the bf16 model math (experts_mxfp4) within what the fp8 rounding of
-  the activations allows (cos >= 0.999 for h, 0.998 for y; the layer-level north_star bar is checked at
-  C2).  Groups of 8 rows or fewer keep the bf16 row-pass kernel, so a decode-sized batch gives the
-  bf16 path's exact bits."""
+  the same two-term operands through an fp32 product (the bar: fp32 accumulation order and bf16
+  rounding of h only), and against the bf16 model math (experts_mxfp4) at the north_star bar
+  (max-abs-rel 2e-2, cosine 0.999; the two terms hold the bf16 operand to 2^-6 of each block's largest
+  value, so the measured agreement is far inside it).  Groups of 8 rows or fewer keep the bf16 row-pass
+  kernel, so a decode-sized batch gives the bf16 path's exact bits."""
 import numpy as np
 import pytest
 import torch
@@ -50,11 +51,15 @@ def test_mx_act_quant_bit_exact(M, K):
     x = x.to(torch.bfloat16)
     q, s = ops.mx_act_quant(x)
     torch.cuda.synchronize()
-    rq, rs = oexperts.act_quant_blocks(x.float().cpu().numpy(), 32)
+    assert q.shape == (2 * M, K) and s.shape[0] == 2 * M
+    rq1, rs1, rq2, rs2 = oexperts.mx_act_quant_two_term(x.float().cpu().numpy())
     got_q = q.cpu().view(torch.float8_e4m3fn).float().numpy()
-    assert np.array_equal(got_q, rq), "fp8 activation bytes differ from the oracle"
-    want_s = (np.log2(rs).astype(np.int32) + 127).astype(np.uint8)
-    assert np.array_equal(_unpack_scales(s, K), want_s), "E8M0 scale bytes differ from the oracle"
+    assert np.array_equal(got_q[:M], rq1), "high-term fp8 bytes differ from the oracle"
+    assert np.array_equal(got_q[M:], rq2), "low-term fp8 bytes differ from the oracle"
+    got_s = _unpack_scales(s, K)
+    for name, rs, part in (("high", rs1, got_s[:M]), ("low", rs2, got_s[M:])):
+        want_s = (np.log2(rs).astype(np.int32) + 127).astype(np.uint8)
+        assert np.array_equal(part, want_s), f"{name}-term E8M0 scale bytes differ from the oracle"
     # every byte past the row's last block reads 127 (2^0)
     G, rowb = K // 32, s.shape[1]
     used = {4 * ((blk // 16) * 4 + blk % 4) + (blk // 4) % 4 for blk in range(G)}
@@ -82,7 +87,7 @@ def _moe_case(T, E, seed):
 @pytest.mark.parametrize("T,E", [(128, 8), (320, 4), (600, 32), (12, 128)])
 def test_moe_experts_fp8act_vs_oracle(T, E):
     """(128, 8): 64 rows per expert, one 64-row pass; (320, 4): every token on every expert, passes of
-    128 + 128 + 64 rows; (600, 32): a spread of group sizes, a few under 9 rows on the row-pass kernel;
+    96 + 96 + 96 + 32 rows; (600, 32): a spread of group sizes, a few under 9 rows on the row-pass kernel;
     (12, 128): decode-sized, all groups on the bf16 row-pass kernel (bit-identical to the bf16 path)."""
     from flyai_amd import ops
     shape, m, w13, w2, x, off, perm, wo = _moe_case(T, E, 60 + E)
@@ -108,14 +113,13 @@ def test_moe_experts_fp8act_vs_oracle(T, E):
     assert mar <= 1e-2 and cos >= 0.99999, f"gate_up vs the fp8-activation oracle: {mar:.3g} {cos:.7f}"
     mar, cos = _metrics(yd, ry.numpy()[dense])
     assert mar <= 1e-2 and cos >= 0.99999, f"down vs the fp8-activation oracle: {mar:.3g} {cos:.7f}"
-    # against the bf16 model math the fp8 rounding of the activations (relative error up to 2^-4 per
-    # value) shows: h (x rounded once) within cos 0.999, y (x and h rounded) within cos 0.998, a
-    # max-abs-rel near 0.1 for both; the layer-level bar (residual included) is checked through the
-    # stage at C2 (test_gpu_configs)
+    # against the bf16 model math: the north_star bar on the expert outputs themselves
     mar, cos = _metrics(hd, rh16.numpy()[dense])
-    assert mar <= 0.15 and cos >= 0.999, f"gate_up vs the bf16 model math: {mar:.3g} {cos:.6f}"
+    print(f"T={T} E={E}: gate_up vs bf16 math max-abs-rel {mar:.3g} cos {cos:.7f}")
+    assert mar <= 2e-2 and cos >= 0.999, f"gate_up vs the bf16 model math: {mar:.3g} {cos:.6f}"
     mar, cos = _metrics(yd, ry16.numpy()[dense])
-    assert mar <= 0.15 and cos >= 0.998, f"down vs the bf16 model math: {mar:.3g} {cos:.6f}"
+    print(f"T={T} E={E}: down vs bf16 math max-abs-rel {mar:.3g} cos {cos:.7f}")
+    assert mar <= 2e-2 and cos >= 0.999, f"down vs the bf16 model math: {mar:.3g} {cos:.6f}"
     if (~dense).any():   # small groups stay on the bf16 row-pass kernel
         mar, cos = _metrics(h.float().cpu().numpy()[~dense], rh16.numpy()[~dense])
         assert mar <= 2e-2 and cos >= 0.999

@@ -511,10 +511,38 @@ def test_mx_fp8_roundtrip_is_identity_on_the_grid_with_unit_scales():
     assert np.array_equal(experts.mx_fp8_roundtrip(y), y)
 
 
+def test_two_term_quantiser_brute_force_and_error_bound():
+    """The low term is act_quant_blocks of the residual, computed exactly (fp64 agrees with the fp32
+    difference).  Bounds from the format: a block's largest magnitude maps into (224, 448], where e4m3
+    steps are at most 32, so one term's rounding error is at most 2^-3 of the block's largest value;
+    the low term rounds a residual of at most 2^-3 of it, so the two terms leave at most 2^-6.  The high
+    term alone exceeds 2^-6 on these inputs (a dropped low term fails the two-term bound)."""
+    rng = np.random.default_rng(44)
+    x = rng.standard_normal((6, 128)).astype(np.float32)
+    x *= np.array([1.0, 300.0, 1e-3, 7.0, 0.05, 2.0], dtype=np.float32)[:, None]
+    x = torch.from_numpy(x).to(torch.bfloat16).float().numpy()     # bf16 inputs, as the kernels see
+    x[2, 32:64] = 0.0
+    q1, s1, q2, s2 = experts.mx_act_quant_two_term(x)
+    rq1, rs1 = experts.act_quant_blocks(x, 32)
+    assert np.array_equal(q1, rq1) and np.array_equal(s1, rs1)
+    x1 = (q1.reshape(6, 4, 32).astype(np.float64) * s1[:, :, None]).reshape(6, 128)
+    r64 = x.astype(np.float64) - x1
+    assert np.array_equal(r64.astype(np.float32).astype(np.float64), r64), "residual not exact in fp32"
+    rq2, rs2 = experts.act_quant_blocks(r64.astype(np.float32), 32)
+    assert np.array_equal(q2, rq2) and np.array_equal(s2, rs2)
+    xhat = experts.mx_fp8_roundtrip(x).astype(np.float64)
+    blk_max = np.abs(x).reshape(6, 4, 32).max(axis=2, keepdims=True).repeat(32, axis=2).reshape(6, 128)
+    err2 = np.abs(xhat - x)
+    assert (err2 <= blk_max * 2.0 ** -6 + 1e-30).all()
+    err1 = np.abs(x1 - x)
+    assert (err1 > blk_max * 2.0 ** -6).any(), "the high term alone must not meet the two-term bound"
+    assert (err1 <= blk_max * 2.0 ** -3 + 1e-30).all()
+
+
 def test_experts_fp8act_gate_up_exact_on_grid_inputs_and_down_recomputed():
     """gate_up: inputs already on the fp8 grid with unit scales give exactly experts_mxfp4's h.
-    down: y is recomputed in fp64 from that h quantised by mx_fp8_roundtrip and the down weights
-    dequantised directly -- a dropped quantisation of h, or a bias on the wrong side, fails."""
+    down: y is recomputed in fp64 from that h carried by mx_fp8_roundtrip and the down weights
+    dequantised directly -- a bias on the wrong side fails."""
     E, H, I, k, T = 3, 64, 64, 2, 5
     rng = np.random.default_rng(43)
     grid = np.array(sorted({g for g, _ in _e4m3_grid()}), dtype=np.float32)
@@ -532,7 +560,6 @@ def test_experts_fp8act_gate_up_exact_on_grid_inputs_and_down_recomputed():
     y8, h8 = experts.experts_mxfp4_fp8act(torch.from_numpy(x), perm, offsets, k, w, return_h=True)
     y16, h16 = experts.experts_mxfp4(torch.from_numpy(x), perm, offsets, k, w, return_h=True)
     assert torch.equal(h8, h16)
-    assert not torch.equal(y8, y16)                                 # h itself is re-quantised
     for e in range(E):
         lo, hi = int(offsets[e]), int(offsets[e + 1])
         if hi == lo:

@@ -302,6 +302,70 @@ __device__ __forceinline__ float lane_xor1(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
 }
 
+// Work units of the dense GEMMs: every group of at least min_rows rows is cut into passes of
+// kGemmRows rows, the passes are numbered expert by expert, and unit u is weight-block chunk
+// u % chunks_per_e of pass u / chunks_per_e.  A group of many rows (a hot expert) so spreads its
+// passes over workgroups instead of running them one after another in each of its workgroups.  Every
+// workgroup derives the numbering from offsets[0..E] (an exclusive scan in LDS); the grid is sized for
+// the most passes any routing can give, sum_e ceil(n_e / kGemmRows) <= rows_total / kGemmRows + E, and
+// units past the last pass exit.
+
+struct DenseUnit {
+  int e, m0, rows, row_lo, n_e;
+};
+
+// The unit of this workgroup; false: none (uniform over the workgroup).  pre: E + 1 ints of LDS.  The
+// live units are spread over the 8 XCDs, consecutive ones on one XCD (workgroups are dealt to the XCDs
+// round-robin by index), so that an XCD's L2 serves a pass's activation rows to all its chunks and
+// the units past the live count, which exit, do not leave XCDs idle.
+__device__ __forceinline__ bool dense_unit(const int32_t* __restrict__ offsets, int E, int min_rows,
+                                           int chunks_per_e, int* pre, DenseUnit& u, int& unit) {
+  const int tid = threadIdx.x;
+  if (tid < 64) {  // one wave: 4 experts per lane, scanned in order (E <= 256)
+    int v[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * tid + j;
+      const int n = e < E ? offsets[e + 1] - offsets[e] : 0;
+      v[j] = (n > 0 && n >= min_rows) ? (n + kGemmRows - 1) / kGemmRows : 0;
+      sum += v[j];
+    }
+    int incl = sum;
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(incl, o, 64);
+      if (tid >= o) incl += y;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = 4 * tid + j;
+      if (e < E) pre[e] = run;
+      run += v[j];
+    }
+    if (tid == 63) pre[E] = incl;  // every pass (experts past E add none)
+  }
+  __syncthreads();  // no global load is in flight yet
+  const int live = pre[E] * chunks_per_e;
+  const int per_xcd = (live + 7) / 8;
+  const int slot = (int)(blockIdx.x / 8);
+  unit = (int)(blockIdx.x % 8) * per_xcd + slot;
+  if (slot >= per_xcd || unit >= live) return false;
+  const int p = unit / chunks_per_e;
+  // the expert whose pass range holds p: the largest e with pre[e] <= p (pre is non-decreasing; an
+  // expert with no passes shares its pre with the next, so the largest such e has passes); a fixed
+  // 8-step search covers E <= 256 without a loop
+  int e = 0;
+#pragma unroll
+  for (int step = 128; step > 0; step >>= 1)
+    if (e + step < E && pre[e + step] <= p) e += step;
+  u.e = e;
+  u.row_lo = offsets[e];
+  u.n_e = offsets[e + 1] - u.row_lo;
+  u.m0 = (p - pre[e]) * kGemmRows;
+  u.rows = min(kGemmRows, u.n_e - u.m0);
+  return true;
+}
+
 // what one workgroup of the tiled GEMM works on: an expert, its rows, a chunk of weight blocks
 struct GemmCtx {
   const uint16_t* act;
@@ -535,17 +599,14 @@ __global__ __launch_bounds__(512) void moe_mxfp4_gemm_kernel(
   c.gm = mx_geom(E, N, K);
   const int blocks_per_e = (c.gm.NT + kGemmTiles - 1) / kGemmTiles;
   const int chunks_per_e = (blocks_per_e + chunk - 1) / chunk;
-  // work units (expert, chunk of weight blocks) are spread so that consecutive ones run on one XCD
-  // (workgroups are dealt to the 8 XCDs round-robin): its L2 then serves an expert's rows to all.
-  const int per_xcd = (int)(gridDim.x / 8);
-  const int unit = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-  if (unit >= E * chunks_per_e) return;
-  c.e = unit / chunks_per_e;
+  __shared__ int pass_pre[257];
+  DenseUnit du;
+  int unit = 0;
+  if (!dense_unit(offsets, E, min_rows, chunks_per_e, pass_pre, du, unit)) return;
+  c.e = du.e;
   c.nb0 = (unit % chunks_per_e) * chunk;
   c.nbn = min(chunk, blocks_per_e - c.nb0);  // weight blocks in this chunk
-  c.row_lo = offsets[c.e];
-  const int n_e = offsets[c.e + 1] - c.row_lo;
-  if (n_e <= 0 || n_e < min_rows) return;  // uniform over the workgroup
+  c.row_lo = du.row_lo;
   c.act = act;
   c.perm = perm;
   c.bias = bias;
@@ -561,13 +622,10 @@ __global__ __launch_bounds__(512) void moe_mxfp4_gemm_kernel(
   c.tile_bytes = (size_t)c.gm.G * 256;
   c.wbase = packed + (size_t)c.e * c.gm.NT * c.tile_bytes + c.lane * 16;
   c.sbase = packed + c.gm.data_bytes + (size_t)c.e * c.gm.NT * c.gm.KG4 * 256 + c.lane * 4;
-  // passes of 96 rows; the last one takes the fewest 32-row multiples that hold its rows
-  for (int m0 = 0; m0 < n_e; m0 += kGemmRows) {
-    const int rows = min(kGemmRows, n_e - m0);
-    if (rows > 64) gemm_pass<GATE_UP, 6>(c, st0, st1, st2, st3, m0, rows);
-    else if (rows > 32) gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, m0, rows);
-    else gemm_pass<GATE_UP, 2>(c, st0, st1, st2, st3, m0, rows);
-  }
+  // this unit's pass of 96 rows; a group's last pass takes the fewest 32-row multiples that hold its rows
+  if (du.rows > 64) gemm_pass<GATE_UP, 6>(c, st0, st1, st2, st3, du.m0, du.rows);
+  else if (du.rows > 32) gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, du.m0, du.rows);
+  else gemm_pass<GATE_UP, 2>(c, st0, st1, st2, st3, du.m0, du.rows);
 }
 
 // ---- dense groups on the scaled MFMA: fp8 activations x MXFP4 weights -------------------------------
@@ -896,16 +954,14 @@ __global__ __launch_bounds__(512) void moe_mx_gemm_kernel(
   c.gm = mx_geom(E, N, K);
   const int blocks_per_e = (c.gm.NT + kGemmTiles - 1) / kGemmTiles;
   const int chunks_per_e = (blocks_per_e + chunk - 1) / chunk;
-  // consecutive work units on one XCD (workgroups are dealt to the 8 XCDs round-robin)
-  const int per_xcd = (int)(gridDim.x / 8);
-  const int unit = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
-  if (unit >= E * chunks_per_e) return;
-  c.e = unit / chunks_per_e;
+  __shared__ int pass_pre[257];
+  DenseUnit du;
+  int unit = 0;
+  if (!dense_unit(offsets, E, min_rows, chunks_per_e, pass_pre, du, unit)) return;
+  c.e = du.e;
   c.nb0 = (unit % chunks_per_e) * chunk;
   c.nbn = min(chunk, blocks_per_e - c.nb0);
-  c.row_lo = offsets[c.e];
-  const int n_e = offsets[c.e + 1] - c.row_lo;
-  if (n_e <= 0 || n_e < min_rows) return;  // uniform over the workgroup
+  c.row_lo = du.row_lo;
   c.act = act;
   c.ascale = ascale;
   c.perm = perm;
@@ -924,14 +980,11 @@ __global__ __launch_bounds__(512) void moe_mx_gemm_kernel(
   c.tile_bytes = (size_t)c.gm.G * 256;
   c.wbase = packed + (size_t)c.e * c.gm.NT * c.tile_bytes + c.lane * 16;
   c.sbase = packed + c.gm.data_bytes + (size_t)c.e * c.gm.NT * c.gm.KG4 * 256 + c.lane * 4;
-  // passes of 96 rows (6 row tiles, each with its high and low term); the last takes the fewest 32-row
-  // multiples that hold its rows
-  for (int m0 = 0; m0 < n_e; m0 += 96) {
-    const int rows = min(96, n_e - m0);
-    if (rows > 64) mx_gemm_pass<GATE_UP, 12>(c, st0, st1, st2, st3, m0, rows);
-    else if (rows > 32) mx_gemm_pass<GATE_UP, 8>(c, st0, st1, st2, st3, m0, rows);
-    else mx_gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, m0, rows);
-  }
+  // this unit's pass of 96 rows (6 row tiles, each with its high and low term); a group's last pass takes
+  // the fewest 32-row multiples that hold its rows
+  if (du.rows > 64) mx_gemm_pass<GATE_UP, 12>(c, st0, st1, st2, st3, du.m0, du.rows);
+  else if (du.rows > 32) mx_gemm_pass<GATE_UP, 8>(c, st0, st1, st2, st3, du.m0, du.rows);
+  else mx_gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, du.m0, du.rows);
 }
 
 // Chunk of weight blocks per workgroup: the largest chunk that still gives at least 3 rounds of
@@ -960,9 +1013,9 @@ inline int gemm_chunk(const MxGeom& gm, int E) {
 }
 
 // grid of the tiled GEMM: the work units (expert, chunk of weight blocks) rounded up to 8 XCDs
-inline int gemm_grid(const MxGeom& gm, int E, int chunk) {
+inline int gemm_grid(const MxGeom& gm, int E, int chunk, int rows_total) {
   const int W = (gm.NT + kGemmTiles - 1) / kGemmTiles;
-  const int units = E * ((W + chunk - 1) / chunk);
+  const int units = (E + ceil_div(rows_total, kGemmRows)) * ((W + chunk - 1) / chunk);
   return ((units + 7) / 8) * 8;
 }
 
@@ -991,7 +1044,7 @@ int launch_moe_gate_up(const uint16_t* x, const int32_t* perm, const int32_t* of
   }
   if (dense || H > 4064) {
     const int chunk = gemm_chunk(gm, E);
-    hipLaunchKernelGGL((moe_mxfp4_gemm_kernel<true>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s,
+    hipLaunchKernelGGL((moe_mxfp4_gemm_kernel<true>), dim3(gemm_grid(gm, E, chunk, T * k_top)), dim3(512), 0, s,
                        x, perm, offsets, k_top, w13, b13, E, 2 * I, H, H > 4064 ? 1 : kDenseFrom + 1, chunk,
                        (void*)h);
     return check_launch("moe_gate_up_mxfp4(dense)");
@@ -1013,7 +1066,7 @@ int launch_moe_down(const uint16_t* h, const int32_t* offsets, const uint8_t* w2
   }
   if (dense || I > 4064) {
     const int chunk = gemm_chunk(gm, E);
-    hipLaunchKernelGGL((moe_mxfp4_gemm_kernel<false>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s,
+    hipLaunchKernelGGL((moe_mxfp4_gemm_kernel<false>), dim3(gemm_grid(gm, E, chunk, rows_total)), dim3(512), 0, s,
                        h, nullptr, offsets, 1, w2, b2, E, H, I, I > 4064 ? 1 : kDenseFrom + 1, chunk, (void*)y);
     return check_launch("moe_down_mxfp4(dense)");
   }
@@ -1045,7 +1098,7 @@ int launch_moe_gate_up_fp8act(const uint16_t* x, const uint8_t* xq, const uint8_
   }
   if (dense || H > 4064) {
     const int chunk = gemm_chunk(gm, E);
-    hipLaunchKernelGGL((moe_mx_gemm_kernel<true>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s, xq, xs, perm,
+    hipLaunchKernelGGL((moe_mx_gemm_kernel<true>), dim3(gemm_grid(gm, E, chunk, T * k_top)), dim3(512), 0, s, xq, xs, perm,
                        offsets, k_top, w13, b13, E, 2 * I, H, H > 4064 ? 1 : kDenseFrom + 1, chunk, T, (void*)h);
     return check_launch("moe_gate_up_mxfp4(scaled mfma)");
   }
@@ -1067,7 +1120,7 @@ int launch_moe_down_fp8act(const uint16_t* h, const uint8_t* hq, const uint8_t* 
   }
   if (dense || I > 4064) {
     const int chunk = gemm_chunk(gm, E);
-    hipLaunchKernelGGL((moe_mx_gemm_kernel<false>), dim3(gemm_grid(gm, E, chunk)), dim3(512), 0, s, hq, hs, nullptr,
+    hipLaunchKernelGGL((moe_mx_gemm_kernel<false>), dim3(gemm_grid(gm, E, chunk, rows_total)), dim3(512), 0, s, hq, hs, nullptr,
                        offsets, 1, w2, b2, E, H, I, I > 4064 ? 1 : kDenseFrom + 1, chunk, rows_total, (void*)y);
     return check_launch("moe_down_mxfp4(scaled mfma)");
   }
@@ -1100,8 +1153,8 @@ extern "C" int flyai_moe_gate_up_mxfp4(const uint16_t* x, const int32_t* perm,
                                        const int32_t* offsets, int32_t T, int32_t k,
                                        const uint8_t* w13_packed, const float* b13, int32_t E,
                                        int32_t H, int32_t I, uint16_t* h, flyai_stream_t stream) {
-  FLYAI_REQUIRE(T >= 0 && E > 0 && H > 0 && I > 0 && H % 32 == 0 && (2 * I) % 16 == 0 && k >= 1,
-                "gate_up: need H %% 32 == 0, 2I %% 16 == 0");
+  FLYAI_REQUIRE(T >= 0 && E > 0 && E <= 256 && H > 0 && I > 0 && H % 32 == 0 && (2 * I) % 16 == 0 && k >= 1,
+                "gate_up: need 1 <= E <= 256, H %% 32 == 0, 2I %% 16 == 0");
   FLYAI_REQUIRE(x && perm && offsets && w13_packed && b13 && h, "gate_up: null pointer");
   return launch_moe_gate_up(x, perm, offsets, k, w13_packed, b13, T, E, H, I, h, as_stream(stream));
 }
@@ -1109,8 +1162,8 @@ extern "C" int flyai_moe_gate_up_mxfp4(const uint16_t* x, const int32_t* perm,
 extern "C" int flyai_moe_down_mxfp4(const uint16_t* h, const int32_t* offsets, int32_t rows,
                                     const uint8_t* w2_packed, const float* b2, int32_t E, int32_t H,
                                     int32_t I, float* y_perm, flyai_stream_t stream) {
-  FLYAI_REQUIRE(rows >= 0 && E > 0 && H > 0 && I > 0 && I % 32 == 0 && H % 16 == 0,
-                "down: need I %% 32 == 0, H %% 16 == 0");
+  FLYAI_REQUIRE(rows >= 0 && E > 0 && E <= 256 && H > 0 && I > 0 && I % 32 == 0 && H % 16 == 0,
+                "down: need 1 <= E <= 256, I %% 32 == 0, H %% 16 == 0");
   FLYAI_REQUIRE(h && offsets && w2_packed && b2 && y_perm, "down: null pointer");
   return launch_moe_down(h, offsets, w2_packed, b2, rows, E, H, I, y_perm, as_stream(stream));
 }
@@ -1131,8 +1184,8 @@ extern "C" int flyai_moe_gate_up_mxfp4_fp8act(const uint16_t* x, const uint8_t* 
                                               const int32_t* perm, const int32_t* offsets, int32_t T, int32_t k,
                                               const uint8_t* w13_packed, const float* b13, int32_t E, int32_t H,
                                               int32_t I, uint16_t* h, flyai_stream_t stream) {
-  FLYAI_REQUIRE(T >= 0 && E > 0 && H > 0 && I > 0 && H % 32 == 0 && (2 * I) % 16 == 0 && k >= 1,
-                "gate_up: need H %% 32 == 0, 2I %% 16 == 0");
+  FLYAI_REQUIRE(T >= 0 && E > 0 && E <= 256 && H > 0 && I > 0 && H % 32 == 0 && (2 * I) % 16 == 0 && k >= 1,
+                "gate_up: need 1 <= E <= 256, H %% 32 == 0, 2I %% 16 == 0");
   FLYAI_REQUIRE(x && xq && xs && perm && offsets && w13_packed && b13 && h, "gate_up: null pointer");
   return launch_moe_gate_up_fp8act(x, xq, xs, perm, offsets, k, w13_packed, b13, T, E, H, I, h, as_stream(stream));
 }
@@ -1141,8 +1194,8 @@ extern "C" int flyai_moe_down_mxfp4_fp8act(const uint16_t* h, const uint8_t* hq,
                                            const int32_t* offsets, int32_t rows, const uint8_t* w2_packed,
                                            const float* b2, int32_t E, int32_t H, int32_t I, float* y_perm,
                                            flyai_stream_t stream) {
-  FLYAI_REQUIRE(rows >= 0 && E > 0 && H > 0 && I > 0 && I % 32 == 0 && H % 16 == 0,
-                "down: need I %% 32 == 0, H %% 16 == 0");
+  FLYAI_REQUIRE(rows >= 0 && E > 0 && E <= 256 && H > 0 && I > 0 && I % 32 == 0 && H % 16 == 0,
+                "down: need 1 <= E <= 256, I %% 32 == 0, H %% 16 == 0");
   FLYAI_REQUIRE(h && hq && hs && offsets && w2_packed && b2 && y_perm, "down: null pointer");
   return launch_moe_down_fp8act(h, hq, hs, offsets, w2_packed, b2, rows, E, H, I, y_perm, as_stream(stream));
 }

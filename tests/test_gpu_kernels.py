@@ -175,11 +175,13 @@ def test_combine_matches_oracle():
 
 # ---- a5 / a6 -----------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("T,E", [(12, 128), (128, 8), (3, 4), (320, 4)])
-def test_moe_experts_vs_oracle(T, E):
+@pytest.mark.parametrize("T,E,hot", [(12, 128, None), (128, 8, None), (3, 4, None), (320, 4, None), (600, 16, 5)])
+def test_moe_experts_vs_oracle(T, E, hot):
     """gate_up (+SwiGLU) and down through the packed MXFP4 layout.  (12, 128) and (3, 4) are
     decode-sized (row-pass kernel); (128, 8) averages 64 rows per expert (dense kernel, one pass);
-    (320, 4) puts all 320 tokens on every expert (dense kernel, four passes of up to 96 rows)."""
+    (320, 4) puts all 320 tokens on every expert (dense kernel, four passes of up to 96 rows, each its
+    own work unit); (600, 16, hot 5) biases the router to one expert, which then holds nearly every
+    token (seven passes) beside groups of about 120 rows."""
     from flyai_amd import ops
     from flyai_amd.weights import GptOssShape, synthetic_moe
     shape = GptOssShape(n_experts=E)
@@ -189,8 +191,13 @@ def test_moe_experts_vs_oracle(T, E):
     x = _rms_input(T, shape.hidden, 21)
     rw = (torch.randn(E, shape.hidden, device=DEV, generator=_gen(22)) * 0.02).to(torch.bfloat16)
     rb = torch.zeros(E, dtype=torch.bfloat16, device=DEV)
+    if hot is not None:
+        rb[hot] = 4.0
     ids, wts = ops.router_topk_softmax(x, rw, rb, 4)
     hist, off, perm, inv = ops.moe_permute(ids, E)
+    if hot is not None:
+        hc = hist.cpu().numpy()
+        assert hc[hot] > 5 * 96, hc
     h = ops.moe_gate_up(x, perm, off, 4, w13, m["b13"], E, shape.intermediate)
     y = ops.moe_down(h, off, w2, m["b2"], E, shape.hidden)
     torch.cuda.synchronize()

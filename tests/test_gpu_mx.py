@@ -67,7 +67,7 @@ def test_mx_act_quant_bit_exact(M, K):
     assert (s.cpu().numpy()[:, pad] == 127).all()
 
 
-def _moe_case(T, E, seed):
+def _moe_case(T, E, seed, hot=None):
     from flyai_amd import ops
     from flyai_amd.weights import GptOssShape, synthetic_moe
     shape = GptOssShape(n_experts=E)
@@ -77,6 +77,8 @@ def _moe_case(T, E, seed):
     x = (torch.randn(T, shape.hidden, device=DEV, generator=_gen(seed + 1))).to(torch.bfloat16)
     rw = (torch.randn(E, shape.hidden, device=DEV, generator=_gen(seed + 2)) * 0.02).to(torch.bfloat16)
     rb = torch.zeros(E, dtype=torch.bfloat16, device=DEV)
+    if hot is not None:
+        rb[hot] = 4.0
     ids, wts = ops.router_topk_softmax(x, rw, rb, 4)
     hist, off, perm, inv = ops.moe_permute(ids, E)
     wo = oexperts.MxExpertWeights(*(m[n].cpu().numpy() for n in
@@ -84,13 +86,14 @@ def _moe_case(T, E, seed):
     return shape, m, w13, w2, x, off, perm, wo
 
 
-@pytest.mark.parametrize("T,E", [(128, 8), (320, 4), (600, 32), (12, 128)])
-def test_moe_experts_fp8act_vs_oracle(T, E):
+@pytest.mark.parametrize("T,E,hot", [(128, 8, None), (320, 4, None), (600, 32, None), (12, 128, None), (600, 16, 5)])
+def test_moe_experts_fp8act_vs_oracle(T, E, hot):
     """(128, 8): 64 rows per expert, one 64-row pass; (320, 4): every token on every expert, passes of
     96 + 96 + 96 + 32 rows; (600, 32): a spread of group sizes, a few under 9 rows on the row-pass kernel;
-    (12, 128): decode-sized, all groups on the bf16 row-pass kernel (bit-identical to the bf16 path)."""
+    (12, 128): decode-sized, all groups on the bf16 row-pass kernel (bit-identical to the bf16 path);
+    (600, 16, hot 5): one expert holds nearly every token (seven passes, each its own work unit)."""
     from flyai_amd import ops
-    shape, m, w13, w2, x, off, perm, wo = _moe_case(T, E, 60 + E)
+    shape, m, w13, w2, x, off, perm, wo = _moe_case(T, E, 60 + E, hot)
     I, H = shape.intermediate, shape.hidden
     xq, xs = ops.mx_act_quant(x)
     h = ops.moe_gate_up_fp8act(x, xq, xs, perm, off, 4, w13, m["b13"], E, I)

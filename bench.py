@@ -69,6 +69,31 @@ def c3_batch(seed=0):
     return [int(v) for v in rng.choice([1, 2, 4], size=64)]
 
 
+C4_MAXLEN = 32768
+
+
+def c4_batch(seed=4, S=256):
+    """256 sequences: Zipf(2.2) query lengths capped at 8 (mostly single-token decode, verify chunks up
+    to 8), two of them 1024-token prefill chunks; KV lengths log-uniform in [128, 32768]."""
+    rng = np.random.default_rng(seed)
+    q = np.minimum(rng.zipf(2.2, size=S), 8)
+    prefill = rng.choice(S, size=2, replace=False)
+    q[prefill] = 1024
+    kv = np.exp(rng.uniform(np.log(128), np.log(C4_MAXLEN), size=S)).astype(np.int64)
+    starts = np.maximum(kv - q, 0)
+    return [int(v) for v in q], [int(v) for v in starts], [int(v) for v in prefill]
+
+
+def c4_skew_router(layer, E, seed=9, boost=1.2):
+    """The stress routing: +boost on the router bias of 10% of the experts, which then take about half
+    of the token-assignments."""
+    import torch
+    hot = torch.randperm(E, generator=torch.Generator().manual_seed(seed))[:E // 10]
+    rb = layer.router_b.float()
+    rb[hot.to(rb.device)] += boost
+    layer.router_b = rb.to(torch.bfloat16)
+
+
 def gate_up_algorithmic_bytes(shape, hist, T, k):
     """Touched experts' gate_up codes + scales + fp32 bias, once each, plus x in, h out, perm."""
     H, I = shape.hidden, shape.intermediate
@@ -107,7 +132,7 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="after timing, copy a buffer of this many MiB 3 times (a known-size kernel "
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
-    ap.add_argument("--workload", choices=("c1", "c2", "c3", "wire"), default="c1")
+    ap.add_argument("--workload", choices=("c0", "c1", "c2", "c3", "c4", "wire"), default="c1")
     ap.add_argument("--frames", type=int, default=20, help="--workload wire: frames per path")
     ap.add_argument("--dense", choices=("fp8", "bf16"), default="bf16",
                     help="--workload c2: dense expert groups on the scaled MFMA with two-term fp8 activations "
@@ -120,12 +145,14 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the stage is single-GPU by design: no collectives, no sharding)", file=sys.stderr)
         sys.exit(2)
-    if args.workload == "c3":
+    if args.workload == "c0":
+        run_c0(args)
+    elif args.workload == "c3":
         run_c3(args)
     elif args.workload == "wire":
         run_wire(args)
     else:
-        run_gptoss(args, chunked_prefill=args.workload == "c2")
+        run_gptoss(args, args.workload)
 
 
 # ---- measurement helpers ---------------------------------------------------------------------------
@@ -251,7 +278,7 @@ def timed_median(fn, runs=3, warmup=1):
 
 # ---- GPT-OSS stage (c1, c2) ------------------------------------------------------------------------
 
-def run_gptoss(args, chunked_prefill=False):
+def run_gptoss(args, workload="c1"):
     import torch
     from flyai_amd import ops
     from flyai_amd.rope import YarnRotary
@@ -261,16 +288,26 @@ def run_gptoss(args, chunked_prefill=False):
     dev = "cuda"
     torch.cuda.set_device(0)
     shape = GptOssShape()
-    q_lens, starts = c2_batch(0) if chunked_prefill else c1_batch(0)
+    chunked_prefill = workload in ("c2", "c4")   # prefill-sized expert groups: the MFMA roofline
+    caps = None
+    if workload == "c4":
+        q_lens, starts, _ = c4_batch()
+        caps = [s_ + q_ for s_, q_ in zip(starts, q_lens)]   # a per-sequence workspace, sized to each context
+        maxlen = C4_MAXLEN + 64
+    else:
+        q_lens, starts = c2_batch(0) if workload == "c2" else c1_batch(0)
+        maxlen = 8192 + 64
     S, T = len(q_lens), sum(q_lens)
     E, k = shape.n_experts, shape.top_k
-    maxlen = 8192 + 64
     with_cpu = not args.no_cpu and not chunked_prefill
     print(f"[bench] building {args.layers}-layer stage ...", file=sys.stderr, flush=True)
     layers = [synthetic_layer(shape, 1000 + i, dev, sliding=(i % 2 == 0), keep_hf=(i < 2 and with_cpu))
               for i in range(args.layers)]
+    if workload == "c4":
+        for lw_ in layers:
+            c4_skew_router(lw_, E)
     rot = YarnRotary(maxlen, device=dev)
-    kv = KVWorkspace(args.layers, S, maxlen, shape.n_kv_heads, shape.head_dim, dev)
+    kv = KVWorkspace(args.layers, S, maxlen, shape.n_kv_heads, shape.head_dim, dev, caps=caps)
     g = torch.Generator(device=dev)
     g.manual_seed(7)
     for t in kv.k + kv.v:
@@ -344,8 +381,8 @@ def run_gptoss(args, chunked_prefill=False):
     gu_gbs = gu_bytes / (gu_us * 1e-6) / 1e9
     dn_gbs = dn_bytes / (dn_us * 1e-6) / 1e9
     if chunked_prefill:
-        traffic = committed_traffic("stage_step_c2_fp8_counters.json" if fp8 else "stage_step_c2_counters.json",
-                                    ("moe_mx_gemm_kernel<true>", "moe_mxfp4_kernel<true") if fp8 else
+        prof = f"stage_step_{workload}{'_fp8' if fp8 else ''}_counters.json"
+        traffic = committed_traffic(prof, ("moe_mx_gemm_kernel<true>", "moe_mxfp4_kernel<true") if fp8 else
                                     ("moe_mxfp4_gemm_kernel<true>", "moe_mxfp4_kernel<true"))
     else:
         traffic = committed_traffic("stage_step_c1_counters.json", ("moe_mxfp4_kernel<true",))
@@ -361,7 +398,8 @@ def run_gptoss(args, chunked_prefill=False):
         moe["act_quant_us"] = round(quant_us, 2)
 
     if chunked_prefill:
-        # dense groups (~65 rows per expert): the gate_up GEMM against the MFMA peak of its dtype
+        # dense groups (the prefill chunk: ~65 rows per expert; the stress batch: its hot experts):
+        # gate_up against the MFMA peak
         P = T * k
         flops = 2.0 * P * shape.hidden * 2 * shape.intermediate
         tflops = flops / (gu_us * 1e-6) / 1e12
@@ -371,13 +409,18 @@ def run_gptoss(args, chunked_prefill=False):
             else "mxfp4-e2m1/bf16 (fp32 accumulate)"
         kname = "moe_mx_gemm_kernel<gate_up> (scaled f8f6f4 MFMA)" if fp8 else "moe_mxfp4_gemm_kernel<gate_up>"
         line = {
-            "metric": "stage tokens/sec at a chunked-prefill mixed batch; MoE layer us; % MFMA roofline",
+            "metric": ("stage tokens/sec at a chunked-prefill mixed batch; MoE layer us; % MFMA roofline"
+                       if workload == "c2" else
+                       "stage tokens/sec at a 256-sequence stress batch; MoE layer us; % MFMA roofline"),
             "value": round(value, 2), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
             "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
             "scaling": "weak", "vs_baseline": None, "dtype": dtype,
             "data": "synthetic (seeded random-init weights, N(0,1) KV and activations)",
-            "config": {"workload": "gpt-oss-120b-shaped 9-layer MXFP4 stage, one 2048-token prefill chunk "
-                                   "(prior KV 4096) + 48 decode rows (KV 512-8192)",
+            "config": {"workload": ("gpt-oss-120b-shaped 9-layer MXFP4 stage, one 2048-token prefill chunk "
+                                    "(prior KV 4096) + 48 decode rows (KV 512-8192)") if workload == "c2" else
+                                   ("gpt-oss-120b-shaped 9-layer MXFP4 stage, 256 sequences: Zipf query lengths "
+                                    "(decode, verify up to 8, two 1024-token prefill chunks), KV log-uniform "
+                                    "128-32768 in per-sequence slabs, 10% of experts take ~50% of assignments"),
                        "layers": args.layers, "tokens": T, "sequences": S, "experts": E,
                        "top_k": k, "hidden": shape.hidden, "parallelism": "single GPU", "step_launch": step_launch,
                        "dense_path": args.dense},
@@ -462,6 +505,92 @@ def cpu_baseline(inp, q_lens, starts, maxlen, n_layers):
                       f"layer 1 (full attention, median {med[1]:.2f} s) of the same {T}-token batch, warmup + "
                       f"median of 3 each; stage = {n_sliding} x sliding + {n_layers - n_sliding} x full = "
                       f"{stage_s:.2f} s"}
+
+
+# ---- one GPT-OSS MoE block on the 12-token ragged batch (c0) ----------------------------------------
+
+def run_c0(args):
+    """The MoE block (RMSNorm'd input -> router top-4 -> permute -> gate_up -> down -> combine) on
+    sequences of 1, 1, 3 and 7 tokens; a step is one block.  E2M1 codes uniform, E8M0 scale bytes
+    119..123 (2^-8..2^-4), bf16 N(0,1) activations; the CPU oracle runs the same block."""
+    import torch
+    from flyai_amd import ops
+    from flyai_amd.weights import GptOssShape, synthetic_moe
+    dev = "cuda"
+    torch.cuda.set_device(0)
+    shape = GptOssShape()
+    E, k, H, I = shape.n_experts, shape.top_k, shape.hidden, shape.intermediate
+    q_lens = [1, 1, 3, 7]
+    T = sum(q_lens)
+
+    def gen(seed):
+        g_ = torch.Generator(device=dev)
+        g_.manual_seed(seed)
+        return g_
+    m = synthetic_moe(shape, gen(0), dev)
+    w13 = ops.mxfp4_repack(m["w13_blocks"], m["w13_scales"])
+    w2 = ops.mxfp4_repack(m["w2_blocks"], m["w2_scales"])
+    x = torch.randn(T, H, device=dev, generator=gen(1)).to(torch.bfloat16)
+    lnw = torch.ones(H, device=dev)
+    rw = (torch.randn(E, H, device=dev, generator=gen(2)) * 0.02).to(torch.bfloat16)
+    rb = (torch.randn(E, device=dev, generator=gen(3)) * 0.02).to(torch.bfloat16)
+    xn = ops.rmsnorm(x, lnw)
+    resid = x.clone()
+
+    def block():
+        ids, wts, _, off, perm, inv = ops.moe_route_permute(xn, rw, rb, k)
+        h = ops.moe_gate_up(xn, perm, off, k, w13, m["b13"], E, I)
+        y = ops.moe_down(h, off, w2, m["b2"], E, H)
+        ops.moe_combine(y, inv, wts, residual=resid, out=resid)
+    for _ in range(args.warmup + 20):
+        block()
+    torch.cuda.synchronize()
+    us = hip_event_us(block, max(args.steps, 100))
+    _, _, hist, _, _, _ = ops.moe_route_permute(xn, rw, rb, k)
+    hist_np = hist.cpu().numpy()
+    moe_bytes = moe_layer_algorithmic_bytes(shape, hist_np, T, k)
+    gbs = moe_bytes / (us * 1e-6) / 1e9
+    traffic = committed_traffic("moe_block_c0_counters.json", ("moe_mxfp4_kernel<true", "moe_mxfp4_kernel<false"))
+    ceiling = hbm_read_ceiling(args.read_probe_mib, dev)
+    copy_probe(args.copy_probe_mib, dev)
+    cpu = None
+    if not args.no_cpu:
+        from oracle import experts as oexperts
+        from oracle import routing as oroute
+        threads = cpu_threads()
+        torch.set_num_threads(threads)
+        wo = oexperts.MxExpertWeights(*(m[n].cpu().numpy() for n in
+                                        ("w13_blocks", "w13_scales", "b13", "w2_blocks", "w2_scales", "b2")))
+        xc, rwc, rbc, xres = xn.float().cpu(), rw.float().cpu(), rb.float().cpu(), x.float().cpu()
+
+        def cpu_block():
+            rids, rwts, _ = oroute.gptoss_route(xc, rwc, rbc, k)
+            _, roff, rperm, rinv = oroute.permute(rids, E)
+            ry = oexperts.experts_mxfp4(xc, rperm, roff, k, wo)
+            oroute.combine(ry, rinv, rwts, residual=xres)
+        print(f"[bench] cpu oracle: the MoE block, {threads} threads", file=sys.stderr, flush=True)
+        med, _ = timed_median(cpu_block)
+        cpu = {"value": round(T / med, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+               "cpu": cpu_model(), "host_cpus": os.cpu_count(),
+               "sample": f"CPU oracle (torch fp32 + numpy) on the whole block, warmup + median of 3: {med:.2f} s"}
+    line = {
+        "metric": "MoE layer us (one GPT-OSS MoE block, ragged batch of 4 sequences); % HBM roofline",
+        "value": round(T / (us * 1e-6), 2), "unit": "tokens/s", "n_gpus": 1, "steps": max(args.steps, 100),
+        "warmup": args.warmup + 20, "ms_per_step": round(us / 1e3, 5), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "mxfp4-e2m1/bf16 (fp32 accumulate)",
+        "data": "synthetic (E2M1 codes uniform, E8M0 scale bytes 119..123, N(0,1) activations RMS-normed)",
+        "config": {"workload": "one gpt-oss-120b-shaped MXFP4 MoE block (128 experts, top-4, H = I = 2880), "
+                               "sequences of 1, 1, 3 and 7 tokens", "tokens": T, "sequences": len(q_lens),
+                   "experts": E, "top_k": k, "hidden": H, "parallelism": "single GPU"},
+        "moe_layer_us": round(us, 2),
+        "roofline": {"bound": "hbm", "kernel": "MoE block (route + permute + gate_up + down + combine)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "algorithmic_bytes": moe_bytes,
+                     "avg_us": round(us, 2), "experts_touched": int((hist_np > 0).sum())},
+        "hbm_read_ceiling": ceiling,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
 
 
 # ---- DeepSeek-V3-shaped FP8 stage (c3) ------------------------------------------------------------

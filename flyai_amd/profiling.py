@@ -184,6 +184,11 @@ def counter_table(pmc_dirs, trace_dir, match, copy_mib, n_cu):
                "avg_us": (sum(ds) / len(ds) / 1e3) if ds else None}
         for c, v in row.items():
             ent[c] = sum(v) / len(v)
+        wave_cyc = ent.get("SQ_WAVE_CYCLES")
+        if wave_cyc:
+            for c, k in (("SQ_WAIT_INST_LDS", "lds_issue_wait_frac"), ("SQ_WAIT_ANY", "wait_any_frac")):
+                if c in ent:
+                    ent[k] = ent[c] / wave_cyc
         if ent["avg_us"]:
             by = ent.get("FETCH_SIZE_bytes", 0.0) + ent.get("WRITE_SIZE_bytes", 0.0)
             if by:
@@ -201,7 +206,9 @@ def counter_markdown(ents, title, commands):
             ("hbm_GBps", "HBM GB/s", "{:.0f}"), ("TA_TA_BUSY_sum_frac", "TA busy", "{:.0%}"),
             ("TCP_PENDING_STALL_CYCLES_sum_frac", "L1 pending stall", "{:.0%}"),
             ("TCP_TCC_READ_REQ_sum", "L1->L2 reads", "{:.3g}"), ("MfmaUtil", "MfmaUtil %", "{:.1f}"),
-            ("mfma_TFLOPs", "MFMA TFLOP/s", "{:.0f}"), ("SQ_LDS_BANK_CONFLICT", "LDS conflict cyc", "{:.3g}")]
+            ("mfma_TFLOPs", "MFMA TFLOP/s", "{:.0f}"), ("LdsUtil", "LdsUtil %", "{:.1f}"),
+            ("SQ_LDS_BANK_CONFLICT", "LDS conflict cyc", "{:.3g}"),
+            ("lds_issue_wait_frac", "LDS issue wait", "{:.0%}"), ("wait_any_frac", "waiting", "{:.0%}")]
     cols = [c for c in cols if any(c[0] in e and e[c[0]] is not None for e in ents)]
     scale = {"FETCH_SIZE_bytes": 1e-6, "WRITE_SIZE_bytes": 1e-6}
     lines = [f"# {title}", "", "Commands (repo root, ``cd /tmp && export TMPDIR=/tmp`` first):", ""]
@@ -224,6 +231,7 @@ PMC_PASSES = (
     ("WRITE_SIZE",),
     ("TA_TA_BUSY_sum", "TCP_PENDING_STALL_CYCLES_sum", "TCP_TCC_READ_REQ_sum", "GRBM_GUI_ACTIVE"),
     ("MfmaUtil", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_INSTS_VALU_MFMA_MOPS_F8", "SQ_INSTS_VALU_MFMA_MOPS_F6F4"),
+    ("LdsUtil", "SQ_LDS_BANK_CONFLICT", "SQ_WAIT_INST_LDS", "SQ_WAIT_ANY", "SQ_WAVE_CYCLES"),
 )
 STAGE_KERNELS = ("moe_", "attn_", "gemm_", "rmsnorm", "qkv_", "pack_", "act_quant", "route", "router",
                  "combine", "mx_", "fp8", "linear_", "grouped_")

@@ -28,43 +28,56 @@ def _round_up(v, m):
 
 
 class KVWorkspace:
-    """Per-layer K/V pools holding ``n_slots`` sequence slabs of ``cap`` positions each, in the tiled
-    layout of ``flyai_amd.kvlayout`` (what the attention kernel streams)."""
+    """Per-layer K/V pools holding ``n_slots`` sequence slabs in the tiled layout of
+    ``flyai_amd.kvlayout`` (what the attention kernel streams).  Every slab holds ``maxlen`` positions,
+    or slot i holds ``caps[i]`` (a per-sequence workspace sized to each sequence's context); a slab's
+    capacity is rounded up to a multiple of 64 positions."""
 
-    def __init__(self, n_layers, n_slots, maxlen, n_kv_heads=8, head_dim=64, device="cuda"):
+    def __init__(self, n_layers, n_slots, maxlen, n_kv_heads=8, head_dim=64, device="cuda", caps=None):
         if head_dim != kvlayout.HEAD_DIM:
             raise ValueError("the tiled KV layout needs head_dim 64")
+        if caps is None:
+            caps = [maxlen] * n_slots
+        if len(caps) != n_slots or min(caps) < 1:
+            raise ValueError("caps needs one positive capacity per slot")
         self.n_layers, self.n_slots = n_layers, n_slots
-        self.cap = _round_up(max(maxlen, 64), 64)
-        self.maxlen = maxlen
+        self.maxlens = [int(c) for c in caps]
+        self.caps = [_round_up(max(int(c), 64), 64) for c in caps]
+        self.maxlen = max(self.maxlens)
+        self.cap = max(self.caps)
         self.n_kv_heads, self.head_dim = n_kv_heads, head_dim
-        self.slab = n_kv_heads * self.cap * head_dim
-        n = n_slots * self.slab
+        self.slabs = [n_kv_heads * c * head_dim for c in self.caps]
+        self.bases = np.concatenate([[0], np.cumsum(self.slabs)]).astype(np.int64)
+        self.slab = self.slabs[0]
+        n = int(self.bases[-1])
         self.k = [torch.zeros(n, dtype=torch.bfloat16, device=device) for _ in range(n_layers)]
         self.v = [torch.zeros(n, dtype=torch.bfloat16, device=device) for _ in range(n_layers)]
 
     def base(self, slot):
-        return slot * self.slab
+        return int(self.bases[slot])
+
+    def slot_cap(self, slot):
+        return self.caps[slot]
 
     def zero(self):
         for t in self.k + self.v:
             t.zero_()
 
     def _slab(self, pools, layer, slot):
-        return pools[layer][self.base(slot):self.base(slot) + self.slab]
+        return pools[layer][self.base(slot):self.base(slot) + self.slabs[slot]]
 
     def k_dense(self, layer, slot, positions=None):
         """Dense [Hkv, P, 64] copy of one slot's keys (all cap positions by default)."""
-        return kvlayout.gather(self._slab(self.k, layer, slot), self.n_kv_heads, self.cap, "k", positions)
+        return kvlayout.gather(self._slab(self.k, layer, slot), self.n_kv_heads, self.caps[slot], "k", positions)
 
     def v_dense(self, layer, slot, positions=None):
         """Dense [Hkv, P, 64] copy of one slot's values."""
-        return kvlayout.gather(self._slab(self.v, layer, slot), self.n_kv_heads, self.cap, "v", positions)
+        return kvlayout.gather(self._slab(self.v, layer, slot), self.n_kv_heads, self.caps[slot], "v", positions)
 
     def set_dense(self, layer, slot, k, v, positions=None):
         """Write dense [Hkv, P, 64] keys and values into one slot."""
-        kvlayout.scatter(self._slab(self.k, layer, slot), self.n_kv_heads, self.cap, "k", k, positions)
-        kvlayout.scatter(self._slab(self.v, layer, slot), self.n_kv_heads, self.cap, "v", v, positions)
+        kvlayout.scatter(self._slab(self.k, layer, slot), self.n_kv_heads, self.caps[slot], "k", k, positions)
+        kvlayout.scatter(self._slab(self.v, layer, slot), self.n_kv_heads, self.caps[slot], "v", v, positions)
 
     def move_positions(self, layer, slot, src, dst):
         """K/V rows at positions src -> positions dst (all read before any is written)."""
@@ -72,7 +85,7 @@ class KVWorkspace:
         self.set_dense(layer, slot, k, v, dst)
 
     def copy_slot(self, dst, src_ws, src_slot=0):
-        if src_ws.cap != self.cap or src_ws.n_kv_heads != self.n_kv_heads:
+        if src_ws.caps[src_slot] != self.caps[dst] or src_ws.n_kv_heads != self.n_kv_heads:
             raise ValueError("load_prefix needs workspaces of the same capacity and heads")
         for l in range(self.n_layers):
             self._slab(self.k, l, dst).copy_(src_ws._slab(src_ws.k, l, src_slot))
@@ -86,8 +99,8 @@ class RaggedStage:
                  max_attn_items=None, split_keys=1024, device="cuda", use_graphs=False, prefill_min=32,
                  dense_fp8=False):
         """dense_fp8: expert groups large enough for the dense kernels run on the scaled f8f6f4 MFMA with
-        fp8 activation operands (faster on prefill-sized batches, within the fp8 rounding of the
-        activations); the default keeps them on bf16 activations, bit-identical to the decode path."""
+        two-term fp8 activation operands (within fp32 accumulation order of the bf16 path, slower on
+        groups of a 2048-token prefill chunk); the default keeps them on bf16 activations, bit-identical to the decode path."""
         self.shape, self.layers, self.rotary, self.kv = shape, layers, rotary, kv
         self.device = torch.device(device)
         self.max_tokens, self.max_seqs = max_tokens, max_seqs
@@ -179,11 +192,12 @@ class RaggedStage:
         ql = np.ascontiguousarray(q_lens, dtype=np.int32)
         st = np.ascontiguousarray(starts, dtype=np.int32)
         base = np.ascontiguousarray([self.kv.base(int(s)) for s in slots], dtype=np.int64)
-        cap = np.full(S, self.kv.cap, dtype=np.int32)
+        cap = np.ascontiguousarray([self.kv.slot_cap(int(s)) for s in slots], dtype=np.int32)
+        lim = np.asarray([self.kv.maxlens[int(s)] for s in slots], dtype=np.int64)
         need = st.astype(np.int64) + ql
-        if np.any(need > self.kv.maxlen):
-            b = int(np.argmax(need > self.kv.maxlen))
-            raise ContextOverflow(_lib.FLYAI_ERANGE, f"sequence {b} needs {int(need[b])} positions > max_ctx {self.kv.maxlen}")
+        if np.any(need > lim):
+            b = int(np.argmax(need > lim))
+            raise ContextOverflow(_lib.FLYAI_ERANGE, f"sequence {b} needs {int(need[b])} positions > max_ctx {int(lim[b])}")
         check(lib().flyai_stage_forward(
             self._h, ql.ctypes.data_as(C.c_void_p), st.ctypes.data_as(C.c_void_p),
             base.ctypes.data_as(C.c_void_p), cap.ctypes.data_as(C.c_void_p), S,
@@ -204,7 +218,7 @@ class RaggedStage:
         de = np.ascontiguousarray(dep, dtype=np.int32)
         check(lib().flyai_stage_forward_tree(
             self._h, int(start), M, pa.ctypes.data_as(C.c_void_p), de.ctypes.data_as(C.c_void_p),
-            self.kv.base(int(slot)), self.kv.cap, C.c_void_p(hidden.data_ptr()),
+            self.kv.base(int(slot)), self.kv.slot_cap(int(slot)), C.c_void_p(hidden.data_ptr()),
             C.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)))
         return hidden
 

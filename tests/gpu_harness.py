@@ -99,10 +99,14 @@ class _SingleLayerKV:
     def __init__(self, kv, layer):
         self.k, self.v = [kv.k[layer]], [kv.v[layer]]
         self.cap, self.maxlen, self.n_slots = kv.cap, kv.maxlen, kv.n_slots
+        self.caps, self.maxlens, self.bases = kv.caps, kv.maxlens, kv.bases
         self.slab, self.n_kv_heads, self.head_dim = kv.slab, kv.n_kv_heads, kv.head_dim
 
     def base(self, slot):
-        return slot * self.slab
+        return int(self.bases[slot])
+
+    def slot_cap(self, slot):
+        return self.caps[slot]
 
 
 def tokens_with_same_routing(ids, ref_ids, ref_logits, k):

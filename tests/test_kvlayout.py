@@ -59,3 +59,22 @@ def test_pack_gather_scatter_roundtrip():
     v = torch.randn(2, Hkv, cap, 64, generator=g)
     vflat = kvlayout.pack(v, "v")
     assert torch.equal(kvlayout.gather(vflat[1], Hkv, cap, "v"), v[1])
+
+
+def test_workspace_with_per_slot_capacities():
+    """A per-sequence workspace: slot i holds caps[i] positions (rounded up to 64), slabs back to back;
+    dense writes and reads go through each slot's own capacity."""
+    import torch
+    from flyai_amd.runtime import KVWorkspace
+    kv = KVWorkspace(2, 3, 0, 2, 64, device="cpu", caps=[100, 64, 200])
+    assert kv.caps == [128, 64, 256] and kv.maxlens == [100, 64, 200] and kv.cap == 256
+    assert [kv.base(s) for s in range(3)] == [0, 2 * 128 * 64, 2 * (128 + 64) * 64]
+    assert kv.k[0].numel() == 2 * (128 + 64 + 256) * 64
+    g = torch.Generator().manual_seed(3)
+    for slot, n in ((0, 100), (2, 200)):
+        k = torch.randn(2, n, 64, generator=g).to(torch.bfloat16)
+        v = torch.randn(2, n, 64, generator=g).to(torch.bfloat16)
+        kv.set_dense(1, slot, k, v, positions=list(range(n)))
+        assert torch.equal(kv.k_dense(1, slot, positions=list(range(n))), k)
+        assert torch.equal(kv.v_dense(1, slot, positions=list(range(n))), v)
+    assert kv.k[1][kv.base(1):kv.base(2)].abs().sum() == 0      # slot 1 untouched

@@ -86,7 +86,7 @@ __device__ __forceinline__ float swiglu_gptoss(float gate, float up) {
   // modeling_gpt_oss.py:82-88: gate clamped above at 7, up clamped to [-7, 7]
   const float g = fminf(gate, 7.0f);
   const float u = fminf(fmaxf(up, -7.0f), 7.0f);
-  const float glu = g * (1.0f / (1.0f + __expf(-1.702f * g)));
+  const float glu = g * __builtin_amdgcn_rcpf(1.0f + __expf(-1.702f * g));
   return (u + 1.0f) * glu;
 }
 
@@ -379,15 +379,36 @@ struct GemmCtx {
   int k_top, N, K, e, nb0, nbn, row_lo, lane, wave, r, g;
 };
 
+// The chunk's bias (nbn blocks of 256 features from block nb0) goes to LDS once per pass, every
+// load before the first store.  The epilogues read it there: a register copy per block would need a
+// global load in the loop, and waiting for it (vector-memory counts complete in issue order) would
+// drain the groups prefetched behind it.
+constexpr int kGemmBiasBlocks = 32;
+__device__ __forceinline__ void stage_chunk_bias(const float* __restrict__ bias, int e, int N, int nb0, int nbn,
+                                                 float (&bias_s)[kGemmBiasBlocks * 256]) {
+  constexpr int kPer = kGemmBiasBlocks * 256 / 512;
+  float v[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = (int)threadIdx.x + j * 512;
+    const int f = nb0 * 256 + i;
+    v[j] = (i < nbn * 256 && f < N) ? bias[(size_t)e * N + f] : 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) bias_s[threadIdx.x + j * 512] = v[j];
+}
+
 // One pass over MT row tiles (16*MT rows from m0) and every block of the chunk.
 template <bool GATE_UP, int MT>
 __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmStage], char (&st1)[kGemmStage],
-                                          char (&st2)[kGemmStage], char (&st3)[kGemmStage], int m0, int rows) {
+                                          char (&st2)[kGemmStage], char (&st3)[kGemmStage],
+                                          float (&bias_s)[kGemmBiasBlocks * 256], int m0, int rows) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) void* lds_ptr;
-  static_assert(MT % 2 == 0 && MT <= 6, "row tiles per pass");
-  constexpr int ABYTES = MT * 4096;                   // activation part of a stage
-  constexpr int LOADS = 2 + 2 + MT / 2;               // weight tiles, scale rows, activation blocks
+  static_assert(MT >= 1 && MT <= 6, "row tiles per pass");
+  constexpr int MD = (MT + 1) / 2;                    // activation DMA instructions (2 row tiles each)
+  constexpr int ABYTES = MD * 8192;                   // activation part of a stage
+  constexpr int LOADS = 2 + 2 + MD;                   // weight tiles, scale rows, activation blocks
   constexpr int WAIT = (kGemmStages - 2) * LOADS;     // loads younger than the stage waited for
   const MxGeom& gm = c.gm;
   const int lane = c.lane, wave = c.wave, r = c.r, g = c.g;
@@ -399,10 +420,11 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
   const int KGP = (gm.KG + kGemmStages - 1) / kGemmStages * kGemmStages;  // groups per block, padded
 
   // activation DMA: instruction J fills fragment block b = J*8 + wave, i.e. row tile b / 4, step
-  // b % 4: the lane fetches row 16*(b/4) + r, elements 8*(4g + b%4) .. +7 of the group
-  const uint16_t* arow[MT / 2];
+  // b % 4: the lane fetches row 16*(b/4) + r, elements 8*(4g + b%4) .. +7 of the group (an odd MT
+  // loads one more row tile, of clamped rows, that no MFMA reads)
+  const uint16_t* arow[MD];
 #pragma unroll
-  for (int J = 0; J < MT / 2; ++J) {
+  for (int J = 0; J < MD; ++J) {
     const int b = J * 8 + wave;
     const int row = (b >> 2) * 16 + r;
     const int p = c.row_lo + m0 + (row < rows ? row : 0);
@@ -425,7 +447,7 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
                                        (lds_ptr)(stage + ABYTES + (2 * wave + n) * 256), 4, 0, 0);
     const int col = blk ? kg * 128 : 0;
 #pragma unroll
-    for (int J = 0; J < MT / 2; ++J)
+    for (int J = 0; J < MD; ++J)
       __builtin_amdgcn_global_load_lds((const void*)(arow[J] + col), (lds_ptr)(stage + (J * 8 + wave) * 1024), 16, 0, 0);
     if (++i_kg == KGP) {
       i_kg = 0;
@@ -484,7 +506,7 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
   float bsum[2];
   auto load_bias = [&](int nb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int n = 0; n < 2; ++n) bsum[n] = c.bias[(size_t)c.e * c.N + tile_of(min(nb, c.nbn - 1), n) * 16 + r];
+    for (int n = 0; n < 2; ++n) bsum[n] = bias_s[(tile_of(min(nb, c.nbn - 1), n) - c.nb0 * kGemmTiles) * 16 + r];
   };
   // acc[m][n][v] = D[group row 16m + 4g + v][feature (block tile 2*wave + n) * 16 + r]
   auto epilogue = [&](int nb) __attribute__((always_inline)) {
@@ -552,8 +574,8 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  lds_barrier();  // every wave is done with the previous pass's stages
-  load_bias(0);
+  lds_barrier();  // every wave is done with the previous pass's stages (and the bias)
+  stage_chunk_bias(c.bias, c.e, c.N, c.nb0, c.nbn, bias_s);
   // the stage waits count loads per group in issue order: no load may move across a group
   asm volatile("" ::: "memory");
   issue(w0, st0);
@@ -579,8 +601,8 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
       group(st2, w2, st3, w3, kg + 2);
       group(st3, w3, st0, w0, kg + 3);
     }
+    load_bias(nb);
     epilogue(nb);
-    load_bias(nb + 1);
     zero_acc();
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the loads past the chunk's end have landed
@@ -600,6 +622,7 @@ __global__ __launch_bounds__(512) void moe_mxfp4_gemm_kernel(
   const int blocks_per_e = (c.gm.NT + kGemmTiles - 1) / kGemmTiles;
   const int chunks_per_e = (blocks_per_e + chunk - 1) / chunk;
   __shared__ int pass_pre[257];
+  __shared__ float bias_s[kGemmBiasBlocks * 256];
   DenseUnit du;
   int unit = 0;
   if (!dense_unit(offsets, E, min_rows, chunks_per_e, pass_pre, du, unit)) return;
@@ -622,10 +645,12 @@ __global__ __launch_bounds__(512) void moe_mxfp4_gemm_kernel(
   c.tile_bytes = (size_t)c.gm.G * 256;
   c.wbase = packed + (size_t)c.e * c.gm.NT * c.tile_bytes + c.lane * 16;
   c.sbase = packed + c.gm.data_bytes + (size_t)c.e * c.gm.NT * c.gm.KG4 * 256 + c.lane * 4;
-  // this unit's pass of 96 rows; a group's last pass takes the fewest 32-row multiples that hold its rows
-  if (du.rows > 64) gemm_pass<GATE_UP, 6>(c, st0, st1, st2, st3, du.m0, du.rows);
-  else if (du.rows > 32) gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, du.m0, du.rows);
-  else gemm_pass<GATE_UP, 2>(c, st0, st1, st2, st3, du.m0, du.rows);
+  // this unit's pass of up to 96 rows, as the fewest 16-row tiles that hold them (at least 2)
+  if (du.rows > 80) gemm_pass<GATE_UP, 6>(c, st0, st1, st2, st3, bias_s, du.m0, du.rows);
+  else if (du.rows > 64) gemm_pass<GATE_UP, 5>(c, st0, st1, st2, st3, bias_s, du.m0, du.rows);
+  else if (du.rows > 48) gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, bias_s, du.m0, du.rows);
+  else if (du.rows > 32) gemm_pass<GATE_UP, 3>(c, st0, st1, st2, st3, bias_s, du.m0, du.rows);
+  else gemm_pass<GATE_UP, 2>(c, st0, st1, st2, st3, bias_s, du.m0, du.rows);
 }
 
 // ---- dense groups on the scaled MFMA: fp8 activations x MXFP4 weights -------------------------------
@@ -754,7 +779,8 @@ struct MxCtx {
 // conflict-free ds_read_b128.
 template <bool GATE_UP, int MT>
 __device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStage], char (&st1)[kMxStage],
-                                             char (&st2)[kMxStage], char (&st3)[kMxStage], int m0, int rows) {
+                                             char (&st2)[kMxStage], char (&st3)[kMxStage],
+                                             float (&bias_s)[kGemmBiasBlocks * 256], int m0, int rows) {
   typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) void* lds_ptr;
   static_assert(MT == 4 || MT == 8 || MT == 12, "row tiles per pass");
@@ -876,7 +902,7 @@ __device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStag
   float bsum[2];
   auto load_bias = [&](int nb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int n = 0; n < 2; ++n) bsum[n] = c.bias[(size_t)c.e * c.N + tile_of(min(nb, c.nbn - 1), n) * 16 + r];
+    for (int n = 0; n < 2; ++n) bsum[n] = bias_s[(tile_of(min(nb, c.nbn - 1), n) - c.nb0 * kGemmTiles) * 16 + r];
   };
   // acc[m][n][v] = D[group row 16m + 4g + v][feature (block tile 2*wave + n) * 16 + r] of the high term
   // (m < MR) or the low term (m >= MR, row 16(m - MR) + 4g + v)
@@ -912,8 +938,8 @@ __device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStag
     issue(wq, cur);  // refill `cur` and the weight slot 4 groups ahead
   };
 
-  lds_barrier();  // every wave is done with the previous pass's stages
-  load_bias(0);
+  lds_barrier();  // every wave is done with the previous pass's stages (and the bias)
+  stage_chunk_bias(c.bias, c.e, c.N, c.nb0, c.nbn, bias_s);
   // the stage waits count loads per group in issue order: no load may move across a group
   asm volatile("" ::: "memory");
   issue(w0, st0);
@@ -933,8 +959,8 @@ __device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStag
       group(st2, w2, kg + 2);
       group(st3, w3, kg + 3);
     }
+    load_bias(nb);
     epilogue(nb);
-    load_bias(nb + 1);
     zero_acc();
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the loads past the chunk's end have landed
@@ -955,6 +981,7 @@ __global__ __launch_bounds__(512) void moe_mx_gemm_kernel(
   const int blocks_per_e = (c.gm.NT + kGemmTiles - 1) / kGemmTiles;
   const int chunks_per_e = (blocks_per_e + chunk - 1) / chunk;
   __shared__ int pass_pre[257];
+  __shared__ float bias_s[kGemmBiasBlocks * 256];
   DenseUnit du;
   int unit = 0;
   if (!dense_unit(offsets, E, min_rows, chunks_per_e, pass_pre, du, unit)) return;
@@ -982,9 +1009,9 @@ __global__ __launch_bounds__(512) void moe_mx_gemm_kernel(
   c.sbase = packed + c.gm.data_bytes + (size_t)c.e * c.gm.NT * c.gm.KG4 * 256 + c.lane * 4;
   // this unit's pass of 96 rows (6 row tiles, each with its high and low term); a group's last pass takes
   // the fewest 32-row multiples that hold its rows
-  if (du.rows > 64) mx_gemm_pass<GATE_UP, 12>(c, st0, st1, st2, st3, du.m0, du.rows);
-  else if (du.rows > 32) mx_gemm_pass<GATE_UP, 8>(c, st0, st1, st2, st3, du.m0, du.rows);
-  else mx_gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, du.m0, du.rows);
+  if (du.rows > 64) mx_gemm_pass<GATE_UP, 12>(c, st0, st1, st2, st3, bias_s, du.m0, du.rows);
+  else if (du.rows > 32) mx_gemm_pass<GATE_UP, 8>(c, st0, st1, st2, st3, bias_s, du.m0, du.rows);
+  else mx_gemm_pass<GATE_UP, 4>(c, st0, st1, st2, st3, bias_s, du.m0, du.rows);
 }
 
 // Chunk of weight blocks per workgroup: the largest chunk that still gives at least 3 rounds of
@@ -1007,7 +1034,7 @@ inline int gemm_chunk(const MxGeom& gm, int E) {
   const int cus = device_cus();
   const int W = (gm.NT + kGemmTiles - 1) / kGemmTiles;
   int best = 1;
-  for (int c = 1; c <= W; ++c)
+  for (int c = 1; c <= min(W, kGemmBiasBlocks); ++c)
     if ((int64_t)E * ((W + c - 1) / c) >= 3LL * cus) best = c;
   return best;
 }

@@ -6,7 +6,8 @@ operations complete in issue order, so the wait is only right if exactly the exp
 issued after the stage's own, group by group.  The compiler is free to reorder independent loads
 unless fenced, and spill code adds vector-memory operations, so both are pinned here:
   * inside every group loop, each group issues exactly LOADS operations (2 weight-tile register
-    loads, 2 scale-row and MT/2 activation direct-to-LDS loads) and the loop has no scratch access;
+    loads, 2 scale-row and ceil(MT/2) activation direct-to-LDS loads, MT = 2..6 row tiles: one loop
+    per MT, two MTs per activation-load count 2 and 3) and the loop has no scratch access;
   * before every stage wait in a pass prologue, the operations since the last full drain end in
     whole groups of that composition (no later group's load moved ahead of an earlier group's);
     fewer than 3 groups after a drain are fine, the drain completed everything before it.
@@ -28,8 +29,9 @@ pytestmark = pytest.mark.skipif(HIPCC is None, reason="hipcc not available")
 VMEM = re.compile(r"\s*(global_load\w*|global_store\w*|scratch_\w+|buffer_\w+)")
 
 
-def _group(mt):
-    return Counter({"global_load_dwordx4": 2, "global_load_lds_dword": 2, "global_load_lds_dwordx4": mt // 2})
+def _group(md):
+    """One group's loads with md activation direct-to-LDS loads (md = ceil(MT / 2))."""
+    return Counter({"global_load_dwordx4": 2, "global_load_lds_dword": 2, "global_load_lds_dwordx4": md})
 
 
 @pytest.fixture(scope="module")
@@ -55,8 +57,8 @@ def _ops(lines):
 def test_group_loops_issue_exact_groups(gemm_asm):
     for name, body in gemm_asm.items():
         loops = [n for n, l in enumerate(body) if "Inner Loop Header" in l]
-        assert len(loops) == 3, f"{name}: one group loop per row-tile count"
-        seen = set()
+        assert len(loops) == 5, f"{name}: one group loop per row-tile count"
+        seen = Counter()
         for lo in loops:
             hi = next(n for n in range(lo, len(body)) if re.search(r"s_cbranch\w* \.LBB", body[n]))
             waits = [n for n in range(lo, hi) if re.search(r"s_waitcnt vmcnt\(\d+\)", body[n])]
@@ -64,14 +66,14 @@ def test_group_loops_issue_exact_groups(gemm_asm):
             wait_n = {int(re.search(r"vmcnt\((\d+)\)", body[w]).group(1)) for w in waits}
             assert len(wait_n) == 1
             loads = wait_n.pop() // 2  # the stage wait leaves 2 younger groups in flight
-            mt = 2 * (loads - 4)
-            assert mt in (2, 4, 6)
-            seen.add(mt)
+            md = loads - 4
+            assert md in (1, 2, 3)
+            seen[md] += 1
             assert not any("scratch_" in body[n] for n in range(lo, hi)), f"{name}: spill code in a group loop"
             bounds = waits + [hi]
             for a, b in zip(bounds, bounds[1:]):
-                assert Counter(_ops(body[a:b])) == _group(mt), f"{name} MT={mt}: group issue {_ops(body[a:b])}"
-        assert seen == {2, 4, 6}
+                assert Counter(_ops(body[a:b])) == _group(md), f"{name} MD={md}: group issue {_ops(body[a:b])}"
+        assert seen == Counter({1: 1, 2: 2, 3: 2})
 
 
 def test_prologue_issues_groups_in_order(gemm_asm):
@@ -82,7 +84,7 @@ def test_prologue_issues_groups_in_order(gemm_asm):
             if not m:
                 continue
             loads = int(m.group(1)) // 3
-            mt = 2 * (loads - 4)
+            md = loads - 4
             ops = []
             for n in range(w - 1, -1, -1):
                 t = body[n].strip()
@@ -97,9 +99,9 @@ def test_prologue_issues_groups_in_order(gemm_asm):
             whole = min(3, len(ops) // loads)
             for g in range(whole):
                 chunk = ops[len(ops) - (g + 1) * loads:len(ops) - g * loads]
-                assert Counter(chunk) == _group(mt), f"{name} MT={mt}: {ops}"
+                assert Counter(chunk) == _group(md), f"{name} MD={md}: {ops}"
             if whole < 3:
                 head = Counter(ops[:len(ops) - whole * loads])
-                assert not head - _group(mt), f"{name} MT={mt}: {ops}"
+                assert not head - _group(md), f"{name} MD={md}: {ops}"
             checked += 1
-        assert checked == 3, f"{name}: expected one prologue wait per row-tile count"
+        assert checked == 5, f"{name}: expected one prologue wait per row-tile count"

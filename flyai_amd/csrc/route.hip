@@ -101,6 +101,32 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
   topk_softmax_lane<K>(logits + (size_t)t * E, E, topk_ids + (size_t)t * K, topk_w + (size_t)t * K);
 }
 
+// The same selection with 4 lanes per token (64 tokens per workgroup) for E % 16 == 0, E <= 256:
+// each lane loads its quarter of the row (E/16 float4, all before the first compare) and parks it in
+// LDS (rows of E + 4 floats), then topk_softmax_group<K, 4> merges the quarters -- bit-identical to
+// topk_softmax_lane.  A lane reads back only what it wrote itself.
+template <int K>
+__global__ __launch_bounds__(256) void router_topk4_kernel(const float* __restrict__ logits, int T, int E,
+                                                           int32_t* __restrict__ topk_ids,
+                                                           float* __restrict__ topk_w) {
+  extern __shared__ float4 rows_lds[];  // [64][E + 4] floats
+  float* row = reinterpret_cast<float*>(rows_lds) + (threadIdx.x >> 2) * (E + 4);
+  const int sub = threadIdx.x & 3, tl = threadIdx.x >> 2;
+  const int t = blockIdx.x * 64 + tl;
+  const int Q = E / 4;
+  float4 v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int e0 = sub * Q + 4 * i;
+    v[i] = (t < T && 4 * i < Q) ? *reinterpret_cast<const float4*>(logits + (size_t)t * E + e0)
+                                : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    if (4 * i < Q) *reinterpret_cast<float4*>(row + sub * Q + 4 * i) = v[i];
+  if (t < T) topk_softmax_group<K, 4>(row, E, sub, topk_ids + (size_t)t * K, topk_w + (size_t)t * K);
+}
+
 int launch_router_logits(const uint16_t* x, const uint16_t* w, const uint16_t* b, int T, int H,
                          int E, float* logits, hipStream_t s) {
   if (H <= 3072 && T >= 256) {  // prefill-sized: 16 experts per workgroup halve the x re-reads
@@ -121,6 +147,18 @@ int launch_router(const uint16_t* x, const uint16_t* w, const uint16_t* b, int T
   if (T == 0) return FLYAI_OK;
   int rc = launch_router_logits(x, w, b, T, H, E, logits, s);
   if (rc) return rc;
+  if (E % 16 == 0 && E <= 256 && (k == 4 || k == 8 || k == 2)) {
+    if (k == 4)
+      hipLaunchKernelGGL(router_topk4_kernel<4>, dim3(ceil_div(T, 64)), dim3(256), 64 * (E + 4) * 4, s, logits, T, E,
+                         ids, wts);
+    else if (k == 8)
+      hipLaunchKernelGGL(router_topk4_kernel<8>, dim3(ceil_div(T, 64)), dim3(256), 64 * (E + 4) * 4, s, logits, T, E,
+                         ids, wts);
+    else
+      hipLaunchKernelGGL(router_topk4_kernel<2>, dim3(ceil_div(T, 64)), dim3(256), 64 * (E + 4) * 4, s, logits, T, E,
+                         ids, wts);
+    return check_launch("router_topk4");
+  }
   if (k == 4)
     hipLaunchKernelGGL(router_topk_kernel<4>, dim3(ceil_div(T, 256)), dim3(256), 0, s, logits, T, E, ids, wts);
   else if (k == 8)

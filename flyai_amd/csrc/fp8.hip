@@ -158,9 +158,10 @@ __device__ __forceinline__ v8i_t ld_nt_v8(const uint8_t* p) {
   return v8i_t{(int)a.x, (int)a.y, (int)a.z, (int)a.w, (int)b.x, (int)b.y, (int)b.z, (int)b.w};
 }
 
+// One workgroup's work (`bid`: its index among the launch's workgroups of this shape).
 template <bool GATE_UP, int MT, int NTW>
-__global__ __launch_bounds__(256) void moe_fp8_kernel(
-    const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, const int32_t* __restrict__ perm,
+__device__ __forceinline__ void moe_fp8_body(
+    int bid, const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, int k_top, const float* __restrict__ row_w,
     const uint8_t* __restrict__ packed, int E, int n_shared, int N, int K, int min_rows,
     int max_rows, uint16_t* __restrict__ out) {
@@ -173,8 +174,8 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
   const Fp8Geom gm = fp8_geom(E + (n_shared > 0), N, K);
   constexpr int kTilesPerWG = 4 * NTW;
   const int wg_per_e = (gm.NT + kTilesPerWG - 1) / kTilesPerWG;
-  const int e = blockIdx.x / wg_per_e;
-  const int wgi = blockIdx.x % wg_per_e;
+  const int e = bid / wg_per_e;
+  const int wgi = bid % wg_per_e;
   const bool shared = e == E;
   const int row_lo = offsets[e];
   const int n_e = shared ? n_shared : offsets[e + 1] - row_lo;
@@ -335,11 +336,28 @@ __global__ __launch_bounds__(256) void moe_fp8_kernel(
   }
 }
 
-// Experts with at most kF8TailRows rows take the one-row-tile kernel (two weight tiles per wave,
-// small LDS); larger groups take the 8-row-tile kernel (one weight tile per wave, 128 rows per
-// pass, so groups up to that size stream their weights once; two waves per SIMD).
+// Experts with at most kF8TailRows rows take the one-row-tile body (two weight tiles per wave,
+// small LDS); larger groups take the 8-row-tile body (one weight tile per wave, 128 rows per pass,
+// so groups up to that size stream their weights once).  Both run in one launch, the dense
+// workgroups first: the few hot experts' long, latency-bound workgroups start at once and run
+// beside the bandwidth-bound row-pass workgroups instead of after them.  Both bodies fit two waves
+// per SIMD (at most 244 registers) and the launch's LDS is the larger body's.
 constexpr int kF8TailRows = 16;
 constexpr int kF8DenseMT = 8;
+
+template <bool GATE_UP>
+__global__ __launch_bounds__(256) void moe_fp8_kernel(
+    const uint8_t* __restrict__ aq, const uint8_t* __restrict__ as, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ offsets, int k_top, const float* __restrict__ row_w,
+    const uint8_t* __restrict__ packed, int E, int n_shared, int N, int K, int dense_wgs,
+    uint16_t* __restrict__ out) {
+  if ((int)blockIdx.x < dense_wgs)
+    moe_fp8_body<GATE_UP, kF8DenseMT, 1>(blockIdx.x, aq, as, perm, offsets, k_top, row_w, packed, E, n_shared,
+                                         N, K, kF8TailRows + 1, 1 << 30, out);
+  else
+    moe_fp8_body<GATE_UP, 1, 2>(blockIdx.x - dense_wgs, aq, as, perm, offsets, k_top, row_w, packed, E,
+                                n_shared, N, K, 1, kF8TailRows, out);
+}
 
 template <bool GATE_UP>
 int launch_moe_fp8(const uint8_t* aq, const uint8_t* as, const int32_t* perm, const int32_t* offsets,
@@ -347,15 +365,11 @@ int launch_moe_fp8(const uint8_t* aq, const uint8_t* as, const int32_t* perm, co
                    int K, uint16_t* out, hipStream_t s) {
   const Fp8Geom gm = fp8_geom(E, N, K);
   const int groups = E + (n_shared > 0);
-  hipLaunchKernelGGL((moe_fp8_kernel<GATE_UP, 1, 2>), dim3(groups * ceil_div(gm.NT, 8)), dim3(256),
-                     fp8_lds_bytes(1, K), s, aq, as, perm, offsets, k_top, row_w, packed, E, n_shared,
-                     N, K, 1, kF8TailRows, out);
-  int rc = check_launch(GATE_UP ? "moe_gate_up_fp8(tail)" : "moe_down_fp8(tail)");
-  if (rc) return rc;
-  hipLaunchKernelGGL((moe_fp8_kernel<GATE_UP, kF8DenseMT, 1>), dim3(groups * ceil_div(gm.NT, 4)),
-                     dim3(256), fp8_lds_bytes(kF8DenseMT, K), s, aq, as, perm, offsets, k_top, row_w,
-                     packed, E, n_shared, N, K, kF8TailRows + 1, 1 << 30, out);
-  return check_launch(GATE_UP ? "moe_gate_up_fp8(dense)" : "moe_down_fp8(dense)");
+  const int dense_wgs = groups * ceil_div(gm.NT, 4), tail_wgs = groups * ceil_div(gm.NT, 8);
+  const int lds = std::max(fp8_lds_bytes(kF8DenseMT, K), fp8_lds_bytes(1, K));
+  hipLaunchKernelGGL((moe_fp8_kernel<GATE_UP>), dim3(dense_wgs + tail_wgs), dim3(256), lds, s, aq, as, perm,
+                     offsets, k_top, row_w, packed, E, n_shared, N, K, dense_wgs, out);
+  return check_launch(GATE_UP ? "moe_gate_up_fp8" : "moe_down_fp8");
 }
 
 // ---- combine: out[t] = bf16(residual + bf16(sum_s y[inv[t*k+s]] + shared[t])) ------------------------

@@ -134,6 +134,8 @@ def main():
                          "that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes)")
     ap.add_argument("--workload", choices=("c0", "c1", "c2", "c3", "c4", "wire"), default="c1")
     ap.add_argument("--frames", type=int, default=20, help="--workload wire: frames per path")
+    ap.add_argument("--split-keys", type=int, default=1024,
+                    help="keys per attention item of the GPT-OSS stages (a multiple of 64)")
     ap.add_argument("--dense", choices=("fp8", "bf16"), default="bf16",
                     help="--workload c2: dense expert groups on the scaled MFMA with two-term fp8 activations "
                          "(fp8) or on the bf16-activation tiled GEMM (bf16)")
@@ -318,7 +320,7 @@ def run_gptoss(args, workload="c1"):
         cpu_inputs = cpu_layer_inputs(layers[:2], kv, hidden0, S)
     fp8 = chunked_prefill and args.dense == "fp8"
     stage = RaggedStage(shape, layers, rot, kv, max_tokens=max(64, T), max_seqs=S, use_graphs=args.graphs,
-                        dense_fp8=fp8)
+                        dense_fp8=fp8, split_keys=args.split_keys)
     slots = list(range(S))
     torch.cuda.synchronize()
     print("[bench] warmup", file=sys.stderr, flush=True)

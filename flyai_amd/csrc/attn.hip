@@ -77,14 +77,16 @@ __device__ __forceinline__ void load_v_tile(uint4 (&v)[4][2], const uint16_t* __
 // Per-wave state of QT query-row tiles of 16 (QT = 1: up to 2 tokens; QT = 2: up to 4 tokens): the
 // Q^T operand, each row's position (and, in a tree, its depth and ancestor set), and the running
 // softmax (max, sum, O^T accumulators).  Query row rq = 16*qt + n is token rq/8, head kv_head*8 + rq%8.
+// The row sums are accumulated like O^T, by an MFMA with an all-ones A operand: every element of
+// lane (n, g)'s L[qt] is row n's complete sum over the keys so far.
 template <int QT>
 struct QRows {
   bf16x8_t qf[QT][2];
   int qpos[QT], qdep[QT];
   bool qval[QT];
   uint64_t qanc[QT];
-  float m_run[QT], l_run[QT];
-  f32x4_t O[QT][4];
+  float m_run[QT];
+  f32x4_t O[QT][4], L[QT];
 };
 
 // Load the rows of tokens tok .. tok+ntok-1 (positions pos0 + ti, or tree positions) and reset the
@@ -121,26 +123,45 @@ __device__ __forceinline__ void rows_init(QRows<QT>& R, const uint16_t* __restri
     R.qf[qt][0] = as_bf16x8(a);
     R.qf[qt][1] = as_bf16x8(b2);
     R.m_run[qt] = -1e30f;
-    R.l_run[qt] = 0.f;
+    R.L[qt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) R.O[qt][dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 }
 
+// Max over the four lanes n, n+16, n+32, n+48 (one query row's lane groups), with gfx950's
+// v_permlane32_swap / v_permlane16_swap (VALU lane swaps, no LDS round trip).  Swapping a register
+// with a copy of itself leaves lane i's value and its partner's in the two results.
+__device__ __forceinline__ float max_lane_groups(float v) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float x0 = __uint_as_float(a[0]), x1 = __uint_as_float(a[1]);
+  v = x0 > x1 ? x0 : x1;
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float y0 = __uint_as_float(b[0]), y1 = __uint_as_float(b[1]);
+  return y0 > y1 ? y0 : y1;
+}
+
 // One 64-key block kb (K fragments kc, V fragments vv of this lane) against the rows: scores
 // S^T = K . Q^T, the mask (positions in [key_lo, key_hi) within each row's causal / window range, or
-// the tree rule), the online softmax update and O^T += V^T . P^T.  interior: every key of the block is
-// visible to every valid row (no mask).  Values of keys at or past key_hi are zeroed (they may be
-// unwritten, even non-finite; P is 0 there).
+// the tree rule), the online softmax update and O^T += V^T . P^T, L += 1 . P^T.  interior: every key of
+// the block is visible to every valid row (no mask).  Values of keys at or past key_hi are zeroed (they
+// may be unwritten, even non-finite; P is 0 there).
+// Scores are kept raw and scaled inside the exponent, P = 2^(s * scale - m) with scale = head_dim^-0.5
+// log2(e) (one FMA and one v_exp_f32; the max commutes with the positive scale).  The running max m
+// (base-2 units) moves only when a block's max exceeds it by more than kMaxSlack, so P <= 2^kMaxSlack
+// between moves; a wave rescales O and L only when one of its rows moved (alpha = 1 exactly for the
+// others, so skipping is exact and a row's result does not depend on its wave mates).
+constexpr float kMaxSlack = 8.f;
+
 template <int QT, bool TREE>
 __device__ __forceinline__ void rows_block(QRows<QT>& R, const uint4 (&kc)[4][2], uint4 (&vv)[4][2], int kb,
                                            bool interior, int key_lo, int key_hi, int window,
                                            const flyai_attn_tree* __restrict__ tree,
                                            const int* __restrict__ dep_s) {
   const int g = (threadIdx.x & 63) >> 4;
-  // scores in base-2 units: head_dim^-0.5 * log2(e), so that P = exp2(s - m) is one v_exp_f32
   const float scale = 0.125f * kLog2e;
   const int tstart = TREE ? tree->start : 0;
+  const bf16x8_t ones = as_bf16x8(make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
   if (kb + 64 > key_hi) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -161,10 +182,7 @@ __device__ __forceinline__ void rows_block(QRows<QT>& R, const uint4 (&kc)[4][2]
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          s[kt][v] *= scale;
-          bmax = fmaxf(bmax, s[kt][v]);
-        }
+        for (int v = 0; v < 4; ++v) bmax = fmaxf(bmax, s[kt][v]);
     } else {
       const int p = R.qpos[qt];
       const int lo = max(key_lo, window > 0 ? p - window + 1 : 0);
@@ -187,32 +205,36 @@ __device__ __forceinline__ void rows_block(QRows<QT>& R, const uint4 (&kc)[4][2]
           } else {
             ok = R.qval[qt] && key >= lo && key <= hi;
           }
-          s[kt][v] = ok ? s[kt][v] * scale : -INFINITY;
+          s[kt][v] = ok ? s[kt][v] : -INFINITY;
           bmax = fmaxf(bmax, s[kt][v]);
         }
     }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float m_new = fmaxf(R.m_run[qt], bmax);
-    // v_exp_f32 directly (results below 2^-126 may flush to zero: immaterial for a probability)
-    const float alpha = __builtin_amdgcn_exp2f(R.m_run[qt] - m_new);
-    R.m_run[qt] = m_new;
+    bmax = max_lane_groups(bmax);
+    // (a fully masked row keeps m = -1e30: -1e30 + kMaxSlack rounds to -1e30 and -inf never exceeds it)
+    const float m_blk = bmax * scale;
+    const bool move = m_blk > R.m_run[qt] + kMaxSlack;
+    if (__ballot(move)) {
+      const float m_new = move ? m_blk : R.m_run[qt];
+      // v_exp_f32 directly (results below 2^-126 may flush to zero: immaterial for a probability)
+      const float alpha = __builtin_amdgcn_exp2f(R.m_run[qt] - m_new);
+      R.m_run[qt] = m_new;
+      R.L[qt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) R.O[qt][dt] *= alpha;
+    }
+    const float neg_m = -R.m_run[qt];
     // P rounded to bf16 (the PV operand; the row sum uses the same rounded values).  The cast is
     // gfx950's v_cvt_pk_bf16_f32: round to nearest even, two values per instruction.
-    float lsum = 0.f;
     bf16x8_t pt[2];
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const __bf16 pb = (__bf16)__builtin_amdgcn_exp2f(s[kt][v] - m_new);
-        lsum += (float)pb;
-        pt[kt >> 1][(kt & 1) * 4 + v] = pb;
-      }
-    R.l_run[qt] = R.l_run[qt] * alpha + lsum;
+      for (int v = 0; v < 4; ++v)
+        pt[kt >> 1][(kt & 1) * 4 + v] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[kt][v], scale, neg_m));
+    R.L[qt] = mfma16x16x32(ones, pt[0], R.L[qt]);
+    R.L[qt] = mfma16x16x32(ones, pt[1], R.L[qt]);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
-      R.O[qt][dt] *= alpha;
       R.O[qt][dt] = mfma16x16x32(as_bf16x8(vv[dt][0]), pt[0], R.O[qt][dt]);
       R.O[qt][dt] = mfma16x16x32(as_bf16x8(vv[dt][1]), pt[1], R.O[qt][dt]);
     }
@@ -236,7 +258,7 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
                                           const float* __restrict__ sinks, uint16_t* __restrict__ out,
                                           const flyai_attn_tree* __restrict__ tree,
                                           const int* __restrict__ dep_s) {
-  const int lane = threadIdx.x;
+  const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   // the item is its rows' whole key range (a group index outside the plan reads as "not single")
   const bool single = it.group >= 0 && it.group < n_groups && groups[it.group].n_splits == 1;
@@ -289,9 +311,7 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
   // split (the same operations in the same order, so the same bits), and the merge skips its group.
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
-    float l = R.l_run[qt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = R.L[qt][0];
     const int rq = 16 * qt + n;
     if (!R.qval[qt]) continue;
     if (single) {
@@ -367,13 +387,13 @@ __global__ __launch_bounds__(64, 2) void attn_partial_kernel(
 // computes.  No key splits: each wave ends with the sink and the normalisation and writes its rows.
 constexpr int kPrefillWaves = kPrefillTokens / 4;
 
-__global__ __launch_bounds__(64 * kPrefillWaves) void attn_prefill_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+__device__ __forceinline__ void attn_prefill_body(
+    int bid, const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
     const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
     const int32_t* __restrict__ kv_cap, const float* __restrict__ sinks, int window, int Hq,
     const flyai_attn_item* __restrict__ items, uint16_t* __restrict__ out) {
   __shared__ uint4 kvs[2][2][512];  // [buffer][K, V][one 64-key block: 4096 bf16]
-  const flyai_attn_item it = items[blockIdx.x];
+  const flyai_attn_item it = items[bid];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int cap = kv_cap[it.seq];
@@ -439,9 +459,7 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void attn_prefill_kernel(
   // single split
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    float l = R.l_run[qt];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = R.L[qt][0];
     const int rq = 16 * qt + n;
     if (!R.qval[qt]) continue;
     const int h = it.kv_head * 8 + (rq & 7);
@@ -457,6 +475,42 @@ __global__ __launch_bounds__(64 * kPrefillWaves) void attn_prefill_kernel(
       *reinterpret_cast<uint2*>(o + 16 * dt + 4 * g) = make_uint2(lo, hi);
     }
   }
+}
+
+__global__ __launch_bounds__(64 * kPrefillWaves, 2) void attn_prefill_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
+    const int32_t* __restrict__ kv_cap, const float* __restrict__ sinks, int window, int Hq,
+    const flyai_attn_item* __restrict__ items, uint16_t* __restrict__ out) {
+  attn_prefill_body(blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, items, out);
+}
+
+// A step with prefill items and split items in one launch: the prefill workgroups first, then
+// workgroups of kPrefillWaves split items (one per wave; the split body has no workgroup barrier,
+// so a wave past the item count leaves alone).  The split items, bandwidth-bound, then fill the
+// slots the prefill workgroups (MFMA- and latency-bound) free towards their end instead of waiting
+// for the whole prefill launch.  Both bodies fit two waves per SIMD.
+__global__ __launch_bounds__(64 * kPrefillWaves, 2) void attn_step_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
+    const int32_t* __restrict__ kv_cap, int window, int Hq,
+    const flyai_attn_item* __restrict__ items, int n_items, const int32_t* __restrict__ n_live,
+    float* __restrict__ partials, const flyai_attn_group* __restrict__ groups, int n_groups,
+    const float* __restrict__ sinks, uint16_t* __restrict__ out, const flyai_attn_item* __restrict__ pitems,
+    int n_pitems) {
+  if ((int)blockIdx.x < n_pitems) {
+    attn_prefill_body(blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, pitems, out);
+    return;
+  }
+  const int idx = ((int)blockIdx.x - n_pitems) * kPrefillWaves + (int)(threadIdx.x >> 6);
+  if (idx >= n_items || (n_live && idx >= *n_live)) return;
+  const flyai_attn_item it = items[idx];
+  if (it.ntok <= 2)
+    attn_item<1, false>(it, idx, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks,
+                        out, nullptr, nullptr);
+  else
+    attn_item<2, false>(it, idx, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks,
+                        out, nullptr, nullptr);
 }
 
 int launch_attn_prefill(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
@@ -546,6 +600,24 @@ int launch_attn(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_poo
   int rc = check_launch("attn_partial");
   if (rc) return rc;
   if (!merge) return FLYAI_OK;  // every group has one split: the items wrote the output
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(n_groups), dim3(256), 0, s, partials, groups, sinks,
+                     Hq, counts ? counts + 1 : nullptr, out);
+  return check_launch("attn_merge");
+}
+
+// One launch of attn_step_kernel for a step with both item kinds, then the merge as in launch_attn.
+int launch_attn_step(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool, const int64_t* kv_base,
+                     const int32_t* kv_cap, const float* sinks, int window, int Hq, const flyai_attn_item* items,
+                     int n_items, const flyai_attn_group* groups, int n_groups, const int32_t* counts, float* partials,
+                     const flyai_attn_item* pitems, int n_pitems, uint16_t* out, bool merge, hipStream_t s) {
+  const int grid = n_pitems + (n_items + kPrefillWaves - 1) / kPrefillWaves;
+  if (grid == 0) return FLYAI_OK;
+  hipLaunchKernelGGL(attn_step_kernel, dim3(grid), dim3(64 * kPrefillWaves), 0, s, q, k_pool, v_pool, kv_base,
+                     kv_cap, window, Hq, items, n_items, counts, partials, groups, n_groups, sinks, out, pitems,
+                     n_pitems);
+  int rc = check_launch("attn_step");
+  if (rc) return rc;
+  if (!merge || n_items == 0) return FLYAI_OK;
   hipLaunchKernelGGL(attn_merge_kernel, dim3(n_groups), dim3(256), 0, s, partials, groups, sinks,
                      Hq, counts ? counts + 1 : nullptr, out);
   return check_launch("attn_merge");

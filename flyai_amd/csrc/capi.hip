@@ -66,6 +66,9 @@ int attn_plan(const int32_t*, const int32_t*, int, int, int, int, flyai_attn_ite
               flyai_attn_group*, int, int*, int*, int*, int, flyai_attn_item*, int, int*);
 int launch_attn_prefill(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
                         const float*, int, int, const flyai_attn_item*, int, uint16_t*, hipStream_t);
+int launch_attn_step(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
+                     const float*, int, int, const flyai_attn_item*, int, const flyai_attn_group*, int,
+                     const int32_t*, float*, const flyai_attn_item*, int, uint16_t*, bool, hipStream_t);
 int attn_plan_tree(const flyai_attn_tree&, int, int, int, flyai_attn_item*, int, flyai_attn_group*, int,
                    int*, int*, int*);
 int launch_pack(const int32_t*, const int32_t*, const int64_t*, const int32_t*, int, int, int, int32_t*,
@@ -360,15 +363,26 @@ static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* count
                            I32(st->o_sid), st->cos_tab, st->sin_tab, c.rope_positions, Tn, H,
                            c.n_q_heads, c.n_kv_heads, c.head_dim, base_d, cap_d, B16(st->o_qrot),
                            L.k_pool, L.v_pool, kv_pos, s));
-    RUN(launch_attn(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks,
-                    L.sliding ? c.window : 0, c.n_q_heads,
-                    reinterpret_cast<const flyai_attn_item*>(blob + sp.off_items[p]), sp.grid_items[p],
-                    sp.n_small[p], reinterpret_cast<const flyai_attn_group*>(blob + sp.off_groups[p]),
-                    sp.grid_groups[p], counts ? counts + 2 * p : nullptr, F32(st->o_parts),
-                    B16(st->o_attn), tree_d, sp.merge[p] != 0, s));
-    RUN(launch_attn_prefill(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks, L.sliding ? c.window : 0,
-                            c.n_q_heads, reinterpret_cast<const flyai_attn_item*>(blob + sp.off_pitems[p]),
-                            sp.n_pitems[p], B16(st->o_attn), s));
+    if (sp.n_pitems[p] > 0 && !tree_d) {
+      // prefill and split items share one launch (attn_step_kernel)
+      RUN(launch_attn_step(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks, L.sliding ? c.window : 0,
+                           c.n_q_heads, reinterpret_cast<const flyai_attn_item*>(blob + sp.off_items[p]),
+                           sp.grid_items[p], reinterpret_cast<const flyai_attn_group*>(blob + sp.off_groups[p]),
+                           sp.grid_groups[p], counts ? counts + 2 * p : nullptr, F32(st->o_parts),
+                           reinterpret_cast<const flyai_attn_item*>(blob + sp.off_pitems[p]), sp.n_pitems[p],
+                           B16(st->o_attn), sp.merge[p] != 0, s));
+    } else {
+      RUN(launch_attn(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks,
+                      L.sliding ? c.window : 0, c.n_q_heads,
+                      reinterpret_cast<const flyai_attn_item*>(blob + sp.off_items[p]), sp.grid_items[p],
+                      sp.n_small[p], reinterpret_cast<const flyai_attn_group*>(blob + sp.off_groups[p]),
+                      sp.grid_groups[p], counts ? counts + 2 * p : nullptr, F32(st->o_parts),
+                      B16(st->o_attn), tree_d, sp.merge[p] != 0, s));
+      RUN(launch_attn_prefill(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks,
+                              L.sliding ? c.window : 0, c.n_q_heads,
+                              reinterpret_cast<const flyai_attn_item*>(blob + sp.off_pitems[p]), sp.n_pitems[p],
+                              B16(st->o_attn), s));
+    }
     if (fused_route) {
       // decode-sized: o-proj finalize + residual + RMSNorm + router logits, then top-k + permute
       RUN(launch_linear_residual_rmsnorm_logits(B16(st->o_attn), L.wo, L.bo, Tn, H, c.n_q_heads * c.head_dim,

@@ -83,6 +83,75 @@ __device__ __forceinline__ float warp_max(float v) {
   return v;
 }
 
+// ---- wave sums of many values at once ------------------------------------------------------------
+// The xor butterfly v += shfl_xor(v, off), off = 32, 16, ..., 1, leaves every lane with the wave's
+// sum.  For N = 2^n values per lane, wave_sum_scatter computes the same N sums with the same
+// additions (each step adds a lane's partial to its partner's, and a + b == b + a bit for bit), but
+// as a reduce-scatter: the step with offset off halves the values a lane carries -- the lane with
+// that bit clear keeps the lower half, its partner the upper -- so the N sums take N - 1 exchanges
+// per lane instead of 6 N.  Offsets 32 and 16 use gfx950's v_permlane32_swap / v_permlane16_swap
+// (which pair value j with value j + half directly), the smaller ones ds_swizzle in its xor bit mode.
+// Lane i ends with the sum of value i >> (6 - n) (2^(6-n) lanes hold each).  Every lane of the wave
+// must be active.
+template <int OFF>
+__device__ __forceinline__ float swizzle_xor(float v) {
+  static_assert(OFF >= 1 && OFF <= 16, "ds_swizzle's bit mode stays within 32 lanes");
+  return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1f | (OFF << 10)));
+}
+
+template <int OFF, int CNT, int N>
+__device__ __forceinline__ void wave_sum_step(float (&a)[N], int lane) {
+  if constexpr (CNT == 1) {  // one value left: the plain butterfly step
+    if constexpr (OFF == 32 || OFF == 16) {
+      const uint32_t u = __float_as_uint(a[0]);
+      const auto r = OFF == 32 ? __builtin_amdgcn_permlane32_swap(u, u, false, false)
+                               : __builtin_amdgcn_permlane16_swap(u, u, false, false);
+      a[0] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    } else {
+      a[0] = a[0] + swizzle_xor<OFF>(a[0]);
+    }
+  } else {
+    constexpr int H = CNT / 2;
+    if constexpr (OFF == 32 || OFF == 16) {
+#pragma unroll
+      for (int j = 0; j < H; ++j) {
+        const auto r = OFF == 32
+                           ? __builtin_amdgcn_permlane32_swap(__float_as_uint(a[j]), __float_as_uint(a[j + H]), false, false)
+                           : __builtin_amdgcn_permlane16_swap(__float_as_uint(a[j]), __float_as_uint(a[j + H]), false, false);
+        a[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+      }
+    } else {
+      const bool upper = (lane & OFF) != 0;
+#pragma unroll
+      for (int j = 0; j < H; ++j) {
+        const float send = upper ? a[j] : a[j + H];
+        const float keep = upper ? a[j + H] : a[j];
+        a[j] = keep + swizzle_xor<OFF>(send);
+      }
+    }
+  }
+}
+
+template <int N>
+__device__ __forceinline__ float wave_sum_scatter(float (&a)[N]) {
+  static_assert(N >= 1 && N <= 64 && (N & (N - 1)) == 0, "N must be a power of two <= 64");
+  const int lane = threadIdx.x & 63;
+  constexpr int c1 = N, c2 = c1 > 1 ? c1 / 2 : 1, c3 = c2 > 1 ? c2 / 2 : 1, c4 = c3 > 1 ? c3 / 2 : 1,
+                c5 = c4 > 1 ? c4 / 2 : 1, c6 = c5 > 1 ? c5 / 2 : 1;
+  wave_sum_step<32, c1>(a, lane);
+  wave_sum_step<16, c2>(a, lane);
+  wave_sum_step<8, c3>(a, lane);
+  wave_sum_step<4, c4>(a, lane);
+  wave_sum_step<2, c5>(a, lane);
+  wave_sum_step<1, c6>(a, lane);
+  return a[0];
+}
+
+template <int N>
+constexpr int wave_sum_scatter_shift() {
+  return N >= 64 ? 0 : N >= 32 ? 1 : N >= 16 ? 2 : N >= 8 ? 3 : N >= 4 ? 4 : N >= 2 ? 5 : 6;
+}
+
 // ---- KV slab layout (head_dim 64) ----------------------------------------------------------------
 // A sequence's slab holds, per kv head, a region of cap x 64 bf16 (cap % 64 == 0) made of 64-key
 // blocks of 4096 elements in the attention kernel's MFMA-fragment order, so that every 16-byte-per-

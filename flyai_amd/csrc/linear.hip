@@ -360,13 +360,12 @@ __global__ __launch_bounds__(kRowThreads) void residual_rmsnorm_logits_kernel(
         }
       }
     }
-#pragma unroll
-    for (int c = 0; c < kBatch; ++c) {
-      float v = acc[c];
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
-      if (lane == 0 && e0 + c < e_hi) logits[(size_t)t * E + e0 + c] = bf16_round(v + bf2f(rb[e0 + c]));
-    }
+    // the butterfly's additions as a reduce-scatter over the kBatch sums: lane l ends with l >> shift
+    const float v = wave_sum_scatter<kBatch>(acc);
+    constexpr int shift = wave_sum_scatter_shift<kBatch>();
+    const int c = lane >> shift;
+    if ((lane & ((1 << shift) - 1)) == 0 && e0 + c < e_hi)
+      logits[(size_t)t * E + e0 + c] = bf16_round(v + bf2f(rb[e0 + c]));
   }
 }
 
@@ -474,6 +473,175 @@ __global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_bf16_kernel(const
     }
 }
 
+// The tiled GEMM for K % 64 == 0 (every projection of both models): the same 128 x 128 workgroup
+// tile, 8 waves of 32 rows x 64 features and per-element arithmetic, but the operand tiles go
+// global -> LDS directly (global_load_lds, no register staging) through 4 stages of one 64-K group
+// each (A and B: 8 row tiles of 2 KiB per stage, 4 load instructions per wave, each reading whole
+// 128-byte rows), a group's loads issued 3 groups ahead.  The stages are separate LDS arrays with compile-time stage numbers,
+// so the compiler can tell a stage's reads from the DMA writes into the others; each stage is
+// waited for with an explicit vmcnt that leaves the 2 younger groups' loads in flight (vector
+// memory loads complete in issue order), then one barrier per group, which also tells the waves
+// that the stage just read can be refilled.  The next group's step-0 fragments are read under the
+// current group's step-1 MFMAs.  A group is 2 MFMA steps of 32 K; step j of 64-K group q is step
+// 2 (q % 2) + j of the split-K kernel's 128-K group q / 2, so the K-to-lane mapping, each slice's
+// MFMA chain and the slice-ordered fold are the split-K kernel's, bit for bit.  The group loop is
+// unrolled by one 512-K slice (8 groups, twice round the stages), so the fold sits at a fixed place
+// and no group carries a branch.  Rows and features past M / N load clamped rows and are never
+// stored; the groups issued past the end read the last group and are never computed on.
+constexpr int kTlStages = 4;
+constexpr int kTlStageBytes = 32 * 1024;  // A then B: [tile 8][step 2][lane 64] x 16 B each
+constexpr int kTlLoads = 4;               // load instructions per wave per group
+constexpr int kTlGroupsPerSlice = 8;      // 64-K groups per 512-K slice
+
+__global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_lds_kernel(const uint16_t* __restrict__ x,
+                                                                          const uint16_t* __restrict__ W,
+                                                                          int M, int N, int K,
+                                                                          float* __restrict__ out) {
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  // per stage: the A fragment blocks and the B fragment blocks as separate arrays
+  __shared__ __align__(1024) char sa0[kTlStageBytes / 2], sb0[kTlStageBytes / 2];
+  __shared__ __align__(1024) char sa1[kTlStageBytes / 2], sb1[kTlStageBytes / 2];
+  __shared__ __align__(1024) char sa2[kTlStageBytes / 2], sb2[kTlStageBytes / 2];
+  __shared__ __align__(1024) char sa3[kTlStageBytes / 2], sb3[kTlStageBytes / 2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // XCD-aware tile order: workgroup b runs on XCD b % 8, and XCD x takes tiles x * per .. x * per +
+  // per - 1 of the row-fastest order (a band of whole feature columns), so the workgroups that share
+  // an XCD's L2 share their weight tiles and the activation rows; without it the output projection
+  // (23 feature tiles) read about 11x its operand bytes from HBM
+  const int gm_ = (M + kTileM - 1) / kTileM, gn_ = (N + kTileN - 1) / kTileN;
+  const int per = (gm_ * gn_ + 7) / 8;
+  const int tile = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (tile >= gm_ * gn_) return;
+  const int m0 = (tile % gm_) * kTileM, n0 = (tile / gm_) * kTileN;
+  const int wm = wave >> 1, wn = wave & 1;  // the wave's 32 x 64 block: row tiles 2wm, 2wm+1
+  const int KG = K / 64;
+  // LDS: a 16-row tile of a 64-K group is 2 KiB, row-major (128 B per row), its eight 16-byte chunks
+  // XOR-swizzled by row: chunk c of row rr sits at position c ^ swz(rr), swz(rr) = (rr / 2) % 8.
+  // A load instruction fills half a tile (8 whole rows): lane L writes position L % 8 of row L / 8
+  // (the DMA's fixed lane order), so it reads chunk (L % 8) ^ swz of that row -- 8 consecutive lanes
+  // read one row's 128 contiguous bytes (a fragment-order load, 16 rows x 64 B per instruction,
+  // streams from L2 at a third of the rate).  Instruction u = 4 wave + i: u < 16: A half-tile u
+  // (tile u / 2, rows 8 (u % 2) ..), else B half-tile u - 16.
+  const int r = lane & 15, g = lane >> 4;
+  const uint16_t* src[kTlLoads];
+#pragma unroll
+  for (int i = 0; i < kTlLoads; ++i) {
+    const int u = kTlLoads * wave + i, ub = u & 15, t = ub >> 1;
+    const int rr = 8 * (ub & 1) + (lane >> 3), chunk = (lane & 7) ^ ((rr >> 1) & 7);
+    const bool is_a = u < 16;
+    const int row = is_a ? min(m0 + 16 * t + rr, M - 1) : min(n0 + 16 * t + rr, N - 1);
+    src[i] = (is_a ? x : W) + (size_t)row * K + 8 * chunk;
+  }
+  // the MFMA fragment of step j, lane (r, g): row r, K 32j + 8g .. +7 = chunk 4j + g, read from its
+  // swizzled position (step 1's chunk is step 0's with bit 2 flipped)
+  const int frag0 = r * 128 + ((g ^ ((r >> 1) & 7)) << 4);
+  // waves 0-3 fill the A blocks, waves 4-7 the B blocks (wave-uniform)
+  auto issue = [&](char* sa, char* sb, int q) __attribute__((always_inline)) {
+    const size_t koff = (size_t)min(q, KG - 1) * 64;
+    char* dst = wave < 4 ? sa + kTlLoads * wave * 1024 : sb + kTlLoads * (wave - 4) * 1024;
+#pragma unroll
+    for (int i = 0; i < kTlLoads; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(src[i] + koff), (lds_ptr)(dst + i * 1024), 16, 0, 0);
+  };
+  // tot starts at -0: -0 + x == x for every x (also -0), so the first fold copies the first slice's
+  // sums bit for bit, as the split-K finalizer's first plane
+  f32x4_t acc[2][4], tot[2][4];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      tot[a][b] = f32x4_t{-0.f, -0.f, -0.f, -0.f};
+    }
+  auto fold = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        tot[a][b] += acc[a][b];
+        acc[a][b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+  };
+  bf16x8_t a0[2], a1[2], b0[4], b1[4];
+  auto read_ab = [&](bf16x8_t (&af)[2], bf16x8_t (&bw)[4], const char* sa, const char* sb, int j) __attribute__((always_inline)) {
+    const int fo = frag0 ^ (j << 6);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) af[t] = as_bf16x8(*reinterpret_cast<const uint4*>(sa + (2 * wm + t) * 2048 + fo));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) bw[t] = as_bf16x8(*reinterpret_cast<const uint4*>(sb + (4 * wn + t) * 2048 + fo));
+  };
+  auto mfma_step = [&](const bf16x8_t (&af)[2], const bf16x8_t (&bw)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = mfma16x16x32(af[a], bw[b], acc[a][b]);
+  };
+  // group q from stage (ca, cb) (its step-0 fragments already in a0 / b0); hands over to (na, nb) and
+  // refills (ca, cb) with group q + 4
+  auto group = [&](char* ca, char* cb, const char* na, const char* nb, int q) __attribute__((always_inline)) {
+    read_ab(a1, b1, ca, cb, 1);
+    mfma_step(a0, b0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm((kTlStages - 2) * kTlLoads));  // this wave's part of the next stage landed
+    lds_barrier();  // every wave's part of the next stage is in LDS; every wave is done reading this one
+    read_ab(a0, b0, na, nb, 0);
+    mfma_step(a1, b1);
+    issue(ca, cb, q + kTlStages);
+  };
+  // the stage waits count loads per group in issue order: no load may move across a group
+  asm volatile("" ::: "memory");
+  issue(sa0, sb0, 0);
+  asm volatile("" ::: "memory");
+  issue(sa1, sb1, 1);
+  asm volatile("" ::: "memory");
+  issue(sa2, sb2, 2);
+  asm volatile("" ::: "memory");
+  issue(sa3, sb3, 3);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm((kTlStages - 1) * kTlLoads));
+  lds_barrier();  // stage 0 is in LDS
+  read_ab(a0, b0, sa0, sb0, 0);
+  // whole 512-K slices (8 groups, two turns of the 4 stages), each folded after its last group
+  const int full = KG / kTlGroupsPerSlice;
+  for (int sl = 0; sl < full; ++sl) {
+    const int q = sl * kTlGroupsPerSlice;
+    group(sa0, sb0, sa1, sb1, q);
+    group(sa1, sb1, sa2, sb2, q + 1);
+    group(sa2, sb2, sa3, sb3, q + 2);
+    group(sa3, sb3, sa0, sb0, q + 3);
+    group(sa0, sb0, sa1, sb1, q + 4);
+    group(sa1, sb1, sa2, sb2, q + 5);
+    group(sa2, sb2, sa3, sb3, q + 6);
+    group(sa3, sb3, sa0, sb0, q + 7);
+    fold();
+  }
+  // the last, partial slice (its first group sits on stage 0)
+  const int rem = KG - full * kTlGroupsPerSlice, q = full * kTlGroupsPerSlice;
+  if (rem > 0) {
+    group(sa0, sb0, sa1, sb1, q);
+    if (rem > 1) group(sa1, sb1, sa2, sb2, q + 1);
+    if (rem > 2) group(sa2, sb2, sa3, sb3, q + 2);
+    if (rem > 3) group(sa3, sb3, sa0, sb0, q + 3);
+    if (rem > 4) group(sa0, sb0, sa1, sb1, q + 4);
+    if (rem > 5) group(sa1, sb1, sa2, sb2, q + 5);
+    if (rem > 6) group(sa2, sb2, sa3, sb3, q + 6);
+    fold();
+  }
+  __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the loads issued past the end have landed
+  // lane (r, g) holds rows 16(2wm + a) + 4g + v of feature 16(4wn + b) + r
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int feat = n0 + 16 * (4 * wn + b) + r;
+      if (feat >= N) continue;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = m0 + 16 * (2 * wm + a) + 4 * g + v;
+        if (row < M) out[(size_t)row * N + feat] = tot[a][b][v];
+      }
+    }
+}
+
 int gemm_slices(int K) { return ((K + 127) / 128 + kKQW - 1) / kKQW; }
 
 size_t linear_partials_bytes(int M, int N, int K) { return (size_t)gemm_slices(K) * M * N * sizeof(float); }
@@ -491,6 +659,12 @@ int launch_gemm(const uint16_t* x, const uint16_t* W, int M, int N, int K, float
                 hipStream_t s) {
   if (M >= kTiledMinRows) {
     *slices = 1;
+    if (K % 64 == 0) {
+      const int tiles = ceil_div(N, kTileN) * ceil_div(M, kTileM);
+      hipLaunchKernelGGL(gemm_tiled_lds_kernel, dim3(8 * ceil_div(tiles, 8)), dim3(64 * kTiledWaves), 0, s, x, W, M,
+                         N, K, part);
+      return check_launch("gemm_tiled_lds");
+    }
     hipLaunchKernelGGL(gemm_tiled_bf16_kernel, dim3(ceil_div(N, kTileN), ceil_div(M, kTileM)),
                        dim3(64 * kTiledWaves), 0, s,
                        x, W, M, N, K, part);

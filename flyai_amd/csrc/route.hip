@@ -1,7 +1,7 @@
 // Router top-k softmax, expert histogram + stable permute, and unpermute/combine.
 // Index outputs are bit-exact against the oracle: the logits use one fixed fp32 summation order
-// (64 lane partials over k = lane + 64 j, then a xor butterfly 32,16,8,4,2,1) and ties in top-k
-// go to the lower expert id.
+// (64 lane partials, lane l over k = 512 j + 8 l + i in order, then a xor butterfly 32,16,8,4,2,1)
+// and ties in top-k go to the lower expert id.
 #include <type_traits>
 
 #include "common.h"
@@ -11,7 +11,8 @@ namespace flyai {
 // ------------------------------------------------------------------------------------------------
 // Router logits: workgroup = (TT tokens, 4*EPW experts); x rows staged in LDS; wave w owns EPW
 // experts.  Lane l accumulates k = 512 j + 8 l + i (i = 0..7) in order -- one 16-byte load of the
-// weight row and one 16-byte LDS read of x per chunk -- then a xor butterfly.  All JMAX weight
+// weight row and one 16-byte LDS read of x per chunk -- then a xor butterfly (as a reduce-scatter
+// over the wave's EPW x TT sums, wave_sum_scatter).  All JMAX weight
 // chunks of the wave's experts are loaded before the first FMA (one memory round trip).
 template <int TT, int EPW, int JMAX, bool ROUND_BF16>
 __global__ __launch_bounds__(256) void router_logits_kernel(
@@ -76,19 +77,19 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
       }
     }
   }
+  // the 64-lane sums of all EPW x TT partials (value c TT + t), the butterfly's additions as a
+  // reduce-scatter: lane l ends with value l >> shift
+  float part[EPW * TT];
 #pragma unroll
-  for (int c = 0; c < EPW; ++c) {
-    const float bias = (e0 + c < E && b) ? bf2f(b[e0 + c]) : 0.f;
+  for (int c = 0; c < EPW; ++c)
 #pragma unroll
-    for (int t = 0; t < TT; ++t) {
-      float v = acc[c][t];
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
-      if (lane == 0 && t < nt && e0 + c < E) {
-        const float r = v + bias;
-        logits[(size_t)(t0 + t) * E + e0 + c] = ROUND_BF16 ? bf16_round(r) : r;
-      }
-    }
+    for (int t = 0; t < TT; ++t) part[c * TT + t] = acc[c][t];
+  const float v = wave_sum_scatter<EPW * TT>(part);
+  constexpr int shift = wave_sum_scatter_shift<EPW * TT>();
+  const int idx = lane >> shift, c = idx / TT, t = idx % TT;
+  if ((lane & ((1 << shift) - 1)) == 0 && t < nt && e0 + c < E) {
+    const float r = v + (b ? bf2f(b[e0 + c]) : 0.f);
+    logits[(size_t)(t0 + t) * E + e0 + c] = ROUND_BF16 ? bf16_round(r) : r;
   }
 }
 

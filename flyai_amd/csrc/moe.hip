@@ -266,11 +266,12 @@ constexpr int kDepthDown = 8;
 //    flight than LDS could;
 //  * the activation rows (shared by all 8 waves) and the weight scales go global -> LDS directly
 //    (global_load_lds) through 4 stages of 28 KiB; a group's loads are issued 3 groups ahead;
-//  * activations sit in LDS in MFMA-fragment order: the 1 KiB block (m, j) holds, at 16*lane, the
-//    8 values lane (g, r) = (lane / 16, lane % 16) feeds to step j of row tile m (row 16m + r,
-//    K = 32g + 8j of the group).  The direct-to-LDS loads gather each lane's 16 bytes from its row,
-//    and every fragment read is one contiguous 1 KiB: ds_read_b128 runs conflict-free only for
-//    lane-contiguous addresses (16 rows at any stride, padded or XOR-swizzled, cost 2x);
+//  * activations sit in LDS row-major, a row tile (16 rows x 128 K) in 4 KiB, each row's sixteen
+//    16-byte chunks XOR-swizzled by the row: chunk c of row r at position c ^ r.  Each direct-to-LDS
+//    load fills 4 whole rows (16 consecutive lanes read one row's 256 contiguous bytes); a
+//    fragment-order load (16 rows x 16 B per lane group) streams from L2 at a third of the rate.
+//    Lane (g, r) = (lane / 16, lane % 16) feeds step j of row tile m with row 16m + r, K = 32g + 8j
+//    of the group, read from position (4g + j) ^ r: 16 lanes cover the 64 banks once;
 //  * the stages are separate LDS arrays with compile-time stage numbers, so the compiler can tell
 //    a stage's reads from the asynchronous writes into the other stages; each stage is waited for
 //    with an explicit vmcnt that leaves the 2 younger groups' loads in flight (vector-memory loads
@@ -419,17 +420,24 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
   };
   const int KGP = (gm.KG + kGemmStages - 1) / kGemmStages * kGemmStages;  // groups per block, padded
 
-  // activation DMA: instruction J fills fragment block b = J*8 + wave, i.e. row tile b / 4, step
-  // b % 4: the lane fetches row 16*(b/4) + r, elements 8*(4g + b%4) .. +7 of the group (an odd MT
-  // loads one more row tile, of clamped rows, that no MFMA reads)
+  // activation DMA: instruction J fills block b = J*8 + wave, rows 4 (b % 4) .. +3 of row tile b / 4:
+  // lane L writes position L % 16 of row rt = 4 (b % 4) + L / 16 and so fetches 16-byte chunk
+  // (L % 16) ^ rt of that row's 256 bytes (16 consecutive lanes read one row; an odd MT loads one
+  // more row tile, of clamped rows, that no MFMA reads)
   const uint16_t* arow[MD];
+  int ablk[MD];  // the 32-K block of the group the lane's chunk lies in
 #pragma unroll
   for (int J = 0; J < MD; ++J) {
     const int b = J * 8 + wave;
-    const int row = (b >> 2) * 16 + r;
+    const int rt = 4 * (b & 3) + (lane >> 4);
+    const int row = (b >> 2) * 16 + rt;
     const int p = c.row_lo + m0 + (row < rows ? row : 0);
-    arow[J] = c.act + (size_t)(GATE_UP ? c.perm[p] / c.k_top : p) * c.K + (4 * g + (b & 3)) * 8;
+    const int chunk = (lane & 15) ^ rt;
+    arow[J] = c.act + (size_t)(GATE_UP ? c.perm[p] / c.k_top : p) * c.K + chunk * 8;
+    ablk[J] = chunk >> 2;
   }
+  // step j's fragment of lane (g, r): row r, K 32g + 8j = chunk 4g + j at position (4g + j) ^ r
+  const int afrag = r * 256 + (((4 * g) ^ r) << 4);
   // the next group to load: block i_nb of the chunk (past the end: the last block), group i_kg
   int i_nb = 0, i_kg = 0;
   // the loads of that group: weights into the ring slot, then scales and activations into the
@@ -445,10 +453,13 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
     for (int n = 0; n < 2; ++n)
       __builtin_amdgcn_global_load_lds((const void*)(c.sbase + ((size_t)tile_of(nb, n) * gm.KG4 + min(kg / 4, gm.KG4 - 1)) * 256),
                                        (lds_ptr)(stage + ABYTES + (2 * wave + n) * 256), 4, 0, 0);
-    const int col = blk ? kg * 128 : 0;
+    // a chunk past the row's last block (or of a padding group) reads the row's first group instead:
+    // in bounds and finite, and multiplied only by zeroed weights
 #pragma unroll
-    for (int J = 0; J < MD; ++J)
+    for (int J = 0; J < MD; ++J) {
+      const int col = 4 * kg + ablk[J] < gm.G ? kg * 128 : 0;
       __builtin_amdgcn_global_load_lds((const void*)(arow[J] + col), (lds_ptr)(stage + (J * 8 + wave) * 1024), 16, 0, 0);
+    }
     if (++i_kg == KGP) {
       i_kg = 0;
       ++i_nb;
@@ -477,8 +488,9 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
     bok = 4 * kg + g < gm.G;  // the lane's weight block exists
   };
   auto read_a = [&](bf16x8_t (&a)[MT], const char* stage, auto j) __attribute__((always_inline)) {
+    const int fo = afrag ^ (int(j) << 4);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) a[m] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + (4 * m + j) * 1024 + lane * 16));
+    for (int m = 0; m < MT; ++m) a[m] = as_bf16x8(*reinterpret_cast<const uint4*>(stage + m * 4096 + fo));
   };
   auto cvt = [&](bf16x8_t (&b)[2], const u32x4 (&bq)[2], auto j) __attribute__((always_inline)) {
 #pragma unroll

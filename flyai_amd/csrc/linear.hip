@@ -493,10 +493,31 @@ constexpr int kTlStageBytes = 32 * 1024;  // A then B: [tile 8][step 2][lane 64]
 constexpr int kTlLoads = 4;               // load instructions per wave per group
 constexpr int kTlGroupsPerSlice = 8;      // 64-K groups per 512-K slice
 
+// The qkv projection's finalize, fused into the tiled GEMM's epilogue (head_dim 64, no tree): the
+// qkv_rope_kv_vec_kernel arithmetic on the folded sums -- x = bf16(sum + bias), then q and k rotated
+// (first = x1 c - x2 s, second = x2 c + x1 s, each product and sum rounded to bf16) -- q written to
+// q_out and k / v to the token's slab slot.  A wave's 64 features are one whole head and lane
+// (r, g) holds dims 16b + r of tiles b = 0..3, so each rotation pair (d, d + 32) sits in one lane.
+struct QkvEpilogue {
+  const uint16_t* bias;
+  const int32_t* positions;
+  const int32_t* seq_id;
+  const uint16_t* cos_tab;
+  const uint16_t* sin_tab;
+  const int64_t* kv_base;
+  const int32_t* kv_cap;
+  uint16_t* q_out;
+  uint16_t* k_pool;
+  uint16_t* v_pool;
+  int rope_positions, Hq, Hkv;
+};
+
+template <bool QKV>
 __global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_lds_kernel(const uint16_t* __restrict__ x,
                                                                           const uint16_t* __restrict__ W,
                                                                           int M, int N, int K,
-                                                                          float* __restrict__ out) {
+                                                                          float* __restrict__ out,
+                                                                          QkvEpilogue ep) {
   typedef __attribute__((address_space(3))) void* lds_ptr;
   // per stage: the A fragment blocks and the B fragment blocks as separate arrays
   __shared__ __align__(1024) char sa0[kTlStageBytes / 2], sb0[kTlStageBytes / 2];
@@ -628,18 +649,67 @@ __global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_lds_kernel(const 
   }
   __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));  // the loads issued past the end have landed
   // lane (r, g) holds rows 16(2wm + a) + 4g + v of feature 16(4wn + b) + r
+  if constexpr (!QKV) {
 #pragma unroll
-  for (int a = 0; a < 2; ++a)
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int feat = n0 + 16 * (4 * wn + b) + r;
-      if (feat >= N) continue;
+      for (int b = 0; b < 4; ++b) {
+        const int feat = n0 + 16 * (4 * wn + b) + r;
+        if (feat >= N) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = m0 + 16 * (2 * wm + a) + 4 * g + v;
+          if (row < M) out[(size_t)row * N + feat] = tot[a][b][v];
+        }
+      }
+  } else {
+    const int fb = n0 + 64 * wn;  // the wave's head: q heads, then k heads, then v heads
+    if (fb >= N) return;
+    const int hd = fb / 64;
+    float bv[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) bv[b] = ep.bias ? bf2f(ep.bias[fb + 16 * b + r]) : 0.f;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const int row = m0 + 16 * (2 * wm + a) + 4 * g + v;
-        if (row < M) out[(size_t)row * N + feat] = tot[a][b][v];
+        const int t = m0 + 16 * (2 * wm + a) + 4 * g + v;
+        if (t >= M) continue;
+        const int pos = ep.positions[t];
+        if (pos < 0 || pos >= ep.rope_positions) continue;  // outside the rotary table: no write
+        const int sq = ep.seq_id[t];
+        const int cap = ep.kv_cap[sq];
+        const int64_t base = ep.kv_base[sq];
+        const bool in_cap = pos < cap;
+        float xv[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) xv[b] = bf16_round(tot[a][b][v] + bv[b]);
+        if (hd < ep.Hq + ep.Hkv) {
+          if (hd >= ep.Hq && !in_cap) continue;
+          uint16_t* kh = ep.k_pool + base + (size_t)(hd - ep.Hq) * cap * 64;
+#pragma unroll
+          for (int b = 0; b < 2; ++b) {
+            const int d = 16 * b + r;
+            const float c = bf2f(ep.cos_tab[(size_t)pos * 32 + d]), sn = bf2f(ep.sin_tab[(size_t)pos * 32 + d]);
+            const float x1 = xv[b], x2 = xv[b + 2];
+            const uint16_t first = f2bf(bf16_round(bf16_round(x1 * c) - bf16_round(x2 * sn)));
+            const uint16_t second = f2bf(bf16_round(bf16_round(x2 * c) + bf16_round(x1 * sn)));
+            if (hd < ep.Hq) {
+              uint16_t* qr = ep.q_out + ((size_t)t * ep.Hq + hd) * 64;
+              qr[d] = first;
+              qr[d + 32] = second;
+            } else {
+              kh[kv_k_off(pos, d)] = first;
+              kh[kv_k_off(pos, d + 32)] = second;
+            }
+          }
+        } else if (in_cap) {
+          uint16_t* vh = ep.v_pool + base + (size_t)(hd - ep.Hq - ep.Hkv) * cap * 64;
+#pragma unroll
+          for (int b = 0; b < 4; ++b) vh[kv_v_off(pos, 16 * b + r)] = f2bf(xv[b]);
+        }
       }
-    }
+  }
 }
 
 int gemm_slices(int K) { return ((K + 127) / 128 + kKQW - 1) / kKQW; }
@@ -661,8 +731,8 @@ int launch_gemm(const uint16_t* x, const uint16_t* W, int M, int N, int K, float
     *slices = 1;
     if (K % 64 == 0) {
       const int tiles = ceil_div(N, kTileN) * ceil_div(M, kTileM);
-      hipLaunchKernelGGL(gemm_tiled_lds_kernel, dim3(8 * ceil_div(tiles, 8)), dim3(64 * kTiledWaves), 0, s, x, W, M,
-                         N, K, part);
+      hipLaunchKernelGGL(gemm_tiled_lds_kernel<false>, dim3(8 * ceil_div(tiles, 8)), dim3(64 * kTiledWaves), 0, s, x,
+                         W, M, N, K, part, QkvEpilogue{});
       return check_launch("gemm_tiled_lds");
     }
     hipLaunchKernelGGL(gemm_tiled_bf16_kernel, dim3(ceil_div(N, kTileN), ceil_div(M, kTileM)),
@@ -913,6 +983,15 @@ int launch_qkv_rope_kv(const uint16_t* x, const uint16_t* Wqkv, const uint16_t* 
                        uint16_t* k_pool, uint16_t* v_pool, const int32_t* kv_pos, hipStream_t s) {
   if (T == 0) return FLYAI_OK;
   const int width = (Hq + 2 * Hkv) * D;
+  if (T >= kTiledMinRows && H % 64 == 0 && D == 64 && !kv_pos) {
+    // prefill-sized: the finalize, RoPE and KV append in the tiled GEMM's epilogue (no fp32 plane)
+    const int tiles = ceil_div(width, kTileN) * ceil_div(T, kTileM);
+    const QkvEpilogue ep{bqkv, positions, seq_id, cos_tab, sin_tab, kv_base, kv_cap, q_out, k_pool, v_pool,
+                         rope_positions, Hq, Hkv};
+    hipLaunchKernelGGL(gemm_tiled_lds_kernel<true>, dim3(8 * ceil_div(tiles, 8)), dim3(64 * kTiledWaves), 0, s, x,
+                       Wqkv, T, width, H, part, ep);
+    return check_launch("gemm_tiled_lds_qkv");
+  }
   int slices = 0;
   int rc = launch_gemm(x, Wqkv, T, width, H, part, &slices, s);
   if (rc) return rc;

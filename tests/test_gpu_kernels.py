@@ -538,6 +538,31 @@ def test_batched_equals_solo_bit_exact():
         assert torch.equal(solo, batched[cu[b]:cu[b + 1]]), f"stream {b} differs solo vs batched"
 
 
+def test_prefill_batch_decode_rows_equal_solo_bit_exact():
+    """A 300-token prefill chunk makes the batch prefill-sized: the qkv projection then runs the tiled
+    GEMM with the finalize, RoPE and KV append in its epilogue, the o-projection the tiled GEMM and the
+    router the unfused path.  The decode rows beside it must come out as they do alone (split-K
+    projections, the separate qkv finalize kernel, the fused router finalizer), bit for bit."""
+    from gpu_harness import small_stage_case
+    from flyai_amd.runtime import RaggedStage
+    q_lens = [300, 1, 1, 4]
+    starts = [0, 700, 2100, 1500]
+    case = small_stage_case(n_layers=2, n_experts=16, seed=5, q_lens=q_lens, starts=starts, maxlen=4096)
+    kv0 = [(k.clone(), v.clone()) for k, v in zip(case["kv"].k, case["kv"].v)]
+    st = RaggedStage(case["shape"], case["layers"], case["rot"], case["kv"], 320, 4)
+    batched = st.forward(case["hidden"].clone(), q_lens, starts, list(range(4)))
+    torch.cuda.synchronize()
+    assert torch.isfinite(batched.float()).all()
+    cu = np.concatenate([[0], np.cumsum(q_lens)])
+    for b in (1, 2, 3):
+        for l, (k, v) in enumerate(kv0):
+            case["kv"].k[l].copy_(k)
+            case["kv"].v[l].copy_(v)
+        solo = st.forward(case["hidden"][cu[b]:cu[b + 1]].clone(), [q_lens[b]], [starts[b]], [b])
+        torch.cuda.synchronize()
+        assert torch.equal(solo, batched[cu[b]:cu[b + 1]]), f"stream {b} differs solo vs beside a prefill chunk"
+
+
 def test_dense_and_row_pass_experts_bit_identical():
     """The same rows through the row-pass expert kernel (a batch below the dense cutoff of 8 rows per
     expert on average) and through the dense tiled GEMM (a batch above it) give bit-identical h and y:

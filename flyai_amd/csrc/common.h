@@ -265,7 +265,7 @@ __device__ __forceinline__ void topk_softmax_lane(const float* __restrict__ lrow
   sort_ids_with_weights<K>(si, ex);
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    ids_out[j] = si[j];
+    ids_out[j] = (unsigned)si[j] < (unsigned)E ? si[j] : 0;  // a NaN row selects nothing: expert 0
     w_out[j] = ex[j] / sum;
   }
 }
@@ -310,7 +310,7 @@ __device__ __forceinline__ void topk_softmax_wave_vals(const float (&v)[4], int 
 #pragma unroll
   for (int j = 0; j < K; ++j)
     if (lane == j) {
-      ids_out[j] = si[j];
+      ids_out[j] = (unsigned)si[j] < (unsigned)E ? si[j] : 0;  // a NaN row selects nothing: expert 0
       w_out[j] = ex[j] / sum;
     }
 }
@@ -368,7 +368,7 @@ __device__ __forceinline__ void topk_softmax_group(const float* __restrict__ lro
   if (sub == 0) {
 #pragma unroll
     for (int j = 0; j < K; ++j) {
-      ids_out[j] = si[j];
+      ids_out[j] = (unsigned)si[j] < (unsigned)E ? si[j] : 0;  // a NaN row selects nothing: expert 0
       w_out[j] = ex[j] / sum;
     }
   }

@@ -666,47 +666,73 @@ __global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_lds_kernel(const 
     const int fb = n0 + 64 * wn;  // the wave's head: q heads, then k heads, then v heads
     if (fb >= N) return;
     const int hd = fb / 64;
+    const bool rotated = hd < ep.Hq + ep.Hkv;
+    // every load the 8 rows of the lane need goes out in two batches (indices, then the sequences'
+    // slab geometry and the rotary rows) before the first store
+    int pos[2][4], sq[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int t = min(m0 + 16 * (2 * wm + a) + 4 * g + v, M - 1);
+        pos[a][v] = ep.positions[t];
+        sq[a][v] = ep.seq_id[t];
+      }
     float bv[4];
 #pragma unroll
     for (int b = 0; b < 4; ++b) bv[b] = ep.bias ? bf2f(ep.bias[fb + 16 * b + r]) : 0.f;
+    int cap[2][4];
+    int64_t base[2][4];
+    float cs[2][4][2], sn[2][4][2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        cap[a][v] = ep.kv_cap[sq[a][v]];
+        base[a][v] = ep.kv_base[sq[a][v]];
+        const int pc = min(max(pos[a][v], 0), ep.rope_positions - 1);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          cs[a][v][b] = rotated ? bf2f(ep.cos_tab[(size_t)pc * 32 + 16 * b + r]) : 0.f;
+          sn[a][v][b] = rotated ? bf2f(ep.sin_tab[(size_t)pc * 32 + 16 * b + r]) : 0.f;
+        }
+      }
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int t = m0 + 16 * (2 * wm + a) + 4 * g + v;
-        if (t >= M) continue;
-        const int pos = ep.positions[t];
-        if (pos < 0 || pos >= ep.rope_positions) continue;  // outside the rotary table: no write
-        const int sq = ep.seq_id[t];
-        const int cap = ep.kv_cap[sq];
-        const int64_t base = ep.kv_base[sq];
-        const bool in_cap = pos < cap;
+        const int p = pos[a][v];
+        // rows past M, and positions outside the rotary table, write nothing
+        if (t >= M || p < 0 || p >= ep.rope_positions) continue;
+        const bool in_cap = p < cap[a][v];
         float xv[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) xv[b] = bf16_round(tot[a][b][v] + bv[b]);
-        if (hd < ep.Hq + ep.Hkv) {
+        if (rotated) {
           if (hd >= ep.Hq && !in_cap) continue;
-          uint16_t* kh = ep.k_pool + base + (size_t)(hd - ep.Hq) * cap * 64;
+          uint16_t* kh = ep.k_pool + base[a][v] + (size_t)(hd - ep.Hq) * cap[a][v] * 64;
 #pragma unroll
           for (int b = 0; b < 2; ++b) {
             const int d = 16 * b + r;
-            const float c = bf2f(ep.cos_tab[(size_t)pos * 32 + d]), sn = bf2f(ep.sin_tab[(size_t)pos * 32 + d]);
+            const float c = cs[a][v][b], s_ = sn[a][v][b];
             const float x1 = xv[b], x2 = xv[b + 2];
-            const uint16_t first = f2bf(bf16_round(bf16_round(x1 * c) - bf16_round(x2 * sn)));
-            const uint16_t second = f2bf(bf16_round(bf16_round(x2 * c) + bf16_round(x1 * sn)));
-            if (hd < ep.Hq) {
-              uint16_t* qr = ep.q_out + ((size_t)t * ep.Hq + hd) * 64;
-              qr[d] = first;
-              qr[d + 32] = second;
-            } else {
-              kh[kv_k_off(pos, d)] = first;
-              kh[kv_k_off(pos, d + 32)] = second;
-            }
+            const uint32_t first = f2bf(bf16_round(bf16_round(x1 * c) - bf16_round(x2 * s_)));
+            const uint32_t second = f2bf(bf16_round(bf16_round(x2 * c) + bf16_round(x1 * s_)));
+            // dims d and d + 1 sit in lanes r and r ^ 1 of the same row (both active or both not):
+            // the even lane stores the pair as one dword (q rows and the K slab keep them adjacent)
+            const uint32_t pair = __builtin_amdgcn_update_dpp(0, (int)(first | (second << 16)), 0xB1, 0xF, 0xF, false);
+            if (r & 1) continue;
+            const uint32_t lo = first | (pair << 16), hi = second | (pair & 0xffff0000u);
+            uint16_t* d1 = hd < ep.Hq ? ep.q_out + ((size_t)t * ep.Hq + hd) * 64 + d : kh + kv_k_off(p, d);
+            uint16_t* d2 = hd < ep.Hq ? ep.q_out + ((size_t)t * ep.Hq + hd) * 64 + d + 32 : kh + kv_k_off(p, d + 32);
+            *reinterpret_cast<uint32_t*>(d1) = lo;
+            *reinterpret_cast<uint32_t*>(d2) = hi;
           }
         } else if (in_cap) {
-          uint16_t* vh = ep.v_pool + base + (size_t)(hd - ep.Hq - ep.Hkv) * cap * 64;
+          uint16_t* vh = ep.v_pool + base[a][v] + (size_t)(hd - ep.Hq - ep.Hkv) * cap[a][v] * 64;
 #pragma unroll
-          for (int b = 0; b < 4; ++b) vh[kv_v_off(pos, 16 * b + r)] = f2bf(xv[b]);
+          for (int b = 0; b < 4; ++b) vh[kv_v_off(p, 16 * b + r)] = f2bf(xv[b]);
         }
       }
   }

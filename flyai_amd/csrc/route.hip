@@ -367,9 +367,11 @@ __device__ void permute_block(const int32_t* ids, int P, int E, int32_t* __restr
   const uint64_t lt = (lane == 0) ? 0ull : ((~0ull) >> (64 - lane));
   for (int base = beg; base < end; base += 64) {
     const int a = base + lane;
+    // an id outside [0, E) (a router row of NaN) counts as expert 0, so the histogram still sums to P
+    // and every slot gets a perm and an inv entry: the expert and combine kernels index with those
     int e = a < end ? ids[a] : -1;
-    const bool valid = e >= 0 && e < E;   // an out-of-range id is dropped, never indexes LDS
-    if (!valid) e = 0;
+    const bool valid = a < end;
+    if (e < 0 || e >= E) e = 0;
     const uint64_t peers = match_peers(e, valid, nbits);
     if (valid && (peers & lt) == 0) cnt[wave][e] += __popcll(peers);
   }
@@ -400,8 +402,8 @@ __device__ void permute_block(const int32_t* ids, int P, int E, int32_t* __restr
   for (int base = beg; base < end; base += 64) {
     const int a = base + lane;
     int e = a < end ? ids[a] : -1;
-    const bool valid = e >= 0 && e < E;
-    if (!valid) e = 0;
+    const bool valid = a < end;
+    if (e < 0 || e >= E) e = 0;
     const uint64_t peers = match_peers(e, valid, nbits);
     if (valid) {
       const int pos = cnt[wave][e] + __popcll(peers & lt);

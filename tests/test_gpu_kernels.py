@@ -159,6 +159,32 @@ def test_permute_bit_exact(T, k, E, mode):
     assert np.array_equal(inv.cpu().numpy(), ri)
 
 
+def test_nan_router_rows_route_consistently():
+    """A router row of NaN (a NaN hidden state) must not break the routing's index invariants: the
+    expert and combine kernels index with perm, inv and offsets.  The top-k gives such a row
+    in-range ids, and the permute counts any id outside [0, E) as expert 0, so the histogram sums to
+    T*k and perm / inv stay a permutation and its inverse."""
+    from flyai_amd import ops
+    T, H, E, k = 40, 2880, 128, 4
+    g = _gen(140)
+    x = torch.randn(T, H, device=DEV, generator=g).to(torch.bfloat16)
+    x[3] = float("nan")
+    x[17, 5] = float("nan")
+    rw = (0.02 * torch.randn(E, H, device=DEV, generator=g)).to(torch.bfloat16)
+    rb = torch.zeros(E, device=DEV, dtype=torch.bfloat16)
+    ids, wts = ops.router_topk_softmax(x, rw, rb, k)
+    ids_h = ids.cpu().numpy()
+    assert ((ids_h >= 0) & (ids_h < E)).all(), "router ids out of range on a NaN row"
+    # ids outside [0, E) straight into the permute: counted as expert 0
+    bad = ids_h.copy()
+    bad[0] = [-1, E, 2**31 - 1, 7]
+    hist, off, perm, inv = ops.moe_permute(torch.tensor(bad, dtype=torch.int32, device=DEV), E)
+    want = np.where((bad >= 0) & (bad < E), bad, 0)
+    rh, ro, rp, ri = oroute.permute(want, E)
+    assert np.array_equal(hist.cpu().numpy(), rh) and np.array_equal(off.cpu().numpy(), ro)
+    assert np.array_equal(perm.cpu().numpy(), rp) and np.array_equal(inv.cpu().numpy(), ri)
+
+
 def test_combine_matches_oracle():
     from flyai_amd import ops
     T, k, H = 56, 4, 2880

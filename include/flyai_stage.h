@@ -61,7 +61,8 @@ int flyai_pack_ragged(const int32_t* q_lens, const int32_t* starts, const int64_
  * routing_torch_dist :435-444).  x bf16 [T,H], w bf16 [E,H], b bf16 [E].  Logits are the bf16
  * rounding of an fp32 dot product in a fixed order (64 lane partials, lane l summing
  * k = 512j + 8l + i in order, then a xor butterfly 32..1) plus bias; top-k by (value desc, id asc);
- * softmax over the k selected values in fp32; each row's ids sorted ascending with their weights.
+ * softmax over the k selected values in fp32; each row's ids sorted ascending with their weights
+ * (a row of NaN logits selects nothing by value; its slots get id 0).
  * H % 8 == 0, H <= 7168, E % 4 == 0, E <= 256, k in {2, 4, 8}.  logits_out (fp32 [T,E], required) receives the
  * bf16-valued logits and is the scratch between the logits and top-k kernels. */
 int flyai_router_topk_softmax(const uint16_t* x, const uint16_t* w, const uint16_t* b, int32_t T,
@@ -73,7 +74,9 @@ int flyai_router_topk_softmax(const uint16_t* x, const uint16_t* w, const uint16
  * (transformers/integrations/mxfp4.py:449-457) and the one_hot/where expert loop of
  * GptOssExperts.forward (modeling_gpt_oss.py:93-107).  topk_ids int32 [T*k] in [0,E).
  * hist[E], offsets[E+1] (exclusive scan), perm[T*k] (experts ascending, flat index ascending
- * within an expert), inv[T*k] (inverse).  T*k <= 65536, E <= 256. */
+ * within an expert), inv[T*k] (inverse).  T*k <= 65536, E <= 256.  An id outside [0,E) (a router row
+ * of NaN) is counted as expert 0, so hist sums to T*k and perm / inv stay a permutation and its
+ * inverse whatever the ids hold (the expert and combine kernels index with them). */
 int flyai_moe_permute(const int32_t* topk_ids, int32_t T, int32_t k, int32_t E, int32_t* hist,
                       int32_t* offsets, int32_t* perm, int32_t* inv, flyai_stream_t stream);
 

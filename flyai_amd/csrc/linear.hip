@@ -477,8 +477,9 @@ __global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_bf16_kernel(const
 // tile, 8 waves of 32 rows x 64 features and per-element arithmetic, but the operand tiles go
 // global -> LDS directly (global_load_lds, no register staging) through 4 stages of one 64-K group
 // each (A and B: 8 row tiles of 2 KiB per stage, 4 load instructions per wave, each reading whole
-// 128-byte rows), a group's loads issued 3 groups ahead.  The stages are separate LDS arrays with compile-time stage numbers,
-// so the compiler can tell a stage's reads from the DMA writes into the others; each stage is
+// 128-byte rows), a group's loads issued 3 groups ahead.  The stages (A and B apart) are separate
+// LDS arrays with compile-time stage numbers, so the compiler can tell a stage's reads from the DMA
+// writes into the others; each stage is
 // waited for with an explicit vmcnt that leaves the 2 younger groups' loads in flight (vector
 // memory loads complete in issue order), then one barrier per group, which also tells the waves
 // that the stage just read can be refilled.  The next group's step-0 fragments are read under the
@@ -489,7 +490,7 @@ __global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_bf16_kernel(const
 // and no group carries a branch.  Rows and features past M / N load clamped rows and are never
 // stored; the groups issued past the end read the last group and are never computed on.
 constexpr int kTlStages = 4;
-constexpr int kTlStageBytes = 32 * 1024;  // A then B: [tile 8][step 2][lane 64] x 16 B each
+constexpr int kTlStageBytes = 32 * 1024;  // A and B halves: 8 row tiles x 16 rows x 128 B each
 constexpr int kTlLoads = 4;               // load instructions per wave per group
 constexpr int kTlGroupsPerSlice = 8;      // 64-K groups per 512-K slice
 

@@ -17,8 +17,10 @@ Two ways to get such a dict here:
 * ``parts_from_reference(parts)`` -- converts a dict whose ``layers`` are transformers
   ``GptOssDecoderLayer`` modules (what the reference's ``load_stage`` returns) by reading the modules'
   own parameters: ``input_layernorm``, ``post_attention_layernorm``, ``self_attn.{q,k,v,o}_proj``,
-  ``self_attn.sinks``, ``mlp.router`` and the packed MXFP4 experts (``mlp.experts.<proj>_blocks`` /
-  ``<proj>_scales``, or raw ``<proj>`` bytes with ``<proj>_scales``, plus ``<proj>_bias``).
+  ``self_attn.sinks``, ``mlp.router`` and the packed MXFP4 experts with their ``<proj>_bias``.  The
+  experts may hold the wrapped tensors native MXFP4 loading leaves (``<proj>`` with
+  ``<proj>_precision_config``, the form the reference's ``load_stage`` produces), ``<proj>_blocks`` /
+  ``<proj>_scales``, or raw ``<proj>`` bytes with ``<proj>_scales``.
 
 Either way the dict keeps the reference's keys, and ``embed`` / ``norm`` / ``lm_head`` are callables
 over the HIP kernels (``flyai_embed_gather``, ``flyai_rmsnorm``, ``flyai_lm_head_argmax``).  The
@@ -131,16 +133,88 @@ def _param(module, path):
     return obj.detach() if torch.is_tensor(obj) else obj
 
 
+def _is_wrapped(value):
+    """A kernel-library tensor wrapper (what transformers attaches on native MXFP4 loading): an object,
+    not a torch tensor, whose ``storage`` holds the physical bytes in ``data`` and their ``layout``."""
+    storage = getattr(value, "storage", None)
+    return not torch.is_tensor(value) and torch.is_tensor(getattr(storage, "data", None))
+
+
+def _unswizzled(value, what, logical, packed, padded, dtypes):
+    """The bytes of a wrapped tensor in its logical, unswizzled [E, K-side, N] order.
+
+    The checks restate the reference guard's for the wrapped form (``phase0/mxfp4_guard.py:232-243``,
+    ``:264-267``): the published logical shape, the physical byte count between the packed and the
+    512-padded size, and the storage dtype.  The layout object undoes its own swizzle
+    (``storage.layout.unswizzle_data``, the call transformers' reverse op makes,
+    ``transformers/integrations/mxfp4.py:203-222``); nothing of the kernel library is imported here.
+    A layout that keeps its padding after unswizzling has it cut from the ends of the last two axes."""
+    if tuple(getattr(value, "shape", ())) != tuple(logical):
+        raise MXFP4LayoutError(f"{what} has logical shape {tuple(getattr(value, 'shape', ()))}, "
+                               f"expected {tuple(logical)}")
+    data = value.storage.data
+    if data.dtype not in dtypes:
+        raise MXFP4LayoutError(f"{what} storage holds {data.dtype}, not packed bytes")
+    nbytes = data.numel() * data.element_size()
+    if not packed <= nbytes <= padded:
+        raise MXFP4LayoutError(f"{what} storage has {nbytes} bytes, outside [{packed}, {padded}]")
+    unswizzle = getattr(getattr(value.storage, "layout", None), "unswizzle_data", None)
+    if unswizzle is None:
+        raise MXFP4LayoutError(f"{what} storage layout has no unswizzle_data")
+    out = unswizzle(data)
+    E, k, n = logical[0], packed // (logical[0] * logical[2]), logical[2]
+    if not torch.is_tensor(out) or out.dim() != 3 or out.shape[0] != E or out.shape[1] < k or out.shape[2] < n:
+        raise MXFP4LayoutError(f"{what} unswizzles to {tuple(getattr(out, 'shape', ()))}, expected {(E, k, n)}")
+    if out.dtype != torch.uint8:
+        out = out.view(torch.uint8)
+    return out[:, :k, :n]
+
+
+def _wrapped_storage(experts, proj, rows, cols, n_experts):
+    """(blocks, scales) of a wrapped projection, in the raw checkpoint layout.
+
+    The wrapper publishes the transposed logical shape [E, cols, rows] (K before N) and stores the
+    fp4 codes two per byte along K; its scales ride in ``<proj>_precision_config.weight_scale`` with
+    logical shape [E, cols/32, rows].  Transposing the unswizzled bytes back gives the checkpoint's
+    [E, rows, cols/2] codes and [E, rows, cols/32] scales (transformers' reverse op, ``mxfp4.py:203-222``)."""
+    raw = getattr(experts, proj)
+    if not ("fp4" in str(getattr(raw, "dtype", "")).lower()):
+        raise MXFP4LayoutError(f"experts.{proj} wrapper is not FP4 ({getattr(raw, 'dtype', None)})")
+    logical = (n_experts, cols, rows)
+    packed = n_experts * rows * cols // 2
+    padded = n_experts * -(-cols // 512) * 512 * -(-rows // 512) * 512 // 2
+    codes = _unswizzled(raw, f"experts.{proj}", logical, packed, padded, (torch.uint8,))
+    scale = getattr(getattr(experts, proj + "_precision_config", None), "weight_scale", None)
+    if scale is None:
+        raise MXFP4LayoutError(f"experts.{proj}_precision_config has no weight_scale")
+    sdt = tuple(t for t in (torch.uint8, getattr(torch, "float8_e8m0fnu", None)) if t is not None)
+    slogical = (n_experts, cols // 32, rows)
+    if _is_wrapped(scale):
+        sbytes = _unswizzled(scale, f"experts.{proj} weight_scale", slogical, packed // 16, padded // 16, sdt)
+    else:
+        if not torch.is_tensor(scale) or tuple(scale.shape) != slogical or scale.dtype not in sdt:
+            raise MXFP4LayoutError(f"experts.{proj} weight_scale is not E8M0 bytes of shape {slogical}")
+        sbytes = scale.view(torch.uint8)
+    blocks = codes.detach().transpose(1, 2).contiguous().reshape(n_experts, rows, cols // 32, 16)
+    scales = sbytes.detach().transpose(1, 2).contiguous()
+    return blocks, scales
+
+
 def _expert_storage(experts, proj, rows, cols, n_experts):
-    """(blocks u8 [E, rows, cols/32, 16], scales u8 [E, rows, cols/32]) of one packed projection."""
+    """(blocks u8 [E, rows, cols/32, 16], scales u8 [E, rows, cols/32]) of one packed projection:
+    ``<proj>_blocks`` + ``<proj>_scales`` (before the load swizzle), raw ``<proj>`` bytes +
+    ``<proj>_scales``, or the wrapped ``<proj>`` + ``<proj>_precision_config`` that native MXFP4 loading
+    leaves (``phase0/pipeline.py:147-160``)."""
+    if getattr(experts, proj + "_blocks", None) is None and _is_wrapped(getattr(experts, proj, None)):
+        return _wrapped_storage(experts, proj, rows, cols, n_experts)
     blocks = getattr(experts, proj + "_blocks", None)
     if blocks is None:
         blocks = getattr(experts, proj, None)
     scales = getattr(experts, proj + "_scales", None)
     if not torch.is_tensor(blocks) or not torch.is_tensor(scales):
         raise MXFP4LayoutError(
-            f"experts.{proj} is not raw packed MXFP4 with {proj}_scales (a swizzled or dequantized expert "
-            "cannot be re-packed); load the stage with flyai_amd.stage_parts.load_stage instead")
+            f"experts.{proj} is neither packed MXFP4 with {proj}_scales nor a wrapped MXFP4 tensor (a "
+            "dequantized expert cannot be re-packed); load the stage with flyai_amd.stage_parts.load_stage instead")
     blocks, scales = blocks.detach(), scales.detach()
     if blocks.dtype != torch.uint8:
         raise MXFP4LayoutError(f"experts.{proj} holds {blocks.dtype}, not packed E2M1 bytes")

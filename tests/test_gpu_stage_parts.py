@@ -1,18 +1,25 @@
 """The reference-shaped ``parts`` dict drives the stage on the GPU.
 
-A dict like the reference's ``load_stage`` returns (``phase0/pipeline.py:166-179``: transformers
-``GptOssDecoderLayer`` modules with packed MXFP4 experts, the model's rotary module, ``_model.config``,
-``sliding``/``window``, and ``embed``/``norm``/``lm_head`` modules) goes straight into
-``FastVerifyStage`` and ``BatchedFastVerifyStage`` (the call sites ``phase0/specpipe.py:544``, ``:666``).
+A dict like the reference's ``load_stage`` returns (``phase0/pipeline.py:166-179``: decoder-layer
+modules under transformers' ``GptOssDecoderLayer`` attribute names with packed MXFP4 experts, the
+model's rotary module, ``_model.config``, ``sliding``/``window``, and ``embed``/``norm``/``lm_head``
+modules) goes straight into ``FastVerifyStage`` and ``BatchedFastVerifyStage`` (the call sites
+``phase0/specpipe.py:544``, ``:666``).  The experts come in both forms: packed blocks and scales, and
+the wrapped codes with precision configs that native MXFP4 loading leaves (``pipeline.py:147-160``).
+The modules are plain containers and the rotary values come from a committed fixture, so nothing of
+transformers runs here.
 Its steps must equal, bit for bit, the steps of the stage built from the same tensors as this build's
 own ``LayerWeights`` -- which the oracle parity tests cover -- so the adapter reads every tensor from
 the right attribute.  The head and tail callables (``specpipe.py:596``, ``:611-612``, ``:796``) are
 checked against the embedding rows, the oracle's RMSNorm and an fp64 logit product."""
+import os
 from types import SimpleNamespace
 
 import numpy as np
 import pytest
 import torch
+
+from conftest import GOLDEN
 
 pytestmark = pytest.mark.gpu
 
@@ -20,45 +27,61 @@ DEV = "cuda"
 E, V = 8, 4096
 
 
-def _reference_parts(layers, shape, vocab_weights):
-    from transformers import GptOssConfig
-    from transformers.models.gpt_oss.modeling_gpt_oss import GptOssDecoderLayer, GptOssRMSNorm, GptOssRotaryEmbedding
-    cfg = GptOssConfig(hidden_size=shape.hidden, intermediate_size=shape.intermediate,
-                       num_attention_heads=shape.n_q_heads, num_key_value_heads=shape.n_kv_heads,
-                       head_dim=shape.head_dim, num_local_experts=E, num_experts_per_tok=shape.top_k,
-                       num_hidden_layers=len(layers), sliding_window=shape.window, vocab_size=V)
+def _holder(**tensors):
+    """A plain module carrying parameters under transformers' attribute names."""
+    m = torch.nn.Module()
+    for k, v in tensors.items():
+        if torch.is_tensor(v):
+            m.register_parameter(k, torch.nn.Parameter(v.detach().clone(), requires_grad=False))
+        else:
+            setattr(m, k, v)
+    return m
+
+
+def _rotary_module():
+    """The model's rotary module as the stage reads it: ``inv_freq`` and ``attention_scaling``, the
+    values transformers' ``GptOssRotaryEmbedding`` holds for the GPT-OSS config (committed fixture)."""
+    f = np.load(os.path.join(GOLDEN, "rope_yarn.npz"))
+    m = torch.nn.Module()
+    m.register_buffer("inv_freq", torch.from_numpy(f["inv_freq"]))
+    m.attention_scaling = float(f["attention_scaling"])
+    return m
+
+
+def _reference_parts(layers, shape, vocab_weights, wrapped=False):
+    """What the reference's ``load_stage`` returns (``phase0/pipeline.py:166-179``), with each decoder
+    layer a module tree under transformers' ``GptOssDecoderLayer`` attribute names.  ``wrapped`` gives
+    the experts the form native MXFP4 loading leaves (wrapped codes + precision configs)."""
+    from wrapped_mxfp4 import wrap_projection
+    cfg = SimpleNamespace(hidden_size=shape.hidden, intermediate_size=shape.intermediate,
+                          num_attention_heads=shape.n_q_heads, num_key_value_heads=shape.n_kv_heads,
+                          head_dim=shape.head_dim, num_local_experts=E, num_experts_per_tok=shape.top_k,
+                          num_hidden_layers=len(layers), sliding_window=shape.window, vocab_size=V,
+                          rms_norm_eps=shape.rms_eps, max_position_embeddings=2048)
     nq, nkv = shape.n_q_heads * shape.head_dim, shape.n_kv_heads * shape.head_dim
-    P = lambda t: torch.nn.Parameter(t.detach().clone(), requires_grad=False)
     mods = []
-    for i, lw in enumerate(layers):
-        with torch.device("meta"):
-            m = GptOssDecoderLayer(cfg, i)
-        at = m.self_attn
-        at.q_proj.weight, at.k_proj.weight, at.v_proj.weight = (P(w) for w in lw.wqkv.split([nq, nkv, nkv]))
-        at.q_proj.bias, at.k_proj.bias, at.v_proj.bias = (P(b) for b in lw.bqkv.split([nq, nkv, nkv]))
-        at.o_proj.weight, at.o_proj.bias = P(lw.wo), P(lw.bo)
-        at.sinks = P(lw.sinks.to(torch.bfloat16))           # the checkpoint's sinks are bf16
-        m.input_layernorm.weight, m.post_attention_layernorm.weight = P(lw.ln1), P(lw.ln2)
-        m.mlp.router.weight, m.mlp.router.bias = P(lw.router_w), P(lw.router_b)
-        ex = torch.nn.Module()
-        ex.gate_up_proj_blocks, ex.gate_up_proj_scales = P(lw.w13_blocks), P(lw.w13_scales)
-        ex.down_proj_blocks, ex.down_proj_scales = P(lw.w2_blocks), P(lw.w2_scales)
-        ex.gate_up_proj_bias, ex.down_proj_bias = P(lw.b13), P(lw.b2)
-        m.mlp.experts = ex
-        mods.append(m)
+    for lw in layers:
+        (wq, wk, wv), (bq, bk, bv) = lw.wqkv.split([nq, nkv, nkv]), lw.bqkv.split([nq, nkv, nkv])
+        at = _holder(q_proj=_holder(weight=wq, bias=bq), k_proj=_holder(weight=wk, bias=bk),
+                     v_proj=_holder(weight=wv, bias=bv), o_proj=_holder(weight=lw.wo, bias=lw.bo),
+                     sinks=lw.sinks.to(torch.bfloat16))          # the checkpoint's sinks are bf16
+        ex = _holder(gate_up_proj_blocks=lw.w13_blocks, gate_up_proj_scales=lw.w13_scales,
+                     down_proj_blocks=lw.w2_blocks, down_proj_scales=lw.w2_scales,
+                     gate_up_proj_bias=lw.b13, down_proj_bias=lw.b2)
+        if wrapped:
+            wrap_projection(ex, "gate_up_proj", lw.w13_blocks, lw.w13_scales)
+            wrap_projection(ex, "down_proj", lw.w2_blocks, lw.w2_scales)
+        mlp = _holder(router=_holder(weight=lw.router_w, bias=lw.router_b), experts=ex)
+        mods.append(_holder(input_layernorm=_holder(weight=lw.ln1), post_attention_layernorm=_holder(weight=lw.ln2),
+                            self_attn=at, mlp=mlp))
     emb_w, norm_w, head_w = vocab_weights
-    embed = torch.nn.Embedding(V, shape.hidden, device=DEV, dtype=torch.bfloat16)
-    embed.weight = P(emb_w)
-    norm = GptOssRMSNorm(shape.hidden, eps=shape.rms_eps).to(DEV)
-    norm.weight = P(norm_w)
-    head = torch.nn.Linear(shape.hidden, V, bias=False, device=DEV, dtype=torch.bfloat16)
-    head.weight = P(head_w)
-    return {"layers": torch.nn.ModuleList(mods), "rotary": GptOssRotaryEmbedding(cfg),
+    return {"layers": torch.nn.ModuleList(mods), "rotary": _rotary_module(),
             "_model": SimpleNamespace(config=cfg), "sliding": [lw.sliding for lw in layers], "window": shape.window,
-            "n_layers": len(layers), "lo": 0, "hi": len(layers), "embed": embed, "norm": norm, "lm_head": head}
+            "n_layers": len(layers), "lo": 0, "hi": len(layers), "embed": _holder(weight=emb_w),
+            "norm": _holder(weight=norm_w), "lm_head": _holder(weight=head_w)}
 
 
-def _setup():
+def _setup(wrapped=False):
     from flyai_amd.rope import YarnRotary
     from flyai_amd.weights import GptOssShape, synthetic_layer
     shape = GptOssShape(n_experts=E)
@@ -69,12 +92,13 @@ def _setup():
              (1 + 0.05 * torch.randn(shape.hidden, device=DEV, generator=g)).float(),
              (torch.randn(V, shape.hidden, device=DEV, generator=g) * 0.02).to(torch.bfloat16))
     ours = {"layers": layers, "rotary": YarnRotary(2048, device=DEV), "shape": shape}
-    return shape, layers, ours, _reference_parts(layers, shape, vocab), vocab, g
+    return shape, layers, ours, _reference_parts(layers, shape, vocab, wrapped), vocab, g
 
 
-def test_fast_verify_from_reference_parts_equals_own_parts():
+@pytest.mark.parametrize("wrapped", [False, True])
+def test_fast_verify_from_reference_parts_equals_own_parts(wrapped):
     from flyai_amd.runtime import FastVerifyStage
-    shape, _, ours, ref, _, g = _setup()
+    shape, _, ours, ref, _, g = _setup(wrapped)
     fv_ref, fv_own = FastVerifyStage(ref, maxlen=2048), FastVerifyStage(ours, maxlen=2048)
     assert fv_ref.shape == shape
     h = torch.randn(1, 40, shape.hidden, device=DEV, generator=g).to(torch.bfloat16)
@@ -88,9 +112,10 @@ def test_fast_verify_from_reference_parts_equals_own_parts():
         assert torch.equal(a, b), f"decode step {step} differs"
 
 
-def test_batched_fast_verify_from_reference_parts():
+@pytest.mark.parametrize("wrapped", [False, True])
+def test_batched_fast_verify_from_reference_parts(wrapped):
     from flyai_amd.runtime import BatchedFastVerifyStage
-    shape, _, ours, ref, _, g = _setup()
+    shape, _, ours, ref, _, g = _setup(wrapped)
     bref, bown = BatchedFastVerifyStage(ref, 3, maxlen=2048), BatchedFastVerifyStage(ours, 3, maxlen=2048)
     h = torch.randn(3, 5, shape.hidden, device=DEV, generator=g).to(torch.bfloat16)
     starts = torch.tensor([0, 17, 300])

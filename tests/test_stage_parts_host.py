@@ -118,3 +118,65 @@ def test_as_stage_parts_passes_our_own_dict_through():
     parts = {"layers": [], "rotary": None}
     out = stage_parts.as_stage_parts(parts, "cpu")
     assert out["layers"] == [] and out["shape"] is not None
+
+
+# ---- the wrapped form native MXFP4 loading leaves (phase0/pipeline.py:147-160) -------------------
+
+def _wrapped_layer(cfg, seed, keep_padding=False, e8m0=False):
+    from wrapped_mxfp4 import wrap_projection
+    layer = _mxfp4_layer(cfg, seed, e8m0_scales=e8m0)
+    ex = layer.mlp.experts
+    raw = {p: (getattr(ex, p + "_blocks").detach().clone(), getattr(ex, p + "_scales").detach().view(torch.uint8).clone())
+           for p in ("gate_up_proj", "down_proj")}
+    for p, (b, s) in raw.items():
+        wrap_projection(ex, p, b, getattr(ex, p + "_scales").detach() if e8m0 else s, keep_padding=keep_padding)
+    return layer, raw
+
+
+@pytest.mark.parametrize("keep_padding,e8m0", [(False, False), (True, False), (False, True)])
+def test_wrapped_experts_repack_to_the_raw_bytes(keep_padding, e8m0):
+    cfg = _config()
+    layer, raw = _wrapped_layer(cfg, 11, keep_padding, e8m0)
+    ex = layer.mlp.experts
+    assert not hasattr(ex, "gate_up_proj_blocks") and not hasattr(ex, "down_proj_scales")
+    # the stand-in swizzle really moves the bytes, so reading storage.data as it lies would fail
+    codes = raw["gate_up_proj"][0].reshape(E, 2 * I, H // 2).transpose(1, 2).reshape(-1)
+    assert not torch.equal(ex.gate_up_proj.storage.data.reshape(-1)[:codes.numel()], codes)
+    t = stage_parts.module_tensors(layer, _shape(cfg), sliding=False)
+    for key, proj in (("w13", "gate_up_proj"), ("w2", "down_proj")):
+        b, s = raw[proj]
+        assert t[key + "_blocks"].dtype == torch.uint8 and torch.equal(t[key + "_blocks"], b), proj
+        assert t[key + "_scales"].dtype == torch.uint8 and torch.equal(t[key + "_scales"], s), proj
+
+
+def test_wrapped_experts_checked_like_the_reference_guard():
+    from wrapped_mxfp4 import WrappedTensor
+    cfg = _config()
+    sh = _shape(cfg)
+    # logical shape not the transposed [E, K, N]
+    layer, _ = _wrapped_layer(cfg, 12)
+    layer.mlp.experts.down_proj.shape = torch.Size((E, H, I))
+    with pytest.raises(MXFP4LayoutError, match="logical shape"):
+        stage_parts.module_tensors(layer, sh, sliding=False)
+    # physical storage smaller than the packed bytes
+    layer, _ = _wrapped_layer(cfg, 13)
+    w = layer.mlp.experts.gate_up_proj
+    w.storage.data = w.storage.data.reshape(-1)[:100].clone()
+    with pytest.raises(MXFP4LayoutError, match="bytes"):
+        stage_parts.module_tensors(layer, sh, sliding=False)
+    # an expanded (non-FP4) wrapper
+    layer, _ = _wrapped_layer(cfg, 14)
+    layer.mlp.experts.down_proj.dtype = torch.bfloat16
+    with pytest.raises(MXFP4LayoutError, match="not FP4"):
+        stage_parts.module_tensors(layer, sh, sliding=False)
+    # scales missing from the precision config
+    layer, _ = _wrapped_layer(cfg, 15)
+    layer.mlp.experts.gate_up_proj_precision_config.weight_scale = None
+    with pytest.raises(MXFP4LayoutError, match="weight_scale"):
+        stage_parts.module_tensors(layer, sh, sliding=False)
+    # a layout that cannot unswizzle
+    layer, _ = _wrapped_layer(cfg, 16)
+    layer.mlp.experts.down_proj.storage.layout = object()
+    with pytest.raises(MXFP4LayoutError, match="unswizzle_data"):
+        stage_parts.module_tensors(layer, sh, sliding=False)
+    assert isinstance(_wrapped_layer(cfg, 17)[0].mlp.experts.down_proj, WrappedTensor)

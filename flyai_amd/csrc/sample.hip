@@ -316,11 +316,12 @@ __global__ __launch_bounds__(kSampThreads) void sample_rows_kernel(
     if (tid == 0) {
       int a = V;
       for (int w = 0; w < kSampWaves; ++w) a = min(a, (int)sh.red32[w]);
-      draw[row] = a;
+      draw[row] = a < V ? a : 0;  // every weight 0 (a non-finite row): the first id, as argmax of zeros
     }
     return;
   }
-  const double uu = u[row];
+  double uu = u[row];
+  if (!(uu >= 0.0)) uu = 0.0;  // u below 0 (or NaN) draws as 0; u >= 1 is held at Wr - 1 below
   uint64_t target = (uint64_t)(uu * (double)Wr);
   if (target >= Wr) target = Wr - 1;
   const uint64_t base = sh.scan[tid];

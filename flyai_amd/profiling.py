@@ -248,15 +248,17 @@ def _run(cmd, log, timeout):
         subprocess.run(cmd, stdout=f, stderr=subprocess.STDOUT, timeout=timeout, check=True)
 
 
-def collect(out, name, bench_args, python="python3", timeout=300):
+def collect(out, name, bench_args, python=None, timeout=300):
     """Kernel trace + the PMC_PASSES counter passes of ``bench.py bench_args`` under rocprofv3, each a
     child process (this process never touches the GPU), then the counter table (``name_counters.md``
     and ``.json``) and the kernel table (``name_kernel_stats.md``).  Raw rocprofv3 output is removed;
-    the kernel trace is kept gzipped."""
+    the kernel trace is kept gzipped.  The program after rocprofv3's ``--`` is the interpreter binary
+    itself (this process's, symlinks resolved), so no launcher or shim runs between the profiler's
+    preloaded library and bench.py."""
     import gzip
     import shutil
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-    bench = [python, os.path.join(root, "bench.py")]
+    bench = [python or os.path.realpath(sys.executable), os.path.join(root, "bench.py")]
     os.makedirs(out, exist_ok=True)
     trace = os.path.join(out, name + "_trace")
     cmds = [["rocprofv3", "--kernel-trace", "--stats", "-f", "csv", "-d", trace, "-o", "run", "--", *bench,

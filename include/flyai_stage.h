@@ -341,12 +341,14 @@ int flyai_hbm_read_probe(const void* src, size_t bytes, int32_t nontemporal, int
  * (0 < top_k < V) keeps z >= the k-th largest z; weights w = floor(2^40 e^(z - max z)) as exact integers
  * (a fixed fp64 exp); top-p (0 < top_p < 1) keeps, in (z desc, id asc) order, each token whose preceding
  * weight is <= floor(top_p * W); the distribution is w / W over what is kept.  Outputs (each nullable):
- * p_draft[r] = the kept probability of token draft[r] (draft nullable; -1 = none); probs [R, V] fp32 the
+ * p_draft[r] = the kept probability of token draft[r] (draft nullable; each in [-1, V), -1 = none: an id
+ * outside that range is read as none); probs [R, V] fp32 the
  * distribution; draw[r] = the first id (ascending) whose inclusive prefix of w exceeds floor(u[r] * W'')
  * where w has the drafted token removed (the speculative-sampling residual) -- the first id of maximal w
- * when nothing is left; a sampled draw needs u (fp64 in [0, 1)).  temp <= 0 is greedy: draw is the first
- * id of maximal x (u unused) and p_draft is 1 for that id, else 0.  Logits must be finite.  Sums are
- * integer, so results do not depend on the launch. */
+ * when nothing is left, and id 0 when every weight is 0 (a row with a NaN or infinite logit); a sampled
+ * draw needs u (fp64 in [0, 1); a u below 0 draws as 0 and one at or above 1 as just below 1).  temp <= 0
+ * is greedy: draw is the first id of maximal x (u unused) and p_draft is 1 for that id, else 0.  Logits
+ * should be finite.  Sums are integer, so results do not depend on the launch. */
 int flyai_sample_rows(const uint16_t* logits, int32_t R, int32_t V, float temp, int32_t top_k, float top_p,
                       const int32_t* draft, const double* u, float* p_draft, int32_t* draw, float* probs,
                       flyai_stream_t stream);

@@ -161,3 +161,31 @@ def test_tail_tokens_over_the_lm_head():
     assert tail_tokens(parts, h, sm()) == [S.draw(w, next(u)) for w in ws]
     draft = [int(np.argmax(ws[0])), int(np.argmax(ws[1])), 5, 6]
     assert tail_tokens(parts, h, sm(), draft=draft) == S.accept(list(logits), draft, temp, top_k, top_p, uni())
+
+
+@pytest.mark.parametrize("bad", [float("nan"), float("inf"), float("-inf")])
+def test_sample_rows_non_finite_logits_and_out_of_range_uniforms(bad):
+    """A row with a NaN or infinite logit: the kernel's weights and draw equal the oracle's (every weight
+    0 for NaN/+inf, so the draw is id 0, inside the vocabulary); uniforms outside [0, 1) are held to its
+    ends, so they draw what 0 and the largest double below 1 draw."""
+    from flyai_amd import ops
+    V = 3001
+    x = _logits(4, V, seed=5)
+    x[0, 17] = bad
+    x[1, 0] = bad
+    x[1, V - 1] = bad
+    xf = x.float().numpy()
+    u = np.array([0.3, 0.6, -0.25, 1.5])
+    u_eff = np.array([0.3, 0.6, 0.0, np.nextafter(1.0, 0.0)])
+    out = ops.sample_rows(x.to(DEV), 0.9, 0, 1.0, draft=torch.tensor([17, -1, 5, 9], dtype=torch.int32, device=DEV),
+                          u=torch.tensor(u, dtype=torch.float64, device=DEV), want_draw=True, want_probs=True)
+    draw = out["draw"].cpu().numpy()
+    probs = out["probs"].cpu().numpy()
+    for r, d in enumerate([17, -1, 5, 9]):
+        w = S.weights(xf[r], 0.9)
+        want = S.draw(w, float(u_eff[r]), exclude=d)
+        assert 0 <= draw[r] < V and draw[r] == want, (r, draw[r], want)
+        if w.sum(dtype=np.uint64) > 0:
+            assert np.array_equal(probs[r], S.probs(w)), r
+        else:
+            assert not probs[r].any(), r

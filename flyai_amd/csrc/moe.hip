@@ -267,11 +267,12 @@ constexpr int kDepthDown = 8;
 //  * the activation rows (shared by all 8 waves) and the weight scales go global -> LDS directly
 //    (global_load_lds) through 4 stages of 28 KiB; a group's loads are issued 3 groups ahead;
 //  * activations sit in LDS row-major, a row tile (16 rows x 128 K) in 4 KiB, each row's sixteen
-//    16-byte chunks XOR-swizzled by the row: chunk c of row r at position c ^ r.  Each direct-to-LDS
-//    load fills 4 whole rows (16 consecutive lanes read one row's 256 contiguous bytes); a
-//    fragment-order load (16 rows x 16 B per lane group) streams from L2 at a third of the rate.
-//    Lane (g, r) = (lane / 16, lane % 16) feeds step j of row tile m with row 16m + r, K = 32g + 8j
-//    of the group, read from position (4g + j) ^ r: 16 lanes cover the 64 banks once;
+//    16-byte chunks XOR-swizzled by the row: chunk c of row r at position c ^ act_swz(r).  Each
+//    direct-to-LDS load fills 4 whole rows (16 consecutive lanes read one row's 256 contiguous
+//    bytes); a fragment-order load (16 rows x 16 B per lane group) streams from L2 at a third of
+//    the rate.  Lane (g, r) = (lane / 16, lane % 16) feeds step j of row tile m with row 16m + r,
+//    K = 32g + 8j of the group, read from position (4g + j) ^ act_swz(r), which is conflict-free
+//    under the rule act_swz states;
 //  * the stages are separate LDS arrays with compile-time stage numbers, so the compiler can tell
 //    a stage's reads from the asynchronous writes into the other stages; each stage is waited for
 //    with an explicit vmcnt that leaves the 2 younger groups' loads in flight (vector-memory loads
@@ -301,6 +302,20 @@ constexpr int kSchedValu = 0x2, kSchedMfma = 0x8, kSchedVmem = 0x10, kSchedDsRea
 // value of lane ^ 1 (DPP quad permutation [1, 0, 3, 2]; no LDS traffic)
 __device__ __forceinline__ float lane_xor1(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+
+// Position key of activation row r (0..15) in the dense GEMM's LDS row tiles: the chunk c of row r sits
+// at 16-byte slot c ^ act_swz(r).  gfx950's LDS has 64 banks of 4 bytes, and a ds_read_b128 serves
+// the 64 lanes in four cycles of 16, each a half-wave's lane quads of one parity (quads 0, 3, 5, 6 of
+// the half together, then quads 1, 2, 4, 7); it is conflict-free when the 16 lanes of each cycle read
+// 16 different slots of a 256-byte row (measured with single-lane pairs and the conflict counter).
+// Lane (g, r) reads slot (4g + j) ^ act_swz(r).  A cycle holds lanes of g = 2h with r in one class
+// of (r2 ^ r3) and lanes of g = 2h + 1 with r in the other (r2, r3 the bits of r), and their chunks
+// differ in bit 2.  act_swz maps each class onto a set closed under ^4 ({0..7} and {8..15}), so
+// the two halves of a cycle land on complementary slot sets.  (Keying by r itself put lanes 0-3
+// and 20-23 on the same slots: a 2-way conflict on every read.)
+__device__ __forceinline__ int act_swz(int r) {
+  return (r & 3) | ((r >> 1) & 4) | ((((r >> 2) ^ (r >> 3)) & 1) << 3);
 }
 
 // Work units of the dense GEMMs: every group of at least min_rows rows is cut into passes of
@@ -422,7 +437,7 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
 
   // activation DMA: instruction J fills block b = J*8 + wave, rows 4 (b % 4) .. +3 of row tile b / 4:
   // lane L writes position L % 16 of row rt = 4 (b % 4) + L / 16 and so fetches 16-byte chunk
-  // (L % 16) ^ rt of that row's 256 bytes (16 consecutive lanes read one row; an odd MT loads one
+  // (L % 16) ^ act_swz(rt) of that row's 256 bytes (16 consecutive lanes read one row; an odd MT loads one
   // more row tile, of clamped rows, that no MFMA reads)
   const uint16_t* arow[MD];
   int ablk[MD];  // the 32-K block of the group the lane's chunk lies in
@@ -432,12 +447,12 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
     const int rt = 4 * (b & 3) + (lane >> 4);
     const int row = (b >> 2) * 16 + rt;
     const int p = c.row_lo + m0 + (row < rows ? row : 0);
-    const int chunk = (lane & 15) ^ rt;
+    const int chunk = (lane & 15) ^ act_swz(rt);
     arow[J] = c.act + (size_t)(GATE_UP ? c.perm[p] / c.k_top : p) * c.K + chunk * 8;
     ablk[J] = chunk >> 2;
   }
-  // step j's fragment of lane (g, r): row r, K 32g + 8j = chunk 4g + j at position (4g + j) ^ r
-  const int afrag = r * 256 + (((4 * g) ^ r) << 4);
+  // step j's fragment of lane (g, r): row r, K 32g + 8j = chunk 4g + j at position (4g + j) ^ act_swz(r)
+  const int afrag = r * 256 + (((4 * g) ^ act_swz(r)) << 4);
   // the next group to load: block i_nb of the chunk (past the end: the last block), group i_kg
   int i_nb = 0, i_kg = 0;
   // the loads of that group: weights into the ring slot, then scales and activations into the

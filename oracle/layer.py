@@ -112,21 +112,27 @@ class LayerParams:
         self.sliding = sliding
 
 
-def moe_block(x_norm, p: LayerParams, k=4, trace=None):
-    """Router -> permute -> experts -> combine (no residual); x_norm is the RMSNorm output."""
+def moe_block(x_norm, p: LayerParams, k=4, trace=None, force_ids=None):
+    """Router -> permute -> experts -> combine (no residual); x_norm is the RMSNorm output.
+    force_ids (int [T, k], optional): teacher forcing for parity tests -- rows whose own selection
+    differs from it are routed to its experts (routing.forced_route); the trace keeps the block's own
+    ids under "ids" and the replaced rows under "forced_rows"."""
     ids, wts, logits = routing.gptoss_route(x_norm, p.router_w, p.router_b, k)
+    own_ids, forced_rows = ids, np.zeros(0, dtype=np.int64)
+    if force_ids is not None:
+        ids, wts, forced_rows = routing.forced_route(logits, ids, wts, force_ids)
     hist, offsets, perm, inv = routing.permute(ids, p.router_w.shape[0])
     y = experts.experts_mxfp4(x_norm, perm, offsets, k, p.moe)
     out = routing.combine(y, inv, wts)
     if trace is not None:
-        trace.update(ids=ids, weights=wts, logits=logits, hist=hist, offsets=offsets, perm=perm,
-                     inv=inv, y_perm=y, moe_out=out)
+        trace.update(ids=own_ids, used_ids=ids, forced_rows=forced_rows, weights=wts, logits=logits, hist=hist,
+                     offsets=offsets, perm=perm, inv=inv, y_perm=y, moe_out=out)
     return out
 
 
-def decoder_layer(h, p: LayerParams, kv, q_lens, starts, cos_tab, sin_tab, trace=None, tree=None):
+def decoder_layer(h, p: LayerParams, kv, q_lens, starts, cos_tab, sin_tab, trace=None, tree=None, force_ids=None):
     """h bf16-valued fp32 [T, H]; kv = (k_seqs, v_seqs), per-sequence fp32 [Hkv, cap, D] tensors
-    that are written in place.  Returns the new hidden state.
+    that are written in place.  Returns the new hidden state.  force_ids: moe_block's teacher forcing.
 
     tree = (par, dep) makes this the tree-verify step of one sequence (``FastVerify.tree_decode``,
     ``phase0/fastverify.py:233-299``): q_lens == [M], node i is rotated at position
@@ -163,7 +169,7 @@ def decoder_layer(h, p: LayerParams, kv, q_lens, starts, cos_tab, sin_tab, trace
     ao = linear(o.reshape(T, nq), p.wo, p.bo)
     h = bf16(h + ao)
     xn2 = rmsnorm(h, p.ln2)
-    mo = moe_block(xn2, p, trace=trace)
+    mo = moe_block(xn2, p, trace=trace, force_ids=force_ids)
     h_out = bf16(h + mo)
     if trace is not None:
         trace.update(xn=xn, qkv=qkv, q_rope=qr, k_rope=kr, attn=o, h_mid=h, xn2=xn2, h_out=h_out)

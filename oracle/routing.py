@@ -73,19 +73,43 @@ def _topk_desc(vals, k):
     return np.argsort(-vals, axis=1, kind="stable")[:, :k]
 
 
-def gptoss_route(x, w, b, k=4):
-    """x bf16-valued [T, H], router weight [E, H] and bias [E] (bf16 values).
-    Returns (ids int32 [T,k] ascending per row, weights fp32 [T,k], logits fp32 [T,E] bf16-valued)."""
-    logits = bf16(dot_fixed(x, w) + torch.as_tensor(b).float()[None, :])
-    lg = logits.numpy()
-    sel = _topk_desc(lg, k)
+def _selection_weights(lg, sel):
+    """(ids ascending, fp32 softmax weights in the same order) of a selection sel [T, k] whose rows
+    are in (logit desc, id asc) order: the softmax over the k selected logits
+    (``transformers/integrations/mxfp4.py:435-447``: top-k, then softmax over the k values)."""
     v = np.take_along_axis(lg, sel, axis=1).astype(np.float32)
     e = np.exp(v - v.max(axis=1, keepdims=True)).astype(np.float32)
     wts = (e / e.sum(axis=1, keepdims=True)).astype(np.float32)
     order = np.argsort(sel, axis=1, kind="stable")
     ids = np.take_along_axis(sel, order, axis=1).astype(np.int32)
-    wts = np.take_along_axis(wts, order, axis=1)
+    return ids, np.take_along_axis(wts, order, axis=1)
+
+
+def gptoss_route(x, w, b, k=4):
+    """x bf16-valued [T, H], router weight [E, H] and bias [E] (bf16 values).
+    Returns (ids int32 [T,k] ascending per row, weights fp32 [T,k], logits fp32 [T,E] bf16-valued)."""
+    logits = bf16(dot_fixed(x, w) + torch.as_tensor(b).float()[None, :])
+    lg = logits.numpy()
+    ids, wts = _selection_weights(lg, _topk_desc(lg, k))
     return ids, wts, logits
+
+
+def forced_route(logits, ids, wts, force):
+    """Teacher forcing, for parity tests: the rows where the expert set ``force`` (int [T, k], e.g. the
+    ids a GPU router chose on a near-tie) differs from ``ids`` take force's experts, weighted by the
+    same softmax over their logits that gptoss_route applies to its own selection.  Returns
+    (ids, weights, the replaced row indices)."""
+    lg = np.asarray(logits, dtype=np.float32)
+    force = np.sort(np.asarray(force, dtype=np.int64), axis=1)
+    rows = np.nonzero((force != np.asarray(ids)).any(axis=1))[0]
+    ids, wts = np.array(ids, copy=True), np.array(wts, copy=True)
+    if len(rows):
+        sub = lg[rows]
+        sel = force[rows]
+        vals = np.take_along_axis(sub, sel, axis=1)
+        sel = np.take_along_axis(sel, np.lexsort((sel, -vals), axis=1), axis=1)  # (logit desc, id asc)
+        ids[rows], wts[rows] = _selection_weights(sub, sel)
+    return ids, wts, rows
 
 
 # --- deterministic sigmoid for bit-exact grouped selection -------------------------------------

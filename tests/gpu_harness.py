@@ -110,8 +110,10 @@ class _SingleLayerKV:
 
 
 def tokens_with_same_routing(ids, ref_ids, ref_logits, k):
-    """Tokens whose GPU router ids equal the oracle's.  A differing token must sit on a near-tie of
-    the oracle's logits (k-th and (k+1)-th within 2 bf16 ulps), and at most 2 may differ."""
+    """Tokens whose GPU router ids equal the oracle's own.  A differing token must sit on a near-tie of
+    the oracle's logits (k-th and (k+1)-th within 2 bf16 ulps), and at most 2 may differ.  The layer
+    tests then teacher-force the oracle's MoE with the GPU's ids (decoder_layer's force_ids) and hold
+    every row to the bar."""
     ref_ids = np.asarray(ref_ids)
     bad = np.nonzero((ids != ref_ids).any(1))[0]
     assert len(bad) <= 2, f"{len(bad)} tokens routed differently"

@@ -95,12 +95,15 @@ def test_c1_workload_layers_vs_oracle_and_batch_invariance():
         _routing_invariants(ids, perm, inv, off, E, k)
         assert T * k < 8 * E, "C1 is the decode tail: every group takes the row-pass kernel"
         tr = {}
-        ref = olayer.decoder_layer(hin, oracle_layer_params(lw, lw.sliding), okv, q_lens, starts, cos, sin, trace=tr)
-        good = tokens_with_same_routing(ids, tr["ids"], tr["logits"], k)
+        # teacher-forced: a token the oracle routes differently (only on a near-tie, checked below)
+        # takes the GPU's experts in the oracle too, so every row meets the bar
+        ref = olayer.decoder_layer(hin, oracle_layer_params(lw, lw.sliding), okv, q_lens, starts, cos, sin, trace=tr,
+                                   force_ids=ids)
+        tokens_with_same_routing(ids, tr["ids"], tr["logits"], k)
         out = cpu_f32(h).numpy()
-        mar, c = metrics(out[good], ref.numpy()[good])
+        mar, c = metrics(out, ref.numpy())
         assert mar <= MAR and c >= COS, f"C1 layer {l}: max-abs-rel {mar:.3g} cos {c:.6f}"
-        _, c = metrics((out - hin.numpy())[good], (ref.numpy() - hin.numpy())[good])
+        _, c = metrics(out - hin.numpy(), ref.numpy() - hin.numpy())
         assert c >= COS, f"C1 layer {l}: increment cos {c:.6f}"
         attn = cpu_f32(st.debug_buffer(3, torch.bfloat16, (T, shape.n_q_heads * shape.head_dim))).numpy()
         mar, c = metrics(attn, tr["attn"].reshape(T, -1).numpy())
@@ -166,13 +169,13 @@ def test_c2_workload_layers_vs_oracle(dense_fp8):
         tr = {}
         hin_sub = cpu_f32(hin)[rows]
         ref = olayer.decoder_layer(hin_sub, oracle_layer_params(lw, lw.sliding), (ks, vs), sub_q, sub_starts,
-                                   cos, sin, trace=tr)
+                                   cos, sin, trace=tr, force_ids=ids[rows])
         out = cpu_f32(h).numpy()[rows]
-        good = tokens_with_same_routing(ids[rows], tr["ids"], tr["logits"], k)
-        mar, c = metrics(out[good], ref.numpy()[good])
+        tokens_with_same_routing(ids[rows], tr["ids"], tr["logits"], k)
+        mar, c = metrics(out, ref.numpy())
         print(f"C2 {'fp8' if dense_fp8 else 'bf16'} dense, layer {l}: max-abs-rel {mar:.4g} cos {c:.6f}")
         assert mar <= MAR and c >= COS, f"C2 layer {l}: max-abs-rel {mar:.3g} cos {c:.6f}"
-        _, c = metrics((out - hin_sub.numpy())[good], (ref.numpy() - hin_sub.numpy())[good])
+        _, c = metrics(out - hin_sub.numpy(), ref.numpy() - hin_sub.numpy())
         assert c >= COS, f"C2 layer {l}: increment cos {c:.6f}"
         attn = cpu_f32(st.debug_buffer(3, torch.bfloat16, (T, shape.n_q_heads * shape.head_dim))).numpy()[rows]
         mar, c = metrics(attn, tr["attn"].reshape(len(rows), -1).numpy())

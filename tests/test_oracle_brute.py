@@ -568,3 +568,44 @@ def test_experts_fp8act_gate_up_exact_on_grid_inputs_and_down_recomputed():
         hq = experts.mx_fp8_roundtrip(h16[lo:hi].numpy()).astype(np.float64)
         want = hq @ w2.T + w.b2[e][None, :].astype(np.float64)
         np.testing.assert_allclose(y8[lo:hi].numpy(), want, rtol=1e-5, atol=1e-4)
+
+
+def test_forced_route_pinned():
+    """routing.forced_route (teacher forcing for the GPU parity tests): forcing the router's own
+    selection changes nothing, bit for bit (ties included); forcing another expert set gives exactly
+    the sorted set and the fp64 softmax over its logits, and leaves every other row's bits alone.
+    Weights taken over the router's own experts (the mistake forcing exists to avoid) must fail."""
+    import torch
+    from oracle import routing
+    g = torch.Generator().manual_seed(21)
+    T, E, H, k = 40, 32, 256, 4
+    x = torch.randn(T, H, generator=g).bfloat16().float()
+    w = (0.05 * torch.randn(E, H, generator=g)).bfloat16().float()
+    b = torch.zeros(E).bfloat16().float()
+    ids, wts, logits = routing.gptoss_route(x, w, b, k)
+    lg = logits.numpy()
+    lg[3, :] = lg[3, 0]                                   # a row of exact ties: lower ids first
+    ids3, wts3 = routing._selection_weights(lg, routing._topk_desc(lg, k))
+    i2, w2, rows = routing.forced_route(lg, ids3, wts3, ids3)
+    assert len(rows) == 0 and np.array_equal(i2, ids3) and np.array_equal(w2.view(np.uint32), wts3.view(np.uint32))
+    rng = np.random.default_rng(5)
+    force = ids3.copy()
+    picked = [1, 3, 17, 39]
+    for t in picked:
+        force[t] = rng.choice(E, size=k, replace=False)   # any order; forced_route sorts
+    i2, w2, rows = routing.forced_route(lg, ids3, wts3, force)
+    changed = [t for t in picked if set(force[t]) != set(ids3[t])]
+    assert sorted(rows.tolist()) == sorted(changed)
+    keep = np.setdiff1d(np.arange(T), rows)
+    assert np.array_equal(i2[keep], ids3[keep]) and np.array_equal(w2[keep].view(np.uint32), wts3[keep].view(np.uint32))
+    caught = 0
+    for t in rows:
+        s = np.sort(force[t])
+        assert np.array_equal(i2[t], s)
+        v = lg[t, s].astype(np.float64)
+        ref = np.exp(v - v.max()) / np.exp(v - v.max()).sum()
+        assert np.allclose(w2[t], ref, rtol=2e-6, atol=0), (t, w2[t], ref)
+        own = lg[t, ids3[t]].astype(np.float64)
+        wrong = np.exp(own - own.max()) / np.exp(own - own.max()).sum()
+        caught += not np.allclose(wrong, ref, rtol=2e-6, atol=0)
+    assert caught >= len(rows) - 1, "weights over the router's own experts must fail (all but the all-tie row)"

@@ -70,7 +70,7 @@ def _run_small_stage(f, params, steps, teacher=True):
     saved = (layer.N_Q_HEADS, layer.N_KV_HEADS, layer.HEAD_DIM, layer.WINDOW)
     layer.N_Q_HEADS, layer.N_KV_HEADS, layer.HEAD_DIM, layer.WINDOW = NQ, NKV, D, W
     orig_moe = layer.moe_block
-    layer.moe_block = lambda x, p, k=K, trace=None: orig_moe(x, p, k=K, trace=trace)
+    layer.moe_block = lambda x, p, k=K, trace=None, force_ids=None: orig_moe(x, p, k=K, trace=trace, force_ids=force_ids)
     try:
         cos, sin = layer.rope_table(64)
         kv = [([torch.zeros(NKV, 16, D)], [torch.zeros(NKV, 16, D)]) for _ in params]

@@ -16,7 +16,8 @@ resident in HBM.  Beside it:
   research/v4_fp8_gemv_bench.py:11-17);
 * hbm_read_ceiling -- what a kernel that only streams reads reaches on this GPU;
 * cpu_baseline -- the CPU oracle on one sliding and one full layer of the same batch (warmup, then
-  the median of 3), scaled to the 9-layer stage.
+  the median of 3), scaled to the 9-layer stage; for c2 and c4 on a stated subset of the rows (the
+  chunk's last rows and decode rows), since one oracle layer of a whole prefill chunk takes minutes.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
@@ -292,8 +293,9 @@ def run_gptoss(args, workload="c1"):
     shape = GptOssShape()
     chunked_prefill = workload in ("c2", "c4")   # prefill-sized expert groups: the MFMA roofline
     caps = None
+    prefill_seqs = []
     if workload == "c4":
-        q_lens, starts, _ = c4_batch()
+        q_lens, starts, prefill_seqs = c4_batch()
         caps = [s_ + q_ for s_, q_ in zip(starts, q_lens)]   # a per-sequence workspace, sized to each context
         maxlen = C4_MAXLEN + 64
     else:
@@ -301,7 +303,7 @@ def run_gptoss(args, workload="c1"):
         maxlen = 8192 + 64
     S, T = len(q_lens), sum(q_lens)
     E, k = shape.n_experts, shape.top_k
-    with_cpu = not args.no_cpu and not chunked_prefill
+    with_cpu = not args.no_cpu
     print(f"[bench] building {args.layers}-layer stage ...", file=sys.stderr, flush=True)
     layers = [synthetic_layer(shape, 1000 + i, dev, sliding=(i % 2 == 0), keep_hf=(i < 2 and with_cpu))
               for i in range(args.layers)]
@@ -316,8 +318,14 @@ def run_gptoss(args, workload="c1"):
         t.copy_(torch.randn(t.shape, device=dev, generator=g).to(torch.bfloat16))
     hidden0 = torch.randn(T, shape.hidden, device=dev, generator=g).to(torch.bfloat16)
     cpu_inputs = None
+    cpu_rows = cpu_sub = None
     if with_cpu:   # the oracle's copies of layers 0-1 and their KV, taken before any step writes
-        cpu_inputs = cpu_layer_inputs(layers[:2], kv, hidden0, S)
+        if chunked_prefill:   # a stated subset of the rows (the whole chunk takes minutes per layer)
+            cpu_rows, cpu_sub = cpu_row_subset(workload, q_lens, starts, prefill_seqs)
+            cpu_inputs = cpu_layer_inputs(layers[:2], kv, hidden0[torch.as_tensor(cpu_rows, device=dev)],
+                                          cpu_sub["slots"])
+        else:
+            cpu_inputs = cpu_layer_inputs(layers[:2], kv, hidden0, list(range(S)))
     fp8 = chunked_prefill and args.dense == "fp8"
     stage = RaggedStage(shape, layers, rot, kv, max_tokens=max(64, T), max_seqs=S, use_graphs=args.graphs,
                         dense_fp8=fp8, split_keys=args.split_keys)
@@ -433,7 +441,8 @@ def run_gptoss(args, workload="c1"):
             "kernels": {"moe_down": {"avg_us": round(dn_us, 2), "GB/s": round(dn_gbs, 1),
                                      "TFLOP/s": round(flops / 2 / (dn_us * 1e-6) / 1e12, 1)}},
             "hbm_read_ceiling": ceiling,
-            "cpu_baseline": None,
+            "cpu_baseline": (cpu_baseline(cpu_inputs, cpu_sub["q_lens"], cpu_sub["starts"], maxlen, args.layers,
+                                          subset=cpu_sub["what"]) if with_cpu else None),
         }
         print(json.dumps(line))
         return
@@ -462,8 +471,29 @@ def run_gptoss(args, workload="c1"):
     print(json.dumps(line))
 
 
-def cpu_layer_inputs(layers, kv, hidden0, S):
-    """Host copies of the given layers (oracle parameters) and of their KV, per slot."""
+def cpu_row_subset(workload, q_lens, starts, prefill_seqs):
+    """The rows the CPU baseline runs for a chunked-prefill batch: the chunk's last 4 rows and every
+    decode row (c2); the last 4 rows of both prefill chunks and the last row of 60 other sequences
+    (c4).  Each picked run is a sub-sequence at its own positions, over its sequence's slab."""
+    cu = np.concatenate([[0], np.cumsum(q_lens)])
+    if workload == "c2":
+        picks = [(0, 4)] + [(b, 1) for b in range(1, len(q_lens))]
+        what = "the 2048-token chunk's last 4 rows and the 48 decode rows"
+    else:
+        others = [b for b in range(len(q_lens)) if b not in set(prefill_seqs)]
+        picks = [(b, 4) for b in prefill_seqs] + [(b, 1) for b in others[::4][:60]]
+        what = "the last 4 rows of both 1024-token prefill chunks and the last row of 60 other sequences"
+    rows, sub_q, sub_starts = [], [], []
+    for b, n in picks:
+        rows.extend(range(int(cu[b + 1]) - n, int(cu[b + 1])))
+        sub_q.append(n)
+        sub_starts.append(starts[b] + q_lens[b] - n)
+    return rows, {"q_lens": sub_q, "starts": sub_starts, "slots": [b for b, _ in picks],
+                  "what": f"{len(rows)} rows: {what}"}
+
+
+def cpu_layer_inputs(layers, kv, hidden0, slots):
+    """Host copies of the given layers (oracle parameters) and of their KV for the given slots."""
     import torch
     from oracle import experts as oexperts
     from oracle import layer as olayer
@@ -475,17 +505,18 @@ def cpu_layer_inputs(layers, kv, hidden0, S):
                                        lw.w2_scales.cpu().numpy(), lw.b2.cpu().numpy())
         p = olayer.LayerParams(f(lw.ln1), f(lw.ln2), f(lw.wqkv), f(lw.bqkv), f(lw.wo), f(lw.bo), f(lw.sinks),
                                f(lw.router_w), f(lw.router_b), moe, lw.sliding)
-        ks = [f(kv.k_dense(i, s)) for s in range(S)]
-        vs = [f(kv.v_dense(i, s)) for s in range(S)]
+        ks = [f(kv.k_dense(i, s)) for s in slots]
+        vs = [f(kv.v_dense(i, s)) for s in slots]
         out.append((p, ks, vs))
     torch.cuda.synchronize()
     return {"layers": out, "h": f(hidden0)}
 
 
-def cpu_baseline(inp, q_lens, starts, maxlen, n_layers):
+def cpu_baseline(inp, q_lens, starts, maxlen, n_layers, subset=None):
     """The CPU oracle on one sliding (layer 0) and one full-attention layer (layer 1) of the same
     batch, each a warmup then the median of 3 runs; the stage estimate is the 9-layer mix (5 sliding,
-    4 full) of those medians."""
+    4 full) of those medians.  subset: the rows are a stated subset of the batch (tokens/s is then the
+    subset's rows over its stage time)."""
     import torch
     from oracle import layer as olayer
     threads = cpu_threads()
@@ -504,7 +535,8 @@ def cpu_baseline(inp, q_lens, starts, maxlen, n_layers):
     return {"value": round(T / stage_s, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
             "cpu": cpu_model(), "host_cpus": os.cpu_count(),
             "sample": f"CPU oracle (torch fp32 + numpy) on layer 0 (sliding, median {med[0]:.2f} s) and "
-                      f"layer 1 (full attention, median {med[1]:.2f} s) of the same {T}-token batch, warmup + "
+                      f"layer 1 (full attention, median {med[1]:.2f} s) of "
+                      f"{'a subset of the batch, ' + subset if subset else f'the same {T}-token batch'}, warmup + "
                       f"median of 3 each; stage = {n_sliding} x sliding + {n_layers - n_sliding} x full = "
                       f"{stage_s:.2f} s"}
 

@@ -18,6 +18,7 @@
 // per query row; a merge kernel folds the splits and the sink.
 #include <limits.h>
 #include <math.h>
+#include <type_traits>
 #include <vector>
 
 #include "common.h"
@@ -241,6 +242,91 @@ __device__ __forceinline__ void rows_block(QRows<QT>& R, const uint4 (&kc)[4][2]
   }
 }
 
+// The chunked-prefill rows' block step: rows_block's math for the two row tiles of a prefill wave,
+// with the block's K and V fragments read from its LDS copy as they are used -- the scores of both
+// row tiles per K tile, then the softmax, then O per V tile -- so K and V are never live at once
+// (about 40 fewer registers than rows_block over fragments loaded beforehand).  MASKED = false is an
+// interior block, unmasked for every row of the wave, the rows past the wave's tokens included (their
+// scores come from zero queries, they never move another row's max and are never written); it has no
+// masking code at all, so the block loop over interior blocks stays free of it.
+template <bool MASKED>
+__device__ __forceinline__ void prefill_rows_block(QRows<2>& R, const uint4* __restrict__ kbuf,
+                                                   const uint4* __restrict__ vbuf, int kb, int key_lo,
+                                                   int key_hi, int window) {
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4;
+  const float scale = 0.125f * kLog2e;
+  const bf16x8_t ones = as_bf16x8(make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
+  f32x4_t s[2][4];
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    const uint4 k0 = kbuf[kt * 128 + lane], k1 = kbuf[kt * 128 + 64 + lane];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      s[qt][kt] = mfma16x16x32(as_bf16x8(k0), R.qf[qt][0], f32x4_t{0.f, 0.f, 0.f, 0.f});
+      s[qt][kt] = mfma16x16x32(as_bf16x8(k1), R.qf[qt][1], s[qt][kt]);
+    }
+  }
+  bf16x8_t pt[2][2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    // lane holds S^T[key kb + tile_key(kt, 4g + v)][qrow n]
+    float bmax = -INFINITY;
+    if constexpr (!MASKED) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) bmax = fmaxf(bmax, s[qt][kt][v]);
+    } else {
+      const int p = R.qpos[qt];
+      const int lo = max(key_lo, window > 0 ? p - window + 1 : 0);
+      const int hi = min(p, key_hi - 1);
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int key = kb + tile_key(kt, 4 * g + v);
+          const bool ok = R.qval[qt] && key >= lo && key <= hi;
+          s[qt][kt][v] = ok ? s[qt][kt][v] : -INFINITY;
+          bmax = fmaxf(bmax, s[qt][kt][v]);
+        }
+    }
+    bmax = max_lane_groups(bmax);
+    const float m_blk = bmax * scale;
+    const bool move = m_blk > R.m_run[qt] + kMaxSlack;
+    if (__ballot(move)) {
+      const float m_new = move ? m_blk : R.m_run[qt];
+      const float alpha = __builtin_amdgcn_exp2f(R.m_run[qt] - m_new);
+      R.m_run[qt] = m_new;
+      R.L[qt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) R.O[qt][dt] *= alpha;
+    }
+    const float neg_m = -R.m_run[qt];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        pt[qt][kt >> 1][(kt & 1) * 4 + v] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qt][kt][v], scale, neg_m));
+    R.L[qt] = mfma16x16x32(ones, pt[qt][0], R.L[qt]);
+    R.L[qt] = mfma16x16x32(ones, pt[qt][1], R.L[qt]);
+  }
+  const bool tail = MASKED && kb + 64 > key_hi;  // values of keys at or past key_hi are zeroed (maybe unwritten)
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    uint4 v0 = vbuf[dt * 64 + lane], v1 = vbuf[256 + dt * 64 + lane];
+    if (tail) {
+      v0 = mask_keys(v0, kb + 8 * g, INT_MIN, key_hi);
+      v1 = mask_keys(v1, kb + 32 + 8 * g, INT_MIN, key_hi);
+    }
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) {
+      R.O[qt][dt] = mfma16x16x32(as_bf16x8(v0), pt[qt][0], R.O[qt][dt]);
+      R.O[qt][dt] = mfma16x16x32(as_bf16x8(v1), pt[qt][1], R.O[qt][dt]);
+    }
+  }
+}
+
 // One work item (<= 4 tokens x the 8 heads of a kv head, one key split) by one wave, K and V
 // streamed from the slab; writes a partial record (m, l, O[64]) per query row.
 // TREE: the batch is one tree-verify sequence; token (= node) i sits at position
@@ -434,27 +520,25 @@ __device__ __forceinline__ void attn_prefill_body(
   store_block(0);
   lds_barrier();
   int buf = 0;
-  for (int kb = kb_first; kb < it.key_hi; kb += 64) {
+  // One block: the next one's loads go out, this wave's rows take the block (if any of their keys is
+  // in it), the next one is stored, one barrier.  Every wave steps through the same blocks, so the
+  // workgroup's barriers match; each wave's blocks split into a masked run before its interior blocks
+  // (window start), the interior run, and a masked run after (causal diagonal, the item's end), each
+  // its own loop, so the interior loop carries no masking code.
+  auto step = [&](int kb, auto masked) __attribute__((always_inline)) {
     const bool more = kb + 64 < it.key_hi;
     if (more) load_block(kb + 64);
-    if (ntw > 0 && kb <= pos_last && kb + 63 >= lo_w) {
-      uint4 kc[4][2], vv[4][2];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        kc[t][0] = kvs[buf][0][t * 128 + lane];
-        kc[t][1] = kvs[buf][0][t * 128 + 64 + lane];
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) vv[dt][h] = kvs[buf][1][h * 256 + dt * 64 + lane];
-      const bool interior = kb >= int_lo && kb + 63 <= int_hi;
-      rows_block<2, false>(R, kc, vv, kb, interior, it.key_lo, it.key_hi, window, nullptr, nullptr);
-    }
+    if (ntw > 0 && kb <= pos_last && kb + 63 >= lo_w)
+      prefill_rows_block<decltype(masked)::value>(R, kvs[buf][0], kvs[buf][1], kb, it.key_lo, it.key_hi, window);
     if (more) store_block(buf ^ 1);  // every wave finished reading that buffer before the last barrier
     lds_barrier();
     buf ^= 1;
-  }
+  };
+  auto interior = [&](int kb) { return kb >= int_lo && kb + 63 <= int_hi; };
+  int kb = kb_first;
+  for (; kb < it.key_hi && kb < int_lo; kb += 64) step(kb, std::true_type{});
+  for (; kb < it.key_hi && interior(kb); kb += 64) step(kb, std::false_type{});
+  for (; kb < it.key_hi; kb += 64) step(kb, std::true_type{});
   // out = O 2^(m-M) / (l 2^(m-M) + 2^(sink-M)), M = max(m, sink), all in base-2 units: the merge of a
   // single split
 #pragma unroll

@@ -332,7 +332,11 @@ __device__ __forceinline__ void prefill_rows_block(QRows<2>& R, const uint4* __r
 // TREE: the batch is one tree-verify sequence; token (= node) i sits at position
 // tree->start + depth[i] (dep_s: the depths, staged in LDS) and sees the committed keys below
 // tree->start plus the tree slots of its ancestor set (FastVerify._tset masks).
-template <int QT, bool TREE>
+// LEAN: only K is loaded a block ahead; a block's V is loaded at the block's start and is first
+// read by its PV products, after the scores and the softmax.  Three K/V tiles live instead of four
+// (32 fewer registers): the step kernel that fits three waves per SIMD, where the other waves of the
+// SIMD hide what the shorter V lead leaves exposed.
+template <int QT, bool TREE, bool LEAN = false>
 __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_idx,
                                           const uint16_t* __restrict__ q,
                                           const uint16_t* __restrict__ k_pool,
@@ -373,12 +377,13 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
   // K and V of the next block are loaded while the current block computes
   uint4 kc[4][2], kn[4][2], vv[4][2], vn[4][2];
   load_k_tile(kc, K, kb_first, lane);
-  load_v_tile(vv, Vt, kb_first, lane);
+  if (!LEAN) load_v_tile(vv, Vt, kb_first, lane);
   for (int kb = kb_first; kb < it.key_hi; kb += 64) {
     const bool more = kb + 64 < it.key_hi;
+    if (LEAN) load_v_tile(vv, Vt, kb, lane);
     if (more) {
       load_k_tile(kn, K, kb + 64, lane);
-      load_v_tile(vn, Vt, kb + 64, lane);
+      if (!LEAN) load_v_tile(vn, Vt, kb + 64, lane);
     }
     const bool interior = kb >= int_lo && kb + 63 <= int_hi;
     rows_block<QT, TREE>(R, kc, vv, kb, interior, it.key_lo, it.key_hi, window, tree, dep_s);
@@ -387,8 +392,10 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
       for (int t = 0; t < 4; ++t) {
         kc[t][0] = kn[t][0];
         kc[t][1] = kn[t][1];
-        vv[t][0] = vn[t][0];
-        vv[t][1] = vn[t][1];
+        if (!LEAN) {
+          vv[t][0] = vn[t][0];
+          vv[t][1] = vn[t][1];
+        }
       }
     }
   }
@@ -468,9 +475,13 @@ __global__ __launch_bounds__(64, 2) void attn_partial_kernel(
 // Work item = (sequence, kv head, up to kPrefillTokens consecutive query tokens): a workgroup of
 // kPrefillWaves waves, wave w owning tokens 4w .. 4w+3 of the item (32 query rows, the same math as a
 // decode item).  The item's 64-key blocks are staged once in LDS for all waves -- the tiled slab
-// block is copied as it is, so each wave reads its K and V fragments as contiguous KiBs -- through two
-// buffers with one barrier per block, the next block's loads in flight while the current one
-// computes.  No key splits: each wave ends with the sink and the normalisation and writes its rows.
+// block is copied as it is, global -> LDS directly (global_load_lds, no register staging), so each
+// wave reads its K and V fragments as contiguous KiBs -- through two buffers with one barrier per
+// block, the next block's loads in flight while the current one computes.  Block kb sits in buffer
+// (kb / 64) % 2; the buffers are separate LDS arrays picked at compile time (the block loop is
+// unrolled by parity), so the compiler can tell the reads of one from the DMA writes into the other
+// and a block's reads do not wait for the next block's loads.  No key splits: each wave ends with
+// the sink and the normalisation and writes its rows.
 constexpr int kPrefillWaves = kPrefillTokens / 4;
 
 __device__ __forceinline__ void attn_prefill_body(
@@ -478,7 +489,8 @@ __device__ __forceinline__ void attn_prefill_body(
     const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
     const int32_t* __restrict__ kv_cap, const float* __restrict__ sinks, int window, int Hq,
     const flyai_attn_item* __restrict__ items, uint16_t* __restrict__ out) {
-  __shared__ uint4 kvs[2][2][512];  // [buffer][K, V][one 64-key block: 4096 bf16]
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  __shared__ uint4 kvs0[2][512], kvs1[2][512];  // the two buffers: [K, V][one 64-key block: 4096 bf16]
   const flyai_attn_item it = items[bid];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
@@ -496,49 +508,55 @@ __device__ __forceinline__ void attn_prefill_body(
   const int int_lo = max(it.key_lo, window > 0 ? pos_last - window + 1 : 0);
   const int int_hi = min(it.key_hi - 1, pos_w);
 
-  // staging: thread tid copies uint4 s = tid + 256 j (j < 4) of the block (K: s < 512, V: s >= 512)
+  // staging: load instruction j (j < 4) of wave w copies uint4s s0 .. s0 + 63, s0 = 256 j + 64 w, of
+  // the block (K: s < 512, V: s >= 512), lane L the one at s0 + L (the DMA's lane order)
   constexpr int kPer = 1024 / (64 * kPrefillWaves);
   const int kb_first = it.key_lo & ~63;
-  // (native vector registers: a uint4 array carried across iterations would live in scratch)
-  attn_u32x4 st[kPer];
-  auto load_block = [&](int kb) {
+  auto issue = [&](uint4 (&dst)[2][512], int kb) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      const int sidx = tid + 64 * kPrefillWaves * j;
-      const uint4* src = sidx < 512 ? Kb + (size_t)kb * 8 + sidx : Vb + (size_t)kb * 8 + (sidx - 512);
-      st[j] = *reinterpret_cast<const attn_u32x4*>(src);
+      const int s0 = 64 * kPrefillWaves * j + 64 * wave;  // wave-uniform
+      const uint4* src = (s0 < 512 ? Kb + (size_t)kb * 8 + s0 : Vb + (size_t)kb * 8 + (s0 - 512)) + lane;
+      __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr)(&dst[0][0] + s0), 16, 0, 0);
     }
   };
-  auto store_block = [&](int buf) {
-#pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int sidx = tid + 64 * kPrefillWaves * j;
-      *reinterpret_cast<attn_u32x4*>(&kvs[buf][sidx >> 9][sidx & 511]) = st[j];
-    }
-  };
-  load_block(kb_first);
-  store_block(0);
-  lds_barrier();
-  int buf = 0;
-  // One block: the next one's loads go out, this wave's rows take the block (if any of their keys is
-  // in it), the next one is stored, one barrier.  Every wave steps through the same blocks, so the
-  // workgroup's barriers match; each wave's blocks split into a masked run before its interior blocks
-  // (window start), the interior run, and a masked run after (causal diagonal, the item's end), each
-  // its own loop, so the interior loop carries no masking code.
-  auto step = [&](int kb, auto masked) __attribute__((always_inline)) {
-    const bool more = kb + 64 < it.key_hi;
-    if (more) load_block(kb + 64);
-    if (ntw > 0 && kb <= pos_last && kb + 63 >= lo_w)
-      prefill_rows_block<decltype(masked)::value>(R, kvs[buf][0], kvs[buf][1], kb, it.key_lo, it.key_hi, window);
-    if (more) store_block(buf ^ 1);  // every wave finished reading that buffer before the last barrier
+  // the wave's own loads have landed (vector memory loads complete in issue order; the DMA counts
+  // as a load), then the barrier: every wave's have
+  auto landed = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     lds_barrier();
-    buf ^= 1;
   };
-  auto interior = [&](int kb) { return kb >= int_lo && kb + 63 <= int_hi; };
+  if ((kb_first >> 6) & 1) issue(kvs1, kb_first); else issue(kvs0, kb_first);
+  landed();
+  // One block: the next one's loads go out into the other buffer (every wave finished reading it
+  // before the last barrier), this wave's rows take the block (if any of their keys is in it), the
+  // loads land, one barrier.  Every wave steps through the same blocks, so the workgroup's barriers
+  // match; each wave's blocks split into a masked run before its interior blocks (window start), the
+  // interior run, and a masked run after (causal diagonal, the item's end), each its own loop, so the
+  // interior loop carries no masking code.
+  auto step = [&](int kb, auto masked, auto parity) __attribute__((always_inline)) {
+    uint4 (&cur)[2][512] = decltype(parity)::value ? kvs1 : kvs0;
+    uint4 (&nxt)[2][512] = decltype(parity)::value ? kvs0 : kvs1;
+    if (kb + 64 < it.key_hi) issue(nxt, kb + 64);
+    if (ntw > 0 && kb <= pos_last && kb + 63 >= lo_w)
+      prefill_rows_block<decltype(masked)::value>(R, cur[0], cur[1], kb, it.key_lo, it.key_hi, window);
+    landed();
+  };
   int kb = kb_first;
-  for (; kb < it.key_hi && kb < int_lo; kb += 64) step(kb, std::true_type{});
-  for (; kb < it.key_hi && interior(kb); kb += 64) step(kb, std::false_type{});
-  for (; kb < it.key_hi; kb += 64) step(kb, std::true_type{});
+  auto run = [&](auto more, auto masked) __attribute__((always_inline)) {
+    while (more(kb)) {
+      if (((kb >> 6) & 1) == 0) {
+        step(kb, masked, std::false_type{});
+        kb += 64;
+        if (!more(kb)) break;
+      }
+      step(kb, masked, std::true_type{});
+      kb += 64;
+    }
+  };
+  run([&](int k) { return k < it.key_hi && k < int_lo; }, std::true_type{});
+  run([&](int k) { return k < it.key_hi && k >= int_lo && k + 63 <= int_hi; }, std::false_type{});
+  run([&](int k) { return k < it.key_hi; }, std::true_type{});
   // out = O 2^(m-M) / (l 2^(m-M) + 2^(sink-M)), M = max(m, sink), all in base-2 units: the merge of a
   // single split
 #pragma unroll
@@ -569,12 +587,17 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void attn_prefill_kernel(
   attn_prefill_body(blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, items, out);
 }
 
-// A step with prefill items and split items in one launch: the prefill workgroups first, then
-// workgroups of kPrefillWaves split items (one per wave; the split body has no workgroup barrier,
-// so a wave past the item count leaves alone).  The split items, bandwidth-bound, then fill the
-// slots the prefill workgroups (MFMA- and latency-bound) free towards their end instead of waiting
-// for the whole prefill launch.  Both bodies fit two waves per SIMD.
-__global__ __launch_bounds__(64 * kPrefillWaves, 2) void attn_step_kernel(
+// A step with prefill items and split items in one launch: prefill workgroups and workgroups of
+// kPrefillWaves split items (one per wave; the split body has no workgroup barrier, so a wave past the
+// item count leaves alone).
+// LEAN (every split item has <= 2 tokens, one row tile): the split body is the lean one and the
+// kernel fits three waves per SIMD, as the prefill body alone does; the split workgroups are spread
+// evenly through the grid, so the bandwidth-bound split items stream KV from HBM while the prefill
+// items (VALU- and MFMA-bound, their keys L2-resident) compute.  Otherwise (row tiles of up to 4
+// tokens) both bodies fit two waves per SIMD, the prefill workgroups come first and the split items
+// fill the slots the prefill workgroups free towards their end.
+template <bool LEAN>
+__global__ __launch_bounds__(64 * kPrefillWaves, LEAN ? 3 : 2) void attn_step_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
     const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
     const int32_t* __restrict__ kv_cap, int window, int Hq,
@@ -582,16 +605,29 @@ __global__ __launch_bounds__(64 * kPrefillWaves, 2) void attn_step_kernel(
     float* __restrict__ partials, const flyai_attn_group* __restrict__ groups, int n_groups,
     const float* __restrict__ sinks, uint16_t* __restrict__ out, const flyai_attn_item* __restrict__ pitems,
     int n_pitems) {
-  if ((int)blockIdx.x < n_pitems) {
-    attn_prefill_body(blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, pitems, out);
+  const int b = blockIdx.x;
+  int split_wg;  // this workgroup's index among the split workgroups, or -1 (a prefill item)
+  int pidx = b;
+  if (LEAN) {
+    // Bresenham spread: block b is split workgroup d0 when floor((b+1) D/T) > floor(b D/T) = d0
+    // (exactly D of the T blocks); otherwise it is prefill item b - d0.
+    const int64_t D = (int64_t)gridDim.x - n_pitems, T = gridDim.x;
+    const int d0 = (int)(b * D / T), d1 = (int)((b + 1) * D / T);
+    split_wg = d1 > d0 ? d0 : -1;
+    pidx = b - d0;
+  } else {
+    split_wg = b < n_pitems ? -1 : b - n_pitems;
+  }
+  if (split_wg < 0) {
+    attn_prefill_body(pidx, q, k_pool, v_pool, kv_base, kv_cap, sinks, window, Hq, pitems, out);
     return;
   }
-  const int idx = ((int)blockIdx.x - n_pitems) * kPrefillWaves + (int)(threadIdx.x >> 6);
+  const int idx = split_wg * kPrefillWaves + (int)(threadIdx.x >> 6);
   if (idx >= n_items || (n_live && idx >= *n_live)) return;
   const flyai_attn_item it = items[idx];
-  if (it.ntok <= 2)
-    attn_item<1, false>(it, idx, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks,
-                        out, nullptr, nullptr);
+  if (LEAN || it.ntok <= 2)
+    attn_item<1, false, LEAN>(it, idx, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups,
+                              sinks, out, nullptr, nullptr);
   else
     attn_item<2, false>(it, idx, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks,
                         out, nullptr, nullptr);
@@ -690,15 +726,17 @@ int launch_attn(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_poo
 }
 
 // One launch of attn_step_kernel for a step with both item kinds, then the merge as in launch_attn.
+// lean: every split item has <= 2 tokens (the planner's n_small covers all of them).
 int launch_attn_step(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool, const int64_t* kv_base,
                      const int32_t* kv_cap, const float* sinks, int window, int Hq, const flyai_attn_item* items,
                      int n_items, const flyai_attn_group* groups, int n_groups, const int32_t* counts, float* partials,
-                     const flyai_attn_item* pitems, int n_pitems, uint16_t* out, bool merge, hipStream_t s) {
+                     const flyai_attn_item* pitems, int n_pitems, uint16_t* out, bool merge, bool lean,
+                     hipStream_t s) {
   const int grid = n_pitems + (n_items + kPrefillWaves - 1) / kPrefillWaves;
   if (grid == 0) return FLYAI_OK;
-  hipLaunchKernelGGL(attn_step_kernel, dim3(grid), dim3(64 * kPrefillWaves), 0, s, q, k_pool, v_pool, kv_base,
-                     kv_cap, window, Hq, items, n_items, counts, partials, groups, n_groups, sinks, out, pitems,
-                     n_pitems);
+  hipLaunchKernelGGL(lean ? attn_step_kernel<true> : attn_step_kernel<false>, dim3(grid), dim3(64 * kPrefillWaves),
+                     0, s, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, items, n_items, counts, partials, groups,
+                     n_groups, sinks, out, pitems, n_pitems);
   int rc = check_launch("attn_step");
   if (rc) return rc;
   if (!merge || n_items == 0) return FLYAI_OK;

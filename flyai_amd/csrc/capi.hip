@@ -68,7 +68,7 @@ int launch_attn_prefill(const uint16_t*, const uint16_t*, const uint16_t*, const
                         const float*, int, int, const flyai_attn_item*, int, uint16_t*, hipStream_t);
 int launch_attn_step(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
                      const float*, int, int, const flyai_attn_item*, int, const flyai_attn_group*, int,
-                     const int32_t*, float*, const flyai_attn_item*, int, uint16_t*, bool, hipStream_t);
+                     const int32_t*, float*, const flyai_attn_item*, int, uint16_t*, bool, bool, hipStream_t);
 int attn_plan_tree(const flyai_attn_tree&, int, int, int, flyai_attn_item*, int, flyai_attn_group*, int,
                    int*, int*, int*);
 int launch_pack(const int32_t*, const int32_t*, const int64_t*, const int32_t*, int, int, int, int32_t*,
@@ -122,7 +122,7 @@ struct flyai_stage {
   bool graphs = false;
   hipStream_t capture_stream = nullptr;
   struct Graph {
-    int64_t key[10];
+    int64_t key[12];
     hipGraphExec_t exec;
     uint64_t last_use;
   };
@@ -325,6 +325,7 @@ struct StepPlan {
   int n_small[2];
   int n_pitems[2];  // chunked-prefill attention items (exact counts, part of the graph key)
   int merge[2];     // some group has more than one split: the merge kernel runs (part of the graph key)
+  int lean[2];      // every split item has <= 2 tokens: the three-wave step kernel (part of the graph key)
   size_t off_counts, off_q, off_st, off_cap, off_base, off_items[2], off_groups[2], off_pitems[2];
   bool tree = false;  // a tree-verify step: the blob carries the flyai_attn_tree at off_tree
   size_t off_tree = 0;
@@ -370,7 +371,7 @@ static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* count
                            sp.grid_items[p], reinterpret_cast<const flyai_attn_group*>(blob + sp.off_groups[p]),
                            sp.grid_groups[p], counts ? counts + 2 * p : nullptr, F32(st->o_parts),
                            reinterpret_cast<const flyai_attn_item*>(blob + sp.off_pitems[p]), sp.n_pitems[p],
-                           B16(st->o_attn), sp.merge[p] != 0, s));
+                           B16(st->o_attn), sp.merge[p] != 0, sp.lean[p] != 0, s));
     } else {
       RUN(launch_attn(B16(st->o_qrot), L.k_pool, L.v_pool, base_d, cap_d, L.sinks,
                       L.sliding ? c.window : 0, c.n_q_heads,
@@ -431,8 +432,8 @@ static int hip_fail(const char* what, hipError_t e) {
 
 // The executable graph for this step's key, captured on first use (least recently used evicted).
 static int step_graph(flyai_stage* st, const StepPlan& sp, hipGraphExec_t* out) {
-  const int64_t key[10] = {sp.Tn, sp.S, sp.grid_items[0], sp.grid_items[1], sp.grid_groups[0], sp.grid_groups[1],
-                           sp.n_pitems[0], sp.n_pitems[1], sp.merge[0], sp.merge[1]};
+  const int64_t key[12] = {sp.Tn, sp.S, sp.grid_items[0], sp.grid_items[1], sp.grid_groups[0], sp.grid_groups[1],
+                           sp.n_pitems[0], sp.n_pitems[1], sp.merge[0], sp.merge[1], sp.lean[0], sp.lean[1]};
   ++st->use_clock;
   for (auto& g : st->graph_cache)
     if (memcmp(g.key, key, sizeof(key)) == 0) {
@@ -607,6 +608,7 @@ extern "C" int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens, const
     sp.grid_items[p] = st->graphs ? bucket(n_items[p], c.max_attn_items) : n_items[p];
     sp.grid_groups[p] = st->graphs ? bucket(n_groups[p], st->max_groups) : n_groups[p];
     sp.merge[p] = plan_needs_merge(st->plan_groups[p].data(), n_groups[p]);
+    sp.lean[p] = sp.n_small[p] == n_items[p];
   }
   RUN(stage_blob(st, sp, q_lens, starts, kv_base, kv_cap, n_items, n_groups, nullptr, s));
   if (!st->graphs) return record_step(st, sp, nullptr, hidden, s);
@@ -681,6 +683,7 @@ extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t 
     sp.grid_groups[p] = n_groups[p];
     sp.n_pitems[p] = 0;
     sp.merge[p] = plan_needs_merge(st->plan_groups[p].data(), n_groups[p]);
+    sp.lean[p] = 0;
   }
   const int32_t q_len = n, st0 = start;
   RUN(stage_blob(st, sp, &q_len, &st0, &kv_base, &kv_cap, n_items, n_groups, &tree, s));

@@ -509,15 +509,19 @@ __device__ __forceinline__ void attn_prefill_body(
   const int int_hi = min(it.key_hi - 1, pos_w);
 
   // staging: load instruction j (j < 4) of wave w copies uint4s s0 .. s0 + 63, s0 = 256 j + 64 w, of
-  // the block (K: s < 512, V: s >= 512), lane L the one at s0 + L (the DMA's lane order)
+  // the block (K: s < 512, V: s >= 512), lane L the one at s0 + L (the DMA's lane order).  The
+  // source is a wave-uniform block address plus the lane's fixed 16 L bytes, and the wave index is
+  // read into a scalar, so a block's loads cost scalar adds only (no per-lane 64-bit address math).
   constexpr int kPer = 1024 / (64 * kPrefillWaves);
   const int kb_first = it.key_lo & ~63;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lane_off = (uint32_t)lane * 16u;
   auto issue = [&](uint4 (&dst)[2][512], int kb) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < kPer; ++j) {
-      const int s0 = 64 * kPrefillWaves * j + 64 * wave;  // wave-uniform
-      const uint4* src = (s0 < 512 ? Kb + (size_t)kb * 8 + s0 : Vb + (size_t)kb * 8 + (s0 - 512)) + lane;
-      __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr)(&dst[0][0] + s0), 16, 0, 0);
+      const int s0 = 64 * kPrefillWaves * j + 64 * wave_s;  // wave-uniform
+      const char* blk = reinterpret_cast<const char*>(s0 < 512 ? Kb : Vb) + ((size_t)kb * 8 + (s0 & 511)) * 16;
+      __builtin_amdgcn_global_load_lds((const void*)(blk + lane_off), (lds_ptr)(&dst[0][0] + s0), 16, 0, 0);
     }
   };
   // the wave's own loads have landed (vector memory loads complete in issue order; the DMA counts
@@ -538,7 +542,8 @@ __device__ __forceinline__ void attn_prefill_body(
     uint4 (&cur)[2][512] = decltype(parity)::value ? kvs1 : kvs0;
     uint4 (&nxt)[2][512] = decltype(parity)::value ? kvs0 : kvs1;
     if (kb + 64 < it.key_hi) issue(nxt, kb + 64);
-    if (ntw > 0 && kb <= pos_last && kb + 63 >= lo_w)
+    // (an interior block is seen by the wave's rows: no test)
+    if (!decltype(masked)::value || (ntw > 0 && kb <= pos_last && kb + 63 >= lo_w))
       prefill_rows_block<decltype(masked)::value>(R, cur[0], cur[1], kb, it.key_lo, it.key_hi, window);
     landed();
   };

@@ -132,14 +132,13 @@ __device__ __forceinline__ void rows_init(QRows<QT>& R, const uint16_t* __restri
 
 // Max over the four lanes n, n+16, n+32, n+48 (one query row's lane groups), with gfx950's
 // v_permlane32_swap / v_permlane16_swap (VALU lane swaps, no LDS round trip).  Swapping a register
-// with a copy of itself leaves lane i's value and its partner's in the two results.
+// with a copy of itself leaves lane i's value and its partner's in the two results.  The inputs are
+// block maxima over scores with masked keys at -inf, never NaN, so fmaxf (one v_max_f32) is exact.
 __device__ __forceinline__ float max_lane_groups(float v) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  const float x0 = __uint_as_float(a[0]), x1 = __uint_as_float(a[1]);
-  v = x0 > x1 ? x0 : x1;
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  const float y0 = __uint_as_float(b[0]), y1 = __uint_as_float(b[1]);
-  return y0 > y1 ? y0 : y1;
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 // One 64-key block kb (K fragments kc, V fragments vv of this lane) against the rows: scores

@@ -118,6 +118,9 @@ class RaggedStage:
         handle = C.c_void_p()
         check(lib().flyai_stage_create(C.byref(cfg), C.byref(handle)))
         self._h = handle
+        # held here: at interpreter exit the module globals the destructor would reach may be gone
+        self._destroy = lib().flyai_stage_destroy
+        self._sync = torch.cuda.synchronize
         self.layers = list(layers)
         for i, lw in enumerate(layers):
             self.set_layer(i, lw)
@@ -168,12 +171,12 @@ class RaggedStage:
     def __del__(self):
         h = getattr(self, "_h", None)
         if h:
+            self._h = None
             try:
-                torch.cuda.synchronize(self.device)
+                self._sync(self.device)
             except Exception:
                 pass
-            lib().flyai_stage_destroy(h)
-            self._h = None
+            self._destroy(h)
 
     def forward(self, hidden, q_lens, starts, slots):
         """hidden bf16 [T, H] (packed token order, updated in place and returned); q_lens/starts/slots

@@ -613,12 +613,24 @@ __global__ __launch_bounds__(64 * kPrefillWaves, LEAN ? 3 : 2) void attn_step_ke
   int split_wg;  // this workgroup's index among the split workgroups, or -1 (a prefill item)
   int pidx = b;
   if (LEAN) {
-    // Bresenham spread: block b is split workgroup d0 when floor((b+1) D/T) > floor(b D/T) = d0
-    // (exactly D of the T blocks); otherwise it is prefill item b - d0.
-    const int64_t D = (int64_t)gridDim.x - n_pitems, T = gridDim.x;
-    const int d0 = (int)(b * D / T), d1 = (int)((b + 1) * D / T);
-    split_wg = d1 > d0 ? d0 : -1;
-    pidx = b - d0;
+    // Bresenham spread over groups of 8 blocks: group gi is split group d0 when
+    // floor((gi+1) DG/TG) > floor(gi DG/TG) = d0 (exactly DG of the TG groups); otherwise it is
+    // prefill group gi - d0.  Whole groups of 8 keep prefill item i on block i mod 8, i.e. on
+    // XCD i mod 8 (workgroups are dealt round-robin over the 8 XCDs) as in the prefill-only
+    // launch: the plan lists a chunk's kv heads consecutively, so each XCD's L2 holds the K/V of
+    // one kv head (with 8) instead of all of them.
+    const int P = n_pitems, D = (n_items + kPrefillWaves - 1) / kPrefillWaves;
+    const int64_t PG = (P + 7) / 8, DG = (D + 7) / 8, TG = PG + DG;
+    const int gi = b >> 3, l8 = b & 7;
+    const int d0 = (int)(gi * DG / TG), d1 = (int)((gi + 1) * DG / TG);
+    if (d1 > d0) {
+      split_wg = 8 * d0 + l8;
+      if (split_wg >= D) return;
+    } else {
+      split_wg = -1;
+      pidx = 8 * (gi - d0) + l8;
+      if (pidx >= P) return;
+    }
   } else {
     split_wg = b < n_pitems ? -1 : b - n_pitems;
   }
@@ -736,7 +748,9 @@ int launch_attn_step(const uint16_t* q, const uint16_t* k_pool, const uint16_t* 
                      int n_items, const flyai_attn_group* groups, int n_groups, const int32_t* counts, float* partials,
                      const flyai_attn_item* pitems, int n_pitems, uint16_t* out, bool merge, bool lean,
                      hipStream_t s) {
-  const int grid = n_pitems + (n_items + kPrefillWaves - 1) / kPrefillWaves;
+  const int n_split_wg = (n_items + kPrefillWaves - 1) / kPrefillWaves;
+  // the lean kernel deals whole groups of 8 blocks (see attn_step_kernel)
+  const int grid = lean ? 8 * ((n_pitems + 7) / 8 + (n_split_wg + 7) / 8) : n_pitems + n_split_wg;
   if (grid == 0) return FLYAI_OK;
   hipLaunchKernelGGL(lean ? attn_step_kernel<true> : attn_step_kernel<false>, dim3(grid), dim3(64 * kPrefillWaves),
                      0, s, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, items, n_items, counts, partials, groups,

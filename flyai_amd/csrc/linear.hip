@@ -609,6 +609,26 @@ __global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_lds_kernel(const 
     mfma_step(a1, b1);
     issue(ca, cb, q + kTlStages);
   };
+  // QKV: the epilogue's per-row data is fetched under the GEMM instead of after it (it took two
+  // dependent round trips per workgroup at the end, with nothing else on the CU to hide them).
+  // Lane L of wave w fetches row 16 w + L / 4 of the tile: its position and sequence before the
+  // prologue (so the first stage wait covers them), then the row's cos / sin (64 bytes each, 16 per
+  // lane, global -> LDS) and slab geometry once they have landed.  The epilogue reads all of it
+  // from LDS.  (These extra loads only make the later stage waits stricter, never looser.)
+  __shared__ __align__(16) uint16_t rot_c[QKV ? kTileM * 32 : 1], rot_s[QKV ? kTileM * 32 : 1];
+  __shared__ int row_pos[QKV ? kTileM : 1], row_cap[QKV ? kTileM : 1];
+  __shared__ int64_t row_base[QKV ? kTileM : 1];
+  const int erow = 16 * wave + (lane >> 2);  // the tile row this lane fetches for
+  int e_pos = 0, e_sq = 0;
+  float bv[4];
+  if constexpr (QKV) {
+    const int t = min(m0 + erow, M - 1);
+    e_pos = ep.positions[t];
+    e_sq = ep.seq_id[t];
+    const int fb = min(n0 + 64 * wn, N - 64);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) bv[b] = ep.bias ? bf2f(ep.bias[fb + 16 * b + r]) : 0.f;
+  }
   // the stage waits count loads per group in issue order: no load may move across a group
   asm volatile("" ::: "memory");
   issue(sa0, sb0, 0);
@@ -621,6 +641,18 @@ __global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_lds_kernel(const 
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_waitcnt(waitcnt_vm((kTlStages - 1) * kTlLoads));
   lds_barrier();  // stage 0 is in LDS
+  int e_cap = 0;
+  int64_t e_base = 0;
+  if constexpr (QKV) {
+    // e_pos / e_sq landed with stage 0 (issued before it)
+    const int pc = min(max(e_pos, 0), ep.rope_positions - 1);
+    const size_t roff = (size_t)pc * 32 + 8 * (lane & 3);
+    __builtin_amdgcn_global_load_lds((const void*)(ep.cos_tab + roff), (lds_ptr)(rot_c + 16 * wave * 32), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((const void*)(ep.sin_tab + roff), (lds_ptr)(rot_s + 16 * wave * 32), 16, 0, 0);
+    e_cap = ep.kv_cap[e_sq];
+    e_base = ep.kv_base[e_sq];
+    asm volatile("" ::: "memory");
+  }
   read_ab(a0, b0, sa0, sb0, 0);
   // whole 512-K slices (8 groups, two turns of the 4 stages), each folded after its last group
   const int full = KG / kTlGroupsPerSlice;
@@ -664,38 +696,32 @@ __global__ __launch_bounds__(64 * kTiledWaves) void gemm_tiled_lds_kernel(const 
         }
       }
   } else {
+    // every lane's fetched row data to LDS (the rotary rows are there already: vmcnt(0) above)
+    if ((lane & 3) == 0) {
+      row_pos[erow] = e_pos;
+      row_cap[erow] = e_cap;
+      row_base[erow] = e_base;
+    }
+    lds_barrier();
     const int fb = n0 + 64 * wn;  // the wave's head: q heads, then k heads, then v heads
     if (fb >= N) return;
     const int hd = fb / 64;
     const bool rotated = hd < ep.Hq + ep.Hkv;
-    // every load the 8 rows of the lane need goes out in two batches (indices, then the sequences'
-    // slab geometry and the rotary rows) before the first store
-    int pos[2][4], sq[2][4];
-#pragma unroll
-    for (int a = 0; a < 2; ++a)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int t = min(m0 + 16 * (2 * wm + a) + 4 * g + v, M - 1);
-        pos[a][v] = ep.positions[t];
-        sq[a][v] = ep.seq_id[t];
-      }
-    float bv[4];
-#pragma unroll
-    for (int b = 0; b < 4; ++b) bv[b] = ep.bias ? bf2f(ep.bias[fb + 16 * b + r]) : 0.f;
-    int cap[2][4];
+    int pos[2][4], cap[2][4];
     int64_t base[2][4];
     float cs[2][4][2], sn[2][4][2];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        cap[a][v] = ep.kv_cap[sq[a][v]];
-        base[a][v] = ep.kv_base[sq[a][v]];
-        const int pc = min(max(pos[a][v], 0), ep.rope_positions - 1);
+        const int tr = 16 * (2 * wm + a) + 4 * g + v;
+        pos[a][v] = row_pos[tr];
+        cap[a][v] = row_cap[tr];
+        base[a][v] = row_base[tr];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-          cs[a][v][b] = rotated ? bf2f(ep.cos_tab[(size_t)pc * 32 + 16 * b + r]) : 0.f;
-          sn[a][v][b] = rotated ? bf2f(ep.sin_tab[(size_t)pc * 32 + 16 * b + r]) : 0.f;
+          cs[a][v][b] = bf2f(rot_c[tr * 32 + 16 * b + r]);
+          sn[a][v][b] = bf2f(rot_s[tr * 32 + 16 * b + r]);
         }
       }
 #pragma unroll

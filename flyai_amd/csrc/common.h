@@ -24,13 +24,11 @@ int check_launch(const char* what);
 // ---- bf16 <-> fp32 -----------------------------------------------------------------------------
 __device__ __forceinline__ float bf2f(uint16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
 
-// round-to-nearest-even fp32 -> bf16 bits (quiet NaN preserved)
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// round-to-nearest-even fp32 -> bf16 bits, NaN made quiet (high 16 bits | 0x40): gfx950's
+// v_cvt_pk_bf16_f32 (the __bf16 cast), one instruction for two values.  Checked against the integer
+// formulation ((u + 0x7fff + ((u >> 16) & 1)) >> 16, NaN -> (u >> 16) | 0x40) on 1.1 million inputs
+// (random words, every special class, 65,536 denormals): no bit differs.
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 __device__ __forceinline__ float bf16_round(float f) { return bf2f(f2bf(f)); }
 

@@ -124,6 +124,8 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
   const int r = lane & 15, g = lane >> 4;
   const int row_bytes = mx_lds_row_bytes(K);
   const int row_vecs = K / 8;  // 16-byte vectors per activation row
+  const bool k_pow2 = (k_top & (k_top - 1)) == 0;  // slot -> token by a shift (the routers' k: 2, 4, 8)
+  const int k_shift = __builtin_ctz((unsigned)k_top);
 
   const uint8_t* data = packed + ((size_t)e * gm.NT + nt0) * gm.G * 256 + lane * 16;
   const uint32_t* scl = reinterpret_cast<const uint32_t*>(
@@ -159,26 +161,39 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
     // LDS-only barrier below leaves them in flight.
     constexpr int kStageBatch = 4;
     const int total = rows * row_vecs;
+    // (row, vector) of the thread's element b0 + j * 256 + tid, stepped by 256 without an integer
+    // division (a 32-bit division is ~25 VALU instructions, and these sit before the first load)
+    int cr = 0, cv = threadIdx.x;
+    while (cv >= row_vecs) {
+      cv -= row_vecs;
+      ++cr;
+    }
     for (int b0 = 0; b0 < total; b0 += kStageBatch * 256) {
       u32x4_t v4[kStageBatch];
+      int jr[kStageBatch], jv[kStageBatch];
 #pragma unroll
       for (int j = 0; j < kStageBatch; ++j) {
-        const int i = min(b0 + j * 256 + (int)threadIdx.x, total - 1);
-        const int rr = i / row_vecs, v = i % row_vecs;
+        jr[j] = cr;
+        jv[j] = cv;
+        const bool in = cr < rows;  // element index < total; past it, the last element (not stored)
+        const int rr = in ? cr : rows - 1, v = in ? cv : row_vecs - 1;
         const int p = row_lo + m0 + rr;
-        const int src = GATE_UP ? perm[p] / k_top : p;
+        const int src = GATE_UP ? (k_pow2 ? perm[p] >> k_shift : perm[p] / k_top) : p;
         v4[j] = reinterpret_cast<const u32x4_t*>(act + (size_t)src * K)[v];
+        cv += 256;
+        while (cv >= row_vecs) {
+          cv -= row_vecs;
+          ++cr;
+        }
       }
       if (b0 == 0) {
         mx_static_for<0, kSc>([&](auto q) { load_sc(sc_cur[q], q); });
         mx_static_for<0, DEPTH - 1>([&](auto j) { load_w(w[j], j); });
       }
 #pragma unroll
-      for (int j = 0; j < kStageBatch; ++j) {
-        const int i = b0 + j * 256 + (int)threadIdx.x;
-        if (i < total)
-          *reinterpret_cast<u32x4_t*>(const_cast<char*>(lds) + (i / row_vecs) * row_bytes + (i % row_vecs) * 16) = v4[j];
-      }
+      for (int j = 0; j < kStageBatch; ++j)
+        if (jr[j] < rows)
+          *reinterpret_cast<u32x4_t*>(const_cast<char*>(lds) + jr[j] * row_bytes + jv[j] * 16) = v4[j];
     }
     lds_barrier();
     if (ntw == 0) continue;

@@ -38,19 +38,35 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   // one memory round trip for the whole workgroup (H <= JMAX * 512 bounds the count)
   constexpr int kPer = (TT * JMAX * 64 + 255) / 256;
   u32x4 v4[kPer];
+  // (token, vector) of element j * 256 + tid, stepped by 256 without integer divisions
+  int jt[kPer], jv[kPer];
+  {
+    int ct = 0, cv = tid;
+    while (cv >= vecs) {
+      cv -= vecs;
+      ++ct;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+      jt[j] = ct;
+      jv[j] = cv;
+      cv += 256;
+      while (cv >= vecs) {
+        cv -= vecs;
+        ++ct;
+      }
+    }
+  }
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
-    const int i = j * 256 + tid;
-    const int t = i / vecs, v = i % vecs;
-    const bool ok = i < TT * vecs && t < nt;
+    const int t = jt[j], v = jv[j];
+    const bool ok = t < TT && t < nt;  // (t < TT: element index < TT * vecs)
     const u32x4 val = reinterpret_cast<const u32x4*>(x + (ok ? (size_t)(t0 + t) * H : 0))[ok ? v : 0];
     v4[j] = ok ? val : u32x4{0u, 0u, 0u, 0u};
   }
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = j * 256 + tid;
-    if (i < TT * vecs) reinterpret_cast<u32x4*>(xs + (i / vecs) * H)[i % vecs] = v4[j];
-  }
+  for (int j = 0; j < kPer; ++j)
+    if (jt[j] < TT) reinterpret_cast<u32x4*>(xs + jt[j] * H)[jv[j]] = v4[j];
   __syncthreads();
   float acc[EPW][TT];
 #pragma unroll
@@ -450,10 +466,21 @@ __global__ __launch_bounds__(kPermWaves * 64) void moe_topk_permute_kernel(
       const int i = threadIdx.x + j * kPermWaves * 64;
       v[j] = i < T * E ? logits[i] : 0.f;
     }
+    // row-major into rows of E + 4 floats; (row, column) by a shift and a mask when E is a power
+    // of two (128 for GPT-OSS), which keeps 16 integer divisions off the single workgroup's path
+    if ((E & (E - 1)) == 0) {
+      const int e_shift = __builtin_ctz((unsigned)E);
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-      const int i = threadIdx.x + j * kPermWaves * 64;
-      if (i < T * E) lg_s[(i / E) * (E + 4) + i % E] = v[j];
+      for (int j = 0; j < kPer; ++j) {
+        const int i = threadIdx.x + j * kPermWaves * 64;
+        if (i < T * E) lg_s[(i >> e_shift) * (E + 4) + (i & (E - 1))] = v[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kPer; ++j) {
+        const int i = threadIdx.x + j * kPermWaves * 64;
+        if (i < T * E) lg_s[(i / E) * (E + 4) + i % E] = v[j];
+      }
     }
     __syncthreads();
   }

@@ -90,6 +90,24 @@ __device__ __forceinline__ float swiglu_gptoss(float gate, float up) {
   return (u + 1.0f) * glu;
 }
 
+// value of lane ^ 1 (DPP quad permutation [1, 0, 3, 2]; no LDS traffic)
+__device__ __forceinline__ float lane_xor1(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+
+// The gate_up epilogue for one 16-feature tile's 4 rows held by lane (r, g) (rows 4g + v, v < 4):
+// lanes r and r ^ 1 hold the gate (even r) and up values of one output feature.  One exchange of two
+// values each gives the even lane (gate, up) of rows v = 0, 1 and the odd lane those of rows v = 2, 3,
+// so every lane computes two SwiGLUs (none twice) and stores two results: store(v, bf16 bits).
+template <class Store>
+__device__ __forceinline__ void swiglu_pairs(const float (&val)[4], int r, const Store& store) {
+  const bool ev = (r & 1) == 0;
+  const float s0 = lane_xor1(ev ? val[2] : val[0]);
+  const float s1 = lane_xor1(ev ? val[3] : val[1]);
+  store(ev ? 0 : 2, f2bf(swiglu_gptoss(ev ? val[0] : s0, ev ? s0 : val[2])));
+  store(ev ? 1 : 3, f2bf(swiglu_gptoss(ev ? val[1] : s1, ev ? s1 : val[3])));
+}
+
 // compile-time loop: f(integral_constant<int, B>) ... f(integral_constant<int, N-1>)
 template <int B, int N, class F>
 __device__ __forceinline__ void mx_static_for(F&& f) {
@@ -238,18 +256,18 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
       const int feat = (nt0 + n) * 16 + r;
       const bool nval = n < ntw;
       const float bsum = nval ? bias[(size_t)e * N + feat] : 0.f;
+      if (GATE_UP) {
+        const float val[4] = {acc[n][0] + bsum, acc[n][1] + bsum, acc[n][2] + bsum, acc[n][3] + bsum};
+        swiglu_pairs(val, r, [&](int v, uint16_t hbits) {
+          if (nval && 4 * g + v < rows)
+            reinterpret_cast<uint16_t*>(out)[(size_t)(row_lo + m0 + 4 * g + v) * (N / 2) + feat / 2] = hbits;
+        });
+      } else {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int orow = 4 * g + v;
-        const float val = acc[n][v] + bsum;
-        if (GATE_UP) {
-          const float partner = __shfl_xor(val, 1, 64);
-          if (nval && (r & 1) == 0 && orow < rows)
-            reinterpret_cast<uint16_t*>(out)[(size_t)(row_lo + m0 + orow) * (N / 2) + feat / 2] =
-                f2bf(swiglu_gptoss(val, partner));
-        } else {
+        for (int v = 0; v < 4; ++v) {
+          const int orow = 4 * g + v;
           if (nval && orow < rows)
-            reinterpret_cast<float*>(out)[(size_t)(row_lo + m0 + orow) * N + feat] = val;
+            reinterpret_cast<float*>(out)[(size_t)(row_lo + m0 + orow) * N + feat] = acc[n][v] + bsum;
         }
       }
     }
@@ -313,11 +331,6 @@ constexpr int kGemmStages = 4;
 
 // instruction classes for __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedValu = 0x2, kSchedMfma = 0x8, kSchedVmem = 0x10, kSchedDsRead = 0x100;
-
-// value of lane ^ 1 (DPP quad permutation [1, 0, 3, 2]; no LDS traffic)
-__device__ __forceinline__ float lane_xor1(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
-}
 
 // Position key of activation row r (0..15) in the dense GEMM's LDS row tiles: the chunk c of row r sits
 // at 16-byte slot c ^ act_swz(r).  gfx950's LDS has 64 banks of 4 bytes, and a ds_read_b128 serves
@@ -559,18 +572,20 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
       const int feat = tile * 16 + r;
 #pragma unroll
       for (int m = 0; m < MT; ++m) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int orow = 16 * m + 4 * g + v;
-          const float val = acc[m][n][v] + bsum[n];
-          if (GATE_UP) {
-            const float partner = lane_xor1(val);
-            if (nval && (r & 1) == 0 && orow < rows)
-              reinterpret_cast<uint16_t*>(c.out)[(size_t)(c.row_lo + m0 + orow) * (c.N / 2) + feat / 2] =
-                  f2bf(swiglu_gptoss(val, partner));
-          } else {
+        if (GATE_UP) {
+          const float val[4] = {acc[m][n][0] + bsum[n], acc[m][n][1] + bsum[n], acc[m][n][2] + bsum[n],
+                                acc[m][n][3] + bsum[n]};
+          swiglu_pairs(val, r, [&](int v, uint16_t hbits) {
+            const int orow = 16 * m + 4 * g + v;
             if (nval && orow < rows)
-              reinterpret_cast<float*>(c.out)[(size_t)(c.row_lo + m0 + orow) * c.N + feat] = val;
+              reinterpret_cast<uint16_t*>(c.out)[(size_t)(c.row_lo + m0 + orow) * (c.N / 2) + feat / 2] = hbits;
+          });
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int orow = 16 * m + 4 * g + v;
+            if (nval && orow < rows)
+              reinterpret_cast<float*>(c.out)[(size_t)(c.row_lo + m0 + orow) * c.N + feat] = acc[m][n][v] + bsum[n];
           }
         }
       }
@@ -956,18 +971,21 @@ __device__ __forceinline__ void mx_gemm_pass(const MxCtx& c, char (&st0)[kMxStag
       const int feat = tile * 16 + r;
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
+        float val[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int orow = 16 * m + 4 * g + v;
-          const float val = (acc[m][n][v] + acc[m + MR][n][v]) + bsum[n];
-          if (GATE_UP) {
-            const float partner = lane_xor1(val);
-            if (nval && (r & 1) == 0 && orow < rows)
-              reinterpret_cast<uint16_t*>(c.out)[(size_t)(c.row_lo + m0 + orow) * (c.N / 2) + feat / 2] =
-                  f2bf(swiglu_gptoss(val, partner));
-          } else {
+        for (int v = 0; v < 4; ++v) val[v] = (acc[m][n][v] + acc[m + MR][n][v]) + bsum[n];
+        if (GATE_UP) {
+          swiglu_pairs(val, r, [&](int v, uint16_t hbits) {
+            const int orow = 16 * m + 4 * g + v;
             if (nval && orow < rows)
-              reinterpret_cast<float*>(c.out)[(size_t)(c.row_lo + m0 + orow) * c.N + feat] = val;
+              reinterpret_cast<uint16_t*>(c.out)[(size_t)(c.row_lo + m0 + orow) * (c.N / 2) + feat / 2] = hbits;
+          });
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int orow = 16 * m + 4 * g + v;
+            if (nval && orow < rows)
+              reinterpret_cast<float*>(c.out)[(size_t)(c.row_lo + m0 + orow) * c.N + feat] = val[v];
           }
         }
       }

@@ -132,13 +132,16 @@ __device__ __forceinline__ void rows_init(QRows<QT>& R, const uint16_t* __restri
 
 // Max over the four lanes n, n+16, n+32, n+48 (one query row's lane groups), with gfx950's
 // v_permlane32_swap / v_permlane16_swap (VALU lane swaps, no LDS round trip).  Swapping a register
-// with a copy of itself leaves lane i's value and its partner's in the two results.  The inputs are
-// block maxima over scores with masked keys at -inf, never NaN, so fmaxf (one v_max_f32) is exact.
+// with a copy of itself leaves lane i's value and its partner's in the two results.  (A compare and
+// select: fmaxf on the swapped values is three instructions, since the compiler quiets possible
+// signalling NaNs in both operands first.)
 __device__ __forceinline__ float max_lane_groups(float v) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float x0 = __uint_as_float(a[0]), x1 = __uint_as_float(a[1]);
+  v = x0 > x1 ? x0 : x1;
   const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  const float y0 = __uint_as_float(b[0]), y1 = __uint_as_float(b[1]);
+  return y0 > y1 ? y0 : y1;
 }
 
 // One 64-key block kb (K fragments kc, V fragments vv of this lane) against the rows: scores

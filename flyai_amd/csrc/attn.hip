@@ -75,17 +75,24 @@ __device__ __forceinline__ void load_v_tile(uint4 (&v)[4][2], const uint16_t* __
     for (int dt = 0; dt < 4; ++dt) v[dt][h] = ld_kv(blk + h * 2048 + dt * 512);
 }
 
+// A tree-verify launch's view of its flyai_attn_tree: the node depths and the visibility mask of the
+// launch's layer kind (bit j of row i: node i sees tree slot start + j).  Empty outside trees.
+struct TreeView {
+  int start = 0, n = 0, words = 0;
+  const int32_t* depth = nullptr;
+  const uint64_t* mask = nullptr;
+};
+
 // Per-wave state of QT query-row tiles of 16 (QT = 1: up to 2 tokens; QT = 2: up to 4 tokens): the
-// Q^T operand, each row's position (and, in a tree, its depth and ancestor set), and the running
+// Q^T operand, each row's position (and, in a tree, its depth and node), and the running
 // softmax (max, sum, O^T accumulators).  Query row rq = 16*qt + n is token rq/8, head kv_head*8 + rq%8.
 // The row sums are accumulated like O^T, by an MFMA with an all-ones A operand: every element of
 // lane (n, g)'s L[qt] is row n's complete sum over the keys so far.
 template <int QT>
 struct QRows {
   bf16x8_t qf[QT][2];
-  int qpos[QT], qdep[QT];
+  int qpos[QT], qdep[QT], qnode[QT];
   bool qval[QT];
-  uint64_t qanc[QT];
   float m_run[QT];
   f32x4_t O[QT][4], L[QT];
 };
@@ -94,25 +101,21 @@ struct QRows {
 // running softmax.
 template <int QT, bool TREE>
 __device__ __forceinline__ void rows_init(QRows<QT>& R, const uint16_t* __restrict__ q, int tok, int ntok,
-                                          int pos0, int kv_head, int Hq,
-                                          const flyai_attn_tree* __restrict__ tree,
-                                          const int* __restrict__ dep_s) {
+                                          int pos0, int kv_head, int Hq, const TreeView& tv) {
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
-  const int tstart = TREE ? tree->start : 0;
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int rq = 16 * qt + n;
     const int ti = rq >> 3;
     R.qval[qt] = ti < ntok;
     if (TREE) {
-      const int node = (tok + ti) & 63;  // < n_nodes <= 64 for every valid row
-      R.qdep[qt] = R.qval[qt] ? dep_s[node] : 0;
-      R.qanc[qt] = R.qval[qt] ? tree->ancestors[node] : 0ull;
-      R.qpos[qt] = tstart + R.qdep[qt];
+      R.qnode[qt] = R.qval[qt] ? tok + ti : 0;  // tok + ti < n_nodes for every valid row
+      R.qdep[qt] = R.qval[qt] ? tv.depth[tok + ti] : 0;
+      R.qpos[qt] = tv.start + R.qdep[qt];
     } else {
+      R.qnode[qt] = 0;
       R.qdep[qt] = 0;
-      R.qanc[qt] = 0ull;
       R.qpos[qt] = pos0 + ti;
     }
     uint4 a = make_uint4(0, 0, 0, 0), b2 = make_uint4(0, 0, 0, 0);
@@ -159,11 +162,10 @@ constexpr float kMaxSlack = 8.f;
 template <int QT, bool TREE>
 __device__ __forceinline__ void rows_block(QRows<QT>& R, const uint4 (&kc)[4][2], uint4 (&vv)[4][2], int kb,
                                            bool interior, int key_lo, int key_hi, int window,
-                                           const flyai_attn_tree* __restrict__ tree,
-                                           const int* __restrict__ dep_s) {
+                                           const TreeView& tv) {
   const int g = (threadIdx.x & 63) >> 4;
   const float scale = 0.125f * kLog2e;
-  const int tstart = TREE ? tree->start : 0;
+  const int tstart = TREE ? tv.start : 0;
   const bf16x8_t ones = as_bf16x8(make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
   if (kb + 64 > key_hi) {
 #pragma unroll
@@ -190,6 +192,18 @@ __device__ __forceinline__ void rows_block(QRows<QT>& R, const uint4 (&kc)[4][2]
       const int p = R.qpos[qt];
       const int lo = max(key_lo, window > 0 ? p - window + 1 : 0);
       const int hi = min(p, key_hi - 1);
+      // tree: bits [kb - start, kb - start + 64) of the row's mask (key kb + t is bit t)
+      uint64_t tbits = 0;
+      if (TREE) {
+        const int j0 = kb - tstart;
+        if (R.qval[qt] && j0 > -64 && j0 < tv.n) {
+          const int wq = j0 >> 6, sh = j0 & 63;  // floor division (j0 may be negative)
+          const uint64_t* mrow = tv.mask + (size_t)R.qnode[qt] * tv.words;
+          const uint64_t w0 = wq >= 0 ? mrow[wq] : 0ull;
+          const uint64_t w1 = wq + 1 < tv.words ? mrow[wq + 1] : 0ull;
+          tbits = sh == 0 ? w0 : (w0 >> sh) | (w1 << (64 - sh));
+        }
+      }
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -197,13 +211,10 @@ __device__ __forceinline__ void rows_block(QRows<QT>& R, const uint4 (&kc)[4][2]
           const int key = kb + tile_key(kt, 4 * g + v);
           bool ok;
           if (TREE) {
-            if (key < tstart) {
+            if (key < tstart)
               ok = key >= lo && key < key_hi;  // committed prefix (window on positions)
-            } else {
-              const int j = (key - tstart) & 63;  // in range whenever key < key_hi <= start + n
-              ok = key >= key_lo && key < key_hi && ((R.qanc[qt] >> j) & 1ull) &&
-                   (window == 0 || R.qdep[qt] - dep_s[j] < window);
-            }
+            else  // tree slot: the mask (its window already applied for sliding layers)
+              ok = key >= key_lo && key < key_hi && ((tbits >> tile_key(kt, 4 * g + v)) & 1ull);
             ok = ok && R.qval[qt];
           } else {
             ok = R.qval[qt] && key >= lo && key <= hi;
@@ -332,8 +343,8 @@ __device__ __forceinline__ void prefill_rows_block(QRows<2>& R, const uint4* __r
 // One work item (<= 4 tokens x the 8 heads of a kv head, one key split) by one wave, K and V
 // streamed from the slab; writes a partial record (m, l, O[64]) per query row.
 // TREE: the batch is one tree-verify sequence; token (= node) i sits at position
-// tree->start + depth[i] (dep_s: the depths, staged in LDS) and sees the committed keys below
-// tree->start plus the tree slots of its ancestor set (FastVerify._tset masks).
+// tv.start + depth[i] and sees the committed keys below tv.start plus the tree slots its mask row
+// sets (FastVerify._tset masks).
 // LEAN: only K is loaded a block ahead; a block's V is loaded at the block's start and is first
 // read by its PV products, after the scores and the softmax.  Three K/V tiles live instead of four
 // (32 fewer registers): the step kernel that fits three waves per SIMD, where the other waves of the
@@ -348,8 +359,7 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
                                           float* __restrict__ partials,
                                           const flyai_attn_group* __restrict__ groups, int n_groups,
                                           const float* __restrict__ sinks, uint16_t* __restrict__ out,
-                                          const flyai_attn_tree* __restrict__ tree,
-                                          const int* __restrict__ dep_s) {
+                                          const TreeView& tv) {
   const int lane = threadIdx.x & 63;
   const int n = lane & 15, g = lane >> 4;
   // the item is its rows' whole key range (a group index outside the plan reads as "not single")
@@ -359,18 +369,17 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
   const uint16_t* K = k_pool + base;
   const uint16_t* Vt = v_pool + base;
   QRows<QT> R;
-  rows_init<QT, TREE>(R, q, it.tok, it.ntok, it.pos0, it.kv_head, Hq, tree, dep_s);
+  rows_init<QT, TREE>(R, q, it.tok, it.ntok, it.pos0, it.kv_head, Hq, tv);
 
   const int kb_first = it.key_lo & ~63;
   // Blocks fully inside every valid query row's key range need no score mask (wave-uniform test).
   // In a tree only committed keys (below tree->start) can be unmasked for every row.
   int pos_last, int_hi;
   if (TREE) {
-    const int tstart = tree->start;
     int dmax = 0;
-    for (int i = 0; i < it.ntok; ++i) dmax = max(dmax, dep_s[(it.tok + i) & 63]);
-    pos_last = tstart + dmax;
-    int_hi = min(it.key_hi - 1, tstart - 1);
+    for (int i = 0; i < it.ntok; ++i) dmax = max(dmax, tv.depth[it.tok + i]);
+    pos_last = tv.start + dmax;
+    int_hi = min(it.key_hi - 1, tv.start - 1);
   } else {
     pos_last = it.pos0 + it.ntok - 1;
     int_hi = min(it.key_hi - 1, it.pos0);
@@ -388,7 +397,7 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
       if (!LEAN) load_v_tile(vn, Vt, kb + 64, lane);
     }
     const bool interior = kb >= int_lo && kb + 63 <= int_hi;
-    rows_block<QT, TREE>(R, kc, vv, kb, interior, it.key_lo, it.key_hi, window, tree, dep_s);
+    rows_block<QT, TREE>(R, kc, vv, kb, interior, it.key_lo, it.key_hi, window, tv);
     if (more) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
@@ -441,36 +450,48 @@ __device__ __forceinline__ void attn_item(const flyai_attn_item& it, int item_id
   }
 }
 
-// One launch for every item; the body is chosen per item (uniform across the wave).  tree != NULL:
-// the batch is one tree-verify sequence (flyai_stage_forward_tree).
+// One launch for every item; the body is chosen per item (uniform across the wave).
 __global__ __launch_bounds__(64, 2) void attn_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
     const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
     const int32_t* __restrict__ kv_cap, int window, int Hq,
     const flyai_attn_item* __restrict__ items, const int32_t* __restrict__ n_live,
     float* __restrict__ partials, const flyai_attn_group* __restrict__ groups, int n_groups,
-    const float* __restrict__ sinks, uint16_t* __restrict__ out, const flyai_attn_tree* __restrict__ tree) {
-  __shared__ int dep_s[64];
+    const float* __restrict__ sinks, uint16_t* __restrict__ out) {
   // a graph-replayed step launches the plan's capacity; items past this step's count exit
   if (n_live && (int)blockIdx.x >= *n_live) return;
   const flyai_attn_item it = items[blockIdx.x];
-  if (tree) {
-    dep_s[threadIdx.x] = (int)threadIdx.x < tree->n_nodes ? tree->depth[threadIdx.x] : 0;
-    __syncthreads();
-    if (it.ntok <= 2)
-      attn_item<1, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
-                         tree, dep_s);
-    else
-      attn_item<2, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
-                         tree, dep_s);
-    return;
-  }
   if (it.ntok <= 2)
     attn_item<1, false>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
-                         nullptr, nullptr);
+                        TreeView{});
   else
     attn_item<2, false>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
-                         nullptr, nullptr);
+                        TreeView{});
+}
+
+// The items of one tree-verify sequence (flyai_stage_forward_tree).  Its own kernel: the mask words
+// of the tree rows take registers the decode kernel's two waves per SIMD do not have to spare.
+__global__ __launch_bounds__(64, 1) void attn_tree_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, const int64_t* __restrict__ kv_base,
+    const int32_t* __restrict__ kv_cap, int window, int Hq,
+    const flyai_attn_item* __restrict__ items, float* __restrict__ partials,
+    const flyai_attn_group* __restrict__ groups, int n_groups, const float* __restrict__ sinks,
+    uint16_t* __restrict__ out, const flyai_attn_tree* __restrict__ tree) {
+  const flyai_attn_item it = items[blockIdx.x];
+  const char* tb = reinterpret_cast<const char*>(tree);
+  TreeView tv;
+  tv.start = tree->start;
+  tv.n = tree->n_nodes;
+  tv.words = tree->words;
+  tv.depth = reinterpret_cast<const int32_t*>(tb + tree->depth_off);
+  tv.mask = reinterpret_cast<const uint64_t*>(tb + tree->mask_off[window > 0 ? 1 : 0]);
+  if (it.ntok <= 2)
+    attn_item<1, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
+                       tv);
+  else
+    attn_item<2, true>(it, blockIdx.x, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks, out,
+                       tv);
 }
 
 // ---- chunked-prefill rows -------------------------------------------------------------------------
@@ -504,7 +525,7 @@ __device__ __forceinline__ void attn_prefill_body(
   const int ntw = max(0, min(4, it.ntok - 4 * wave));
   const int tok_w = it.tok + 4 * wave, pos_w = it.pos0 + 4 * wave;
   QRows<2> R;
-  rows_init<2, false>(R, q, tok_w, ntw, pos_w, it.kv_head, Hq, nullptr, nullptr);
+  rows_init<2, false>(R, q, tok_w, ntw, pos_w, it.kv_head, Hq, TreeView{});
   const int pos_last = pos_w + max(ntw, 1) - 1;
   const int lo_w = max(it.key_lo, window > 0 ? pos_w - window + 1 : 0);  // the wave's first visible key
   const int int_lo = max(it.key_lo, window > 0 ? pos_last - window + 1 : 0);
@@ -646,10 +667,10 @@ __global__ __launch_bounds__(64 * kPrefillWaves, LEAN ? 3 : 2) void attn_step_ke
   const flyai_attn_item it = items[idx];
   if (LEAN || it.ntok <= 2)
     attn_item<1, false, LEAN>(it, idx, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups,
-                              sinks, out, nullptr, nullptr);
+                              sinks, out, TreeView{});
   else
     attn_item<2, false>(it, idx, q, k_pool, v_pool, kv_base, kv_cap, window, Hq, partials, groups, n_groups, sinks,
-                        out, nullptr, nullptr);
+                        out, TreeView{});
 }
 
 int launch_attn_prefill(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
@@ -734,9 +755,13 @@ int launch_attn(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_poo
                 uint16_t* out, const flyai_attn_tree* tree, bool merge, hipStream_t s) {
   if (n_items == 0) return FLYAI_OK;
   (void)n_small;  // the plan's two ranges share one launch
-  hipLaunchKernelGGL(attn_partial_kernel, dim3(n_items), dim3(64), 0, s, q, k_pool, v_pool, kv_base,
-                     kv_cap, window, Hq, items, counts, partials, groups, n_groups, sinks, out, tree);
-  int rc = check_launch("attn_partial");
+  if (tree)  // launched directly with exact counts (never from a graph)
+    hipLaunchKernelGGL(attn_tree_kernel, dim3(n_items), dim3(64), 0, s, q, k_pool, v_pool, kv_base, kv_cap, window,
+                       Hq, items, partials, groups, n_groups, sinks, out, tree);
+  else
+    hipLaunchKernelGGL(attn_partial_kernel, dim3(n_items), dim3(64), 0, s, q, k_pool, v_pool, kv_base,
+                       kv_cap, window, Hq, items, counts, partials, groups, n_groups, sinks, out);
+  int rc = check_launch(tree ? "attn_tree" : "attn_partial");
   if (rc) return rc;
   if (!merge) return FLYAI_OK;  // every group has one split: the items wrote the output
   hipLaunchKernelGGL(attn_merge_kernel, dim3(n_groups), dim3(256), 0, s, partials, groups, sinks,
@@ -854,18 +879,17 @@ int attn_plan(const int32_t* q_lens, const int32_t* starts, int S, int Hkv, int 
   return FLYAI_OK;
 }
 
-// Tree-verify plan: the n nodes of one sequence (seq 0, tokens 0..n-1) in groups of <= 4
-// consecutive nodes; every group's keys run to start + n (the ancestor mask picks the tree slots),
+// Tree-verify plan: the n nodes of one sequence (seq 0, tokens 0..n-1) at committed length st, in
+// groups of <= 4 consecutive nodes; every group's keys run to st + n (the mask picks the tree slots),
 // and from the window start of its shallowest node on sliding layers.
-int attn_plan_tree(const flyai_attn_tree& tr, int Hkv, int window, int split_keys,
+int attn_plan_tree(int st, int n, const int32_t* depth, int Hkv, int window, int split_keys,
                    flyai_attn_item* items, int max_items, flyai_attn_group* groups, int max_groups,
                    int* n_items, int* n_groups, int* n_small) {
   int ni = 0, ng = 0;
-  const int n = tr.n_nodes, st = tr.start;
   for (int i0 = 0; i0 < n; i0 += 4) {
     const int nt = n - i0 < 4 ? n - i0 : 4;
-    int dmin = tr.depth[i0];
-    for (int i = 1; i < nt; ++i) dmin = tr.depth[i0 + i] < dmin ? tr.depth[i0 + i] : dmin;
+    int dmin = depth[i0];
+    for (int i = 1; i < nt; ++i) dmin = depth[i0 + i] < dmin ? depth[i0 + i] : dmin;
     const int p_first = st + dmin;
     const int key_hi = st + n;
     const int key_lo = window > 0 ? (p_first - window + 1 > 0 ? p_first - window + 1 : 0) : 0;

@@ -69,7 +69,7 @@ int launch_attn_prefill(const uint16_t*, const uint16_t*, const uint16_t*, const
 int launch_attn_step(const uint16_t*, const uint16_t*, const uint16_t*, const int64_t*, const int32_t*,
                      const float*, int, int, const flyai_attn_item*, int, const flyai_attn_group*, int,
                      const int32_t*, float*, const flyai_attn_item*, int, uint16_t*, bool, bool, hipStream_t);
-int attn_plan_tree(const flyai_attn_tree&, int, int, int, flyai_attn_item*, int, flyai_attn_group*, int,
+int attn_plan_tree(int, int, const int32_t*, int, int, int, flyai_attn_item*, int, flyai_attn_group*, int,
                    int*, int*, int*);
 int launch_pack(const int32_t*, const int32_t*, const int64_t*, const int32_t*, int, int, int, int32_t*,
                 int32_t*, int32_t*, int32_t*, int64_t*, int32_t*, const int32_t*, int32_t*, hipStream_t);
@@ -130,22 +130,42 @@ struct flyai_stage {
   uint64_t use_clock = 0;
   int graphs_captured = 0;
   std::vector<int> slab_order;  // host scratch of the slab-overlap check (max_seqs entries)
+  int tree_cap = 0;             // largest tree: min(max_tokens, FLYAI_TREE_MAX_NODES) nodes
+  std::vector<char> tree_img;   // host image of a tree step's flyai_attn_tree (header, depths, masks)
+  std::vector<int> tree_order;  // host scratch: the nodes in order of depth
 };
 static constexpr int kGraphCacheMax = 16;
 static constexpr int kPlanBucket = 64;  // attention plan capacities round up to this
 
-static size_t blob_bytes(int S, int n_items0, int n_items1, int n_groups0, int n_groups1, int n_pitems) {
+// Byte layout of a tree of n nodes as flyai_attn_tree describes it: the header, int32 depths, then the
+// two masks of n rows of (n + 63) / 64 words, each part at a 64-byte boundary.
+static size_t align64(size_t x) { return (x + 63) & ~(size_t)63; }
+static void tree_layout(int n, flyai_attn_tree* h) {
+  h->n_nodes = n;
+  h->words = (n + 63) / 64;
+  h->depth_off = (int32_t)align64(sizeof(flyai_attn_tree));
+  h->mask_off[0] = (int64_t)align64((size_t)h->depth_off + (size_t)n * 4);
+  h->mask_off[1] = h->mask_off[0] + (int64_t)align64((size_t)n * h->words * 8);
+}
+static size_t tree_bytes(int n) {
+  flyai_attn_tree h;
+  tree_layout(n, &h);
+  return (size_t)h.mask_off[1] + align64((size_t)n * h.words * 8);
+}
+
+static size_t blob_bytes(int S, int n_items0, int n_items1, int n_groups0, int n_groups1, int n_pitems,
+                         int tree_nodes) {
   return align256(4 * sizeof(int32_t)) + align256((size_t)S * 4) * 3 + align256((size_t)S * 8) +
          align256((size_t)n_items0 * sizeof(flyai_attn_item)) + align256((size_t)n_items1 * sizeof(flyai_attn_item)) +
          align256((size_t)n_groups0 * sizeof(flyai_attn_group)) + align256((size_t)n_groups1 * sizeof(flyai_attn_group)) +
-         2 * align256((size_t)n_pitems * sizeof(flyai_attn_item)) + align256(sizeof(flyai_attn_tree));
+         2 * align256((size_t)n_pitems * sizeof(flyai_attn_item)) + align256(tree_bytes(tree_nodes));
 }
 
 static void layout(flyai_stage* st) {
   const flyai_stage_config& c = st->cfg;
   const size_t S = c.max_seqs, T = c.max_tokens, P = (size_t)T * c.top_k;
   st->blob_max = blob_bytes(c.max_seqs, c.max_attn_items, c.max_attn_items, st->max_groups, st->max_groups,
-                            st->max_pitems);
+                            st->max_pitems, st->tree_cap);
   Carve d;
   st->o_blob = d.take(st->blob_max);
   st->o_cu = d.take((S + 1) * 4);
@@ -213,11 +233,13 @@ extern "C" int flyai_stage_create(const flyai_stage_config* cfg, flyai_stage** o
   st->qkv_width = (c.n_q_heads + 2 * c.n_kv_heads) * c.head_dim;
   st->max_groups = (c.max_seqs + (c.max_tokens + 3) / 4) * c.n_kv_heads;
   st->max_pitems = c.attn_prefill_min > 0 ? (c.max_seqs + (c.max_tokens + kPrefillTokens - 1) / kPrefillTokens) * c.n_kv_heads : 0;
+  st->tree_cap = std::min(c.max_tokens, FLYAI_TREE_MAX_NODES);
   st->layers = new (std::nothrow) flyai_layer_desc[c.n_layers];
   if (!st->layers) { delete st; return set_error(FLYAI_EINVAL, "stage_create: out of host memory"); }
   memset(st->layers, 0, sizeof(flyai_layer_desc) * c.n_layers);
   try {
     st->slab_order.resize(c.max_seqs);
+    st->tree_order.resize(2 * (size_t)st->tree_cap + 1);
     for (int i = 0; i < 2; ++i) {
       st->plan_items[i].resize(c.max_attn_items);
       st->plan_groups[i].resize(st->max_groups);
@@ -328,7 +350,7 @@ struct StepPlan {
   int lean[2];      // every split item has <= 2 tokens: the three-wave step kernel (part of the graph key)
   size_t off_counts, off_q, off_st, off_cap, off_base, off_items[2], off_groups[2], off_pitems[2];
   bool tree = false;  // a tree-verify step: the blob carries the flyai_attn_tree at off_tree
-  size_t off_tree = 0;
+  size_t off_tree = 0, off_tree_depth = 0;
 };
 }  // namespace
 
@@ -351,7 +373,8 @@ static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* count
                   reinterpret_cast<const int32_t*>(blob + sp.off_st), base_d, cap_d, sp.S, c.head_dim,
                   c.max_tokens, I32(st->o_cu), I32(st->o_pos), I32(st->o_sid), I32(st->o_kvlen),
                   reinterpret_cast<int64_t*>(d + st->o_slot), I32(st->o_status),
-                  tree_d ? tree_d->depth : nullptr, I32(st->o_kvpos), s));
+                  sp.tree ? reinterpret_cast<const int32_t*>(blob + sp.off_tree_depth) : nullptr,
+                  I32(st->o_kvpos), s));
   const int Tn = sp.Tn;
   const int H = c.hidden, E = c.n_experts, k = c.top_k, I = c.intermediate;
   const bool fused_route = Tn <= 256 && Tn * k <= 4096;
@@ -497,7 +520,7 @@ static int plan_needs_merge(const flyai_attn_group* groups, int n) {
 // [| tree], staged through the double-buffered pinned halves and copied with one H2D copy.
 static int stage_blob(flyai_stage* st, StepPlan& sp, const int32_t* q_lens, const int32_t* starts,
                       const int64_t* kv_base, const int32_t* kv_cap, const int* n_items,
-                      const int* n_groups, const flyai_attn_tree* tree, hipStream_t s) {
+                      const int* n_groups, const std::vector<char>* tree, hipStream_t s) {
   const int S = sp.S;
   Carve b;
   sp.off_counts = b.take(4 * sizeof(int32_t));
@@ -509,7 +532,10 @@ static int stage_blob(flyai_stage* st, StepPlan& sp, const int32_t* q_lens, cons
   for (int p = 0; p < 2; ++p) sp.off_groups[p] = b.take((size_t)sp.grid_groups[p] * sizeof(flyai_attn_group));
   for (int p = 0; p < 2; ++p) sp.off_pitems[p] = b.take((size_t)sp.n_pitems[p] * sizeof(flyai_attn_item));
   sp.tree = tree != nullptr;
-  if (tree) sp.off_tree = b.take(sizeof(flyai_attn_tree));
+  if (tree) {
+    sp.off_tree = b.take(tree->size());
+    sp.off_tree_depth = sp.off_tree + reinterpret_cast<const flyai_attn_tree*>(tree->data())->depth_off;
+  }
   if (b.off > st->blob_max) return set_error(FLYAI_ERANGE, "batch blob exceeds its reservation");
   // wait until the GPU consumed this staging half's previous contents, then fill it
   const int h = st->half;
@@ -528,7 +554,7 @@ static int stage_blob(flyai_stage* st, StepPlan& sp, const int32_t* q_lens, cons
     memcpy(hb + sp.off_groups[p], st->plan_groups[p].data(), n_groups[p] * sizeof(flyai_attn_group));
     memcpy(hb + sp.off_pitems[p], st->plan_pitems[p].data(), sp.n_pitems[p] * sizeof(flyai_attn_item));
   }
-  if (tree) memcpy(hb + sp.off_tree, tree, sizeof(flyai_attn_tree));
+  if (tree) memcpy(hb + sp.off_tree, tree->data(), tree->size());
   RUN(copy_h2d(st->dev + st->o_blob, hb, b.off, s));
   const hipError_t er = hipEventRecord(st->staged[h], s);
   if (er != hipSuccess) return hip_fail("hipEventRecord", er);
@@ -633,8 +659,8 @@ extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t 
                                         uint16_t* hidden, flyai_stream_t stream) {
   FLYAI_REQUIRE(st && parent && depth && hidden, "forward_tree: null pointer");
   const flyai_stage_config& c = st->cfg;
-  FLYAI_REQUIRE(n >= 1 && n <= 64, "forward_tree: tree size %d outside [1, 64]", n);
-  FLYAI_REQUIRE(n <= c.max_tokens, "forward_tree: %d nodes > max_tokens %d", n, c.max_tokens);
+  FLYAI_REQUIRE(n >= 1 && n <= st->tree_cap, "forward_tree: tree size %d outside [1, %d] (min(max_tokens, %d))", n,
+                st->tree_cap, FLYAI_TREE_MAX_NODES);
   FLYAI_REQUIRE(start >= 0 && kv_cap > 0 && kv_cap % 64 == 0 && kv_base >= 0 && kv_base % 8 == 0,
                 "forward_tree: needs start >= 0, kv_cap %% 64 == 0 and kv_base %% 8 == 0");
   // validate_tree (phase0/fastverify.py:29-49): parents in range and not self, depths consistent,
@@ -660,15 +686,45 @@ extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t 
   RUN(check_slabs(st, &kv_base, &kv_cap, 1));
   FLYAI_REQUIRE(st->dev && st->host, "forward_tree: workspace not set");
   FLYAI_REQUIRE(st->cos_tab && st->sin_tab, "forward_tree: rope tables not set");
-  flyai_attn_tree tree;
-  memset(&tree, 0, sizeof(tree));
-  tree.start = start;
-  tree.n_nodes = n;
-  for (int i = 0; i < n; ++i) {
-    tree.depth[i] = depth[i];
-    uint64_t a = 0;
-    for (int j = i; j != -1; j = parent[j]) a |= 1ull << j;  // ends: depth falls along the walk
-    tree.ancestors[i] = a;
+  // The two visibility masks (FastVerify._tset, phase0/fastverify.py:250-272): row i of mask 0 holds
+  // node i and its ancestors, row i of mask 1 those of them fewer than `window` levels above node i.
+  // Nodes are visited in order of depth (a counting sort), so a parent's rows are complete before
+  // its children copy them: row(i) = row(parent) + node i, and on sliding layers minus the one
+  // ancestor exactly `window` levels up.
+  try {
+    st->tree_img.assign(tree_bytes(n), 0);
+  } catch (...) {
+    return set_error(FLYAI_EINVAL, "forward_tree: out of host memory for the tree masks");
+  }
+  char* img = st->tree_img.data();
+  flyai_attn_tree* tr = reinterpret_cast<flyai_attn_tree*>(img);
+  tree_layout(n, tr);
+  tr->start = start;
+  const int W = tr->words;
+  memcpy(img + tr->depth_off, depth, (size_t)n * 4);
+  uint64_t* m0 = reinterpret_cast<uint64_t*>(img + tr->mask_off[0]);
+  uint64_t* m1 = reinterpret_cast<uint64_t*>(img + tr->mask_off[1]);
+  int* cnt = st->tree_order.data();  // n + 1 depth counters (depths are below n), then the order
+  int* order = cnt + n + 1;
+  std::fill(cnt, cnt + n + 1, 0);
+  for (int i = 0; i < n; ++i) ++cnt[depth[i] + 1];
+  for (int d = 0; d < n; ++d) cnt[d + 1] += cnt[d];
+  for (int i = 0; i < n; ++i) order[cnt[depth[i]]++] = i;
+  for (int k = 0; k < n; ++k) {
+    const int i = order[k], p = parent[i];
+    uint64_t* r0 = m0 + (size_t)i * W;
+    uint64_t* r1 = m1 + (size_t)i * W;
+    if (p >= 0) {
+      memcpy(r0, m0 + (size_t)p * W, (size_t)W * 8);
+      memcpy(r1, m1 + (size_t)p * W, (size_t)W * 8);
+    }
+    r0[i >> 6] |= 1ull << (i & 63);
+    r1[i >> 6] |= 1ull << (i & 63);
+    if (c.window > 0 && depth[i] >= c.window) {
+      int a = i;
+      for (int up = 0; up < c.window; ++up) a = parent[a];
+      r1[a >> 6] &= ~(1ull << (a & 63));
+    }
   }
   hipStream_t s = as_stream(stream);
   StepPlan sp;
@@ -676,7 +732,7 @@ extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t 
   sp.S = 1;
   int n_items[2], n_groups[2];
   for (int p = 0; p < 2; ++p) {
-    RUN(attn_plan_tree(tree, c.n_kv_heads, p == 0 ? 0 : c.window, c.attn_split_keys, st->plan_items[p].data(),
+    RUN(attn_plan_tree(start, n, depth, c.n_kv_heads, p == 0 ? 0 : c.window, c.attn_split_keys, st->plan_items[p].data(),
                        c.max_attn_items, st->plan_groups[p].data(), st->max_groups, &n_items[p],
                        &n_groups[p], &sp.n_small[p]));
     sp.grid_items[p] = n_items[p];
@@ -686,6 +742,6 @@ extern "C" int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t 
     sp.lean[p] = 0;
   }
   const int32_t q_len = n, st0 = start;
-  RUN(stage_blob(st, sp, &q_len, &st0, &kv_base, &kv_cap, n_items, n_groups, &tree, s));
+  RUN(stage_blob(st, sp, &q_len, &st0, &kv_base, &kv_cap, n_items, n_groups, &st->tree_img, s));
   return record_step(st, sp, nullptr, hidden, s);
 }

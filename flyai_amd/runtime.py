@@ -233,7 +233,7 @@ class RaggedStage:
         return self.workspace[off:off + n].view(dtype).view(*shape)
 
 
-TREE_MAX_NODES = 64  # ancestor sets are 64-bit masks in the tree attention kernel
+TREE_MAX_NODES = 2048  # FLYAI_TREE_MAX_NODES: the stage reserves the masks of a tree this large
 
 
 def validate_tree(M, par, dep):
@@ -303,14 +303,15 @@ class FastVerifyStage:
         """Verify a fixed-topology tree of M nodes in one pass (fastverify.py:281-299): node i at
         position start + dep[i], K/V at scratch slot start + i, attending the committed prefix and its
         ancestors.  Malformed trees raise ValueError and overflows ContextOverflow, both before any
-        write.  Trees are limited to 64 nodes (ValueError beyond)."""
+        write.  Trees are limited to min(max_tokens, 2048) nodes (ValueError beyond)."""
         M = h.shape[1]
         validate_tree(M, list(par), list(dep))
         if start + M > self.maxlen:
             raise ContextOverflow(_lib.FLYAI_ERANGE, f"tree decode needs {start + M} positions > max_ctx "
                                   f"{self.maxlen} (raise --max-ctx)")
-        if M > TREE_MAX_NODES:
-            raise ValueError(f"tree of {M} nodes exceeds the {TREE_MAX_NODES}-node limit")
+        limit = min(TREE_MAX_NODES, self.stage.max_tokens)
+        if M > limit:
+            raise ValueError(f"tree of {M} nodes exceeds the {limit}-node limit")
         self.stage.set_graphs(False)
         flat = h.reshape(M, self.hidden).to(torch.bfloat16).contiguous().clone()
         self.stage.forward_tree(flat, start, list(par), list(dep), 0)

@@ -423,14 +423,21 @@ int flyai_stage_forward(flyai_stage* st, const int32_t* q_lens_host, const int32
  * itself (sliding layers: depth[i] - depth[a] < window).  parent_host/depth_host follow
  * validate_tree (fastverify.py:29-49): parent[i] in [-1, n), parent[i] != i, depth[i] == 0 for a
  * root and depth[parent[i]] + 1 otherwise (which rules out cycles); FLYAI_EINVAL otherwise, and for
- * n_nodes outside [1, 64] (the ancestor sets are 64-bit masks).  start + n_nodes past kv_cap or the
+ * n_nodes outside [1, min(max_tokens, FLYAI_TREE_MAX_NODES)].  start + n_nodes past kv_cap or the
  * rope table, or a slab past the pools -> FLYAI_ERANGE before any launch.  Always launched directly
  * (no graph). */
+#define FLYAI_TREE_MAX_NODES 2048
+/* The tree as the attention kernel reads it (built by flyai_stage_forward_tree in the step's batch
+ * blob): this header, then int32 depth[n_nodes] and two visibility masks uint64 [n_nodes][words],
+ * one per layer kind; bit j of row i (word j / 64, bit j % 64) lets node i see tree slot start + j.
+ * Offsets are in bytes from the header. */
 typedef struct {
-  int32_t start;          /* committed length: node i's K/V sits at slot start + i */
-  int32_t n_nodes;        /* 1..64 */
-  int32_t depth[64];      /* node i is rotated at position start + depth[i] */
-  uint64_t ancestors[64]; /* bit a of ancestors[i]: node a is node i or one of its ancestors */
+  int32_t start;       /* committed length: node i's K/V sits at slot start + i */
+  int32_t n_nodes;     /* 1 .. min(max_tokens, FLYAI_TREE_MAX_NODES) */
+  int32_t words;       /* 64-bit words per mask row: (n_nodes + 63) / 64 */
+  int32_t depth_off;   /* int32 depth[n_nodes]: node i is rotated at position start + depth[i] */
+  int64_t mask_off[2]; /* [0] full-attention layers (ancestors and self), [1] sliding layers (those
+                          of them less than window levels above the node) */
 } flyai_attn_tree;
 
 int flyai_stage_forward_tree(flyai_stage* st, int32_t start, int32_t n_nodes,

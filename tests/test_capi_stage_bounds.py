@@ -89,6 +89,51 @@ def test_tree_slab_past_pool_is_erange(stage):
     assert rc == _lib.FLYAI_EINVAL and "workspace not set" in lib.flyai_last_error().decode()
 
 
+def _make_stage(max_tokens, cap):
+    lib = _lib.lib()
+    cfg = _lib.StageConfig(n_layers=2, hidden=2880, n_q_heads=64, n_kv_heads=HKV, head_dim=D, n_experts=128,
+                           top_k=4, intermediate=2880, window=128, max_tokens=max_tokens, max_seqs=1,
+                           max_attn_items=8192, rope_positions=8192, attn_split_keys=1024, rms_eps=1e-5,
+                           attn_prefill_min=32)
+    h = C.c_void_p()
+    assert lib.flyai_stage_create(C.byref(cfg), C.byref(h)) == 0, lib.flyai_last_error()
+    for l in range(2):
+        d = _lib.LayerDesc(**{f: 0x100000 for f in ("ln1", "ln2", "wqkv", "bqkv", "wo", "bo", "sinks", "router_w",
+                                                   "router_b", "w13_packed", "b13", "w2_packed", "b2", "k_pool",
+                                                   "v_pool")}, sliding=l % 2, pad=0, kv_pool_elems=HKV * cap * D)
+        assert lib.flyai_stage_set_layer(h, l, C.byref(d)) == 0, lib.flyai_last_error()
+    return lib, h
+
+
+def _tree(lib, h, start, par, cap):
+    par = np.ascontiguousarray(par, dtype=np.int32)
+    dep = np.zeros(len(par), dtype=np.int32)
+    for i, p in enumerate(par):  # parents precede children in these trees
+        dep[i] = 0 if p < 0 else dep[p] + 1
+    rc = lib.flyai_stage_forward_tree(h, start, len(par), par.ctypes.data_as(C.c_void_p),
+                                      dep.ctypes.data_as(C.c_void_p), 0, cap, C.c_void_p(0x200000), None)
+    return rc, lib.flyai_last_error().decode()
+
+
+@pytest.mark.parametrize("max_tokens,limit", [(64, 64), (300, 300), (4096, 2048)])
+def test_tree_size_limit_is_min_of_max_tokens_and_2048(max_tokens, limit):
+    """Trees of up to min(max_tokens, FLYAI_TREE_MAX_NODES = 2048) nodes pass validation (and stop at
+    the first check that needs the device); one node more is FLYAI_EINVAL before any launch."""
+    cap = 4096
+    lib, h = _make_stage(max_tokens, cap)
+    try:
+        rng = np.random.default_rng(limit)
+        wide = [-1] + [int(rng.integers(0, i)) for i in range(1, limit)]
+        chain = [-1] + list(range(limit - 1))  # depth limit - 1, past the 128-key window
+        for par in (wide, chain):
+            rc, msg = _tree(lib, h, 100, par, cap)
+            assert rc == _lib.FLYAI_EINVAL and "workspace not set" in msg, msg
+        rc, msg = _tree(lib, h, 100, chain + [limit - 1], cap)
+        assert rc == _lib.FLYAI_EINVAL and f"outside [1, {limit}]" in msg, msg
+    finally:
+        lib.flyai_stage_destroy(h)
+
+
 def test_pool_size_is_required(stage):
     lib, h = stage
     d = _lib.LayerDesc(**{f: 0x100000 for f in ("ln1", "ln2", "wqkv", "bqkv", "wo", "bo", "sinks", "router_w",

@@ -20,6 +20,15 @@ def _random_tree(rng, M):
     return par, dep
 
 
+def _deep_tree(rng, M, chain):
+    """A chain of `chain` nodes (depths past the 128-key sliding window), then random branches."""
+    par = [-1] + list(range(chain - 1)) + [int(rng.integers(0, i)) for i in range(chain, M)]
+    dep = [0] * M
+    for i in range(1, M):
+        dep[i] = dep[par[i]] + 1
+    return par, dep
+
+
 TREES = {
     "tree8": ([-1, 0, 1, 2, 0, 4, 1, 6], [0, 1, 2, 3, 1, 2, 2, 3]),
     "root_not_first": ([1, -1, 1, 0, 3], [1, 0, 1, 2, 3]),
@@ -27,20 +36,27 @@ TREES = {
 
 
 @pytest.mark.parametrize("name,start,M", [("tree8", 300, 8), ("root_not_first", 64, 5), ("random40", 1000, 40),
-                                          ("random64", 130, 64)])
+                                          ("random64", 130, 64), ("random150", 64, 150), ("deep200", 1000, 200)])
 def test_tree_decode_per_layer_vs_oracle(name, start, M):
     """Two layers (sliding, then full) from the GPU's own per-layer input: attention output and the
-    K/V at slots start..start+M-1 against the oracle, and the layer output within the bar."""
+    K/V at slots start..start+M-1 against the oracle, and the layer output within the bar.  Trees
+    past 64 nodes take several mask words per node (starts 64 and 1000: word-aligned and shifted
+    key blocks); deep200's chain of 160 reaches past the sliding window inside the tree."""
     print(f"tree case {name} start={start} M={M}", flush=True)
     rng = np.random.default_rng(M)
-    par, dep = TREES[name] if name in TREES else _random_tree(rng, M)
+    if name in TREES:
+        par, dep = TREES[name]
+    elif name.startswith("deep"):
+        par, dep = _deep_tree(rng, M, 160)
+    else:
+        par, dep = _random_tree(rng, M)
     case = gh.small_stage_case(n_layers=2, n_experts=8, seed=3, q_lens=(M,), starts=(start,))
     shape, layers, kv = case["shape"], case["layers"], case["kv"]
     cos, sin = olayer.rope_table(case["maxlen"])
     h = case["hidden"].clone()
     for l, lw in enumerate(layers):
         okv = gh.oracle_kv(kv, l, [0])
-        st = RaggedStage(shape, [lw], case["rot"], gh._SingleLayerKV(kv, l), max_tokens=64, max_seqs=1)
+        st = RaggedStage(shape, [lw], case["rot"], gh._SingleLayerKV(kv, l), max_tokens=max(64, M), max_seqs=1)
         hin = gh.cpu_f32(h)
         h = st.forward_tree(h.clone(), start, par, dep, 0)
         torch.cuda.synchronize()
@@ -72,14 +88,17 @@ def test_tree_decode_per_layer_vs_oracle(name, start, M):
         del st
 
 
-def test_chain_tree_equals_linear_verify_bit_exact():
+@pytest.mark.parametrize("M", [6, 150])
+def test_chain_tree_equals_linear_verify_bit_exact(M):
     """A chain (par[i] = i-1, dep[i] = i) is a plain verify row: same hidden and KV bytes as the
-    ragged step with q_len M at the same start."""
-    M, start = 6, 517
+    ragged step with q_len M at the same start (decode-sized attention items on both paths; at 150
+    nodes the chain runs past the sliding window and over three mask words per node)."""
+    start = 517
+    print(f"chain tree M={M} start={start}", flush=True)
     par, dep = [-1] + list(range(M - 1)), list(range(M))
     case = gh.small_stage_case(n_layers=2, n_experts=8, seed=5, q_lens=(M,), starts=(start,))
     shape, layers, kv = case["shape"], case["layers"], case["kv"]
-    st = RaggedStage(shape, layers, case["rot"], kv, max_tokens=64, max_seqs=1)
+    st = RaggedStage(shape, layers, case["rot"], kv, max_tokens=max(64, M), max_seqs=1, prefill_min=0)
     k0 = [t.clone() for t in kv.k]
     v0 = [t.clone() for t in kv.v]
     lin = st.forward(case["hidden"].clone(), [M], [start], [0])

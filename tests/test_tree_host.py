@@ -105,8 +105,11 @@ def test_tree_decode_context_overflow(start, maxlen, overflows):
             FastVerifyStage.tree_decode(stub, h, start, [-1, 0, 1], [0, 1, 2])
 
 
-def test_tree_decode_node_limit():
-    n = 65
+@pytest.mark.parametrize("max_tokens,limit", [(100, 100), (4096, 2048)])
+def test_tree_decode_node_limit(max_tokens, limit):
+    """Trees are limited to min(max_tokens, 2048) nodes: one more is ValueError before any write."""
+    stub = SimpleNamespace(maxlen=8192, stage=SimpleNamespace(max_tokens=max_tokens))
+    n = limit + 1
     chain_par, chain_dep = [-1] + list(range(n - 1)), list(range(n))
-    with pytest.raises(ValueError, match="64-node"):
-        FastVerifyStage.tree_decode(_guards_only(4096), torch.zeros(1, n, 8), 0, chain_par, chain_dep)
+    with pytest.raises(ValueError, match=f"{limit}-node"):
+        FastVerifyStage.tree_decode(stub, torch.zeros(1, n, 8), 0, chain_par, chain_dep)

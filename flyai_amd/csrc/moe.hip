@@ -77,6 +77,17 @@ __global__ __launch_bounds__(256) void mxfp4_repack_kernel(const uint8_t* __rest
 // passes over the weights.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
+// Buffer resource word 3 for raw (unformatted, unswizzled) loads on gfx9, and an offset past any
+// resource this file builds (such a load returns zero and touches no memory).
+constexpr int kBufRsrcWord3 = 0x00020000;
+constexpr uint32_t kBufOutside = 0x80000000u;
+
+// 16 bytes through a buffer resource, nontemporal
+__device__ __forceinline__ uint4 buf_ld16_nt(__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 2);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ uint4 ld_nt(const uint8_t* p) {
   const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -145,22 +156,31 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
   const bool k_pow2 = (k_top & (k_top - 1)) == 0;  // slot -> token by a shift (the routers' k: 2, 4, 8)
   const int k_shift = __builtin_ctz((unsigned)k_top);
 
-  const uint8_t* data = packed + ((size_t)e * gm.NT + nt0) * gm.G * 256 + lane * 16;
-  const uint32_t* scl = reinterpret_cast<const uint32_t*>(
-                            packed + gm.data_bytes + ((size_t)e * gm.NT + nt0) * gm.KG4 * 256) + lane;
-  const size_t tile_stride = (size_t)gm.G * 256;
-  const size_t scale_stride = (size_t)gm.KG4 * 64;
+  // The wave's weight tiles and scale dwords through buffer resources: a load outside the valid
+  // range (the last ring body's groups past KG, a block past the row's end, a tile past the
+  // expert's last) gets an offset past the resource and reads zero with no memory access.  The
+  // loads are therefore unconditional: no branch separates a load from the ring, so the compiler's
+  // waits count the ring exactly (with the loads under branches it drained the ring at every body).
+  const int tile_stride = gm.G * 256;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(packed + ((size_t)e * gm.NT + nt0) * tile_stride), (short)0, ntw * tile_stride,
+      kBufRsrcWord3);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(packed + gm.data_bytes + ((size_t)e * gm.NT + nt0) * gm.KG4 * 256), (short)0,
+      ntw * gm.KG4 * 256, kBufRsrcWord3);
   const char* lds = reinterpret_cast<const char*>(xs_lds);
 
   auto load_w = [&](uint4 (&w)[NTW], int kg) {
     const bool bvalid = kg < gm.KG && 4 * kg + g < gm.G;
 #pragma unroll
     for (int n = 0; n < NTW; ++n)
-      w[n] = (bvalid && n < ntw) ? ld_nt(data + n * tile_stride + (size_t)kg * 1024) : make_uint4(0, 0, 0, 0);
+      w[n] = buf_ld16_nt(wrs, bvalid ? (uint32_t)(n * tile_stride + kg * 1024 + lane * 16) : kBufOutside);
   };
   auto load_sc = [&](uint32_t (&sc)[NTW], int kg4) {
 #pragma unroll
-    for (int n = 0; n < NTW; ++n) sc[n] = (kg4 < gm.KG4 && n < ntw) ? scl[n * scale_stride + kg4 * 64] : 0u;
+    for (int n = 0; n < NTW; ++n)
+      sc[n] = __builtin_amdgcn_raw_buffer_load_b32(
+          srs, kg4 < gm.KG4 ? (uint32_t)(n * gm.KG4 * 256 + kg4 * 256 + lane * 4) : kBufOutside, 0, 0);
   };
   // Static bodies of DEPTH groups: a DEPTH-deep weight ring (DEPTH - 1 groups in flight while one
   // computes) and the next body's scale dwords loaded one body ahead, so no wait drains the ring.
@@ -168,6 +188,9 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
   constexpr int kSc = DEPTH / 4;
   uint4 w[DEPTH][NTW];
   uint32_t sc_cur[kSc][NTW], sc_nxt[kSc][NTW];
+  // The tiles' bias, loaded with the first pass's staging: requested ahead of the weight ring, so the
+  // epilogue does not pay a global round trip of its own.
+  float bias_r[NTW];
 
   for (int m0 = 0; m0 < n_e; m0 += kRowsPerPass) {
     const int rows = min(kRowsPerPass, n_e - m0);
@@ -203,6 +226,10 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
           cv -= row_vecs;
           ++cr;
         }
+      }
+      if (m0 == 0 && b0 == 0) {
+#pragma unroll
+        for (int n = 0; n < NTW; ++n) bias_r[n] = n < ntw ? bias[(size_t)e * N + (nt0 + n) * 16 + r] : 0.f;
       }
       if (b0 == 0) {
         mx_static_for<0, kSc>([&](auto q) { load_sc(sc_cur[q], q); });
@@ -255,7 +282,7 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
     for (int n = 0; n < NTW; ++n) {
       const int feat = (nt0 + n) * 16 + r;
       const bool nval = n < ntw;
-      const float bsum = nval ? bias[(size_t)e * N + feat] : 0.f;
+      const float bsum = bias_r[n];
       if (GATE_UP) {
         const float val[4] = {acc[n][0] + bsum, acc[n][1] + bsum, acc[n][2] + bsum, acc[n][3] + bsum};
         swiglu_pairs(val, r, [&](int v, uint16_t hbits) {

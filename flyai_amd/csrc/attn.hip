@@ -158,6 +158,7 @@ __device__ __forceinline__ float max_lane_groups(float v) {
 // between moves; a wave rescales O and L only when one of its rows moved (alpha = 1 exactly for the
 // others, so skipping is exact and a row's result does not depend on its wave mates).
 constexpr float kMaxSlack = 8.f;
+constexpr float kMaxSentinel = -1e29f;  // a running max at or below this is the initial -1e30 (no key yet)
 
 template <int QT, bool TREE>
 __device__ __forceinline__ void rows_block(QRows<QT>& R, const uint4 (&kc)[4][2], uint4 (&vv)[4][2], int kb,
@@ -268,22 +269,27 @@ __device__ __forceinline__ void prefill_rows_block(QRows<2>& R, const uint4* __r
                                                    int key_hi, int window) {
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4;
-  const float scale = 0.125f * kLog2e;
   const bf16x8_t ones = as_bf16x8(make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
+  // The queries are pre-scaled by head_dim^-0.5 log2(e) (attn_prefill_body), and each row's score
+  // MFMAs start from -m (its running max), so they produce s * scale - m directly and P = 2^(score)
+  // needs no FMA.  A row still at the sentinel max (no key seen yet) starts from 0 instead.
   f32x4_t s[2][4];
+  float c0[2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) c0[qt] = R.m_run[qt] > kMaxSentinel ? -R.m_run[qt] : 0.f;
 #pragma unroll
   for (int kt = 0; kt < 4; ++kt) {
     const uint4 k0 = kbuf[kt * 128 + lane], k1 = kbuf[kt * 128 + 64 + lane];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      s[qt][kt] = mfma16x16x32(as_bf16x8(k0), R.qf[qt][0], f32x4_t{0.f, 0.f, 0.f, 0.f});
+      s[qt][kt] = mfma16x16x32(as_bf16x8(k0), R.qf[qt][0], f32x4_t{c0[qt], c0[qt], c0[qt], c0[qt]});
       s[qt][kt] = mfma16x16x32(as_bf16x8(k1), R.qf[qt][1], s[qt][kt]);
     }
   }
   bf16x8_t pt[2][2];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt) {
-    // lane holds S^T[key kb + tile_key(kt, 4g + v)][qrow n]
+    // lane holds S^T[key kb + tile_key(kt, 4g + v)][qrow n], relative to the row's running max
     float bmax = -INFINITY;
     if constexpr (!MASKED) {
 #pragma unroll
@@ -305,22 +311,28 @@ __device__ __forceinline__ void prefill_rows_block(QRows<2>& R, const uint4* __r
         }
     }
     bmax = max_lane_groups(bmax);
-    const float m_blk = bmax * scale;
-    const bool move = m_blk > R.m_run[qt] + kMaxSlack;
+    // the max moves when the block's exceeds it by more than kMaxSlack; a row at the sentinel takes
+    // the block's max as soon as it sees a key (a block fully masked for it leaves it at the sentinel)
+    const bool fresh = R.m_run[qt] <= kMaxSentinel;
+    const bool move = bmax > (fresh ? -INFINITY : kMaxSlack);
     if (__ballot(move)) {
-      const float m_new = move ? m_blk : R.m_run[qt];
-      const float alpha = __builtin_amdgcn_exp2f(R.m_run[qt] - m_new);
-      R.m_run[qt] = m_new;
+      const float delta = move ? bmax : 0.f;  // scores are relative to the old max: shift by delta
+      const float m_new = (fresh ? 0.f : R.m_run[qt]) + delta;
+      const float alpha = move ? __builtin_amdgcn_exp2f(R.m_run[qt] - m_new) : 1.f;
+      R.m_run[qt] = move ? m_new : R.m_run[qt];
       R.L[qt] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) R.O[qt][dt] *= alpha;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s[qt][kt][v] -= delta;
     }
-    const float neg_m = -R.m_run[qt];
+    // P rounded to bf16 (the PV operand; the row sum uses the same rounded values)
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int v = 0; v < 4; ++v)
-        pt[qt][kt >> 1][(kt & 1) * 4 + v] = (__bf16)__builtin_amdgcn_exp2f(fmaf(s[qt][kt][v], scale, neg_m));
+      for (int v = 0; v < 4; ++v) pt[qt][kt >> 1][(kt & 1) * 4 + v] = (__bf16)__builtin_amdgcn_exp2f(s[qt][kt][v]);
     R.L[qt] = mfma16x16x32(ones, pt[qt][0], R.L[qt]);
     R.L[qt] = mfma16x16x32(ones, pt[qt][1], R.L[qt]);
   }
@@ -526,6 +538,13 @@ __device__ __forceinline__ void attn_prefill_body(
   const int tok_w = it.tok + 4 * wave, pos_w = it.pos0 + 4 * wave;
   QRows<2> R;
   rows_init<2, false>(R, q, tok_w, ntw, pos_w, it.kv_head, Hq, TreeView{});
+  // the queries pre-scaled by head_dim^-0.5 log2(e), rounded to bf16 (prefill_rows_block's scores)
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) R.qf[qt][hh][i] = (__bf16)((float)R.qf[qt][hh][i] * (0.125f * kLog2e));
   const int pos_last = pos_w + max(ntw, 1) - 1;
   const int lo_w = max(it.key_lo, window > 0 ? pos_w - window + 1 : 0);  // the wave's first visible key
   const int int_lo = max(it.key_lo, window > 0 ? pos_last - window + 1 : 0);

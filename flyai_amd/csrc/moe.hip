@@ -349,8 +349,9 @@ constexpr int kDepthDown = 8;
 // Loads are unconditional with clamped addresses: rows past the group read row 0 and are never
 // stored; weight lanes past a row's last block (and the padding groups) are zeroed before
 // conversion, their activation slots read the row's first group (finite values); tiles past N
-// compute on a clamped tile and are never stored; the 3 groups issued past the chunk's end read
-// clamped addresses and are never computed on.
+// load a clamped tile whose codes are zeroed before conversion (MFMAs on zero operands draw less
+// power: down at 128 experts x 65 rows 194-195 -> 192 us) and are never stored; the 3 groups issued
+// past the chunk's end read clamped addresses and are never computed on.
 constexpr int kGemmTiles = 16;                       // packed 16-row weight tiles per block
 constexpr int kGemmRows = 96;                        // group rows per pass
 constexpr int kGemmStage = kGemmRows * 256 + kGemmTiles * 256;  // activations + scale dwords
@@ -548,14 +549,17 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
   bf16x8_t a0[MT], a1[MT], b0[2], b1[2];
   u32x4 w0[2], w1[2], w2[2], w3[2];
   float scale[2];
-  bool bok = false;
+  bool bok[2] = {false, false};
+  int live_n = 2;  // this wave's tiles of the current block that lie inside the expert
   auto read_scales = [&](const char* stage, int kg) __attribute__((always_inline)) {
 #pragma unroll
     for (int n = 0; n < 2; ++n) {
       const uint32_t sw = *reinterpret_cast<const uint32_t*>(stage + sfrag_off + n * 256);
       scale[n] = e8m0_operand((sw >> (8 * (kg & 3))) & 0xffu);
     }
-    bok = 4 * kg + g < gm.G;  // the lane's weight block exists
+    // the lane's weight block exists and its tile lies inside the expert
+#pragma unroll
+    for (int n = 0; n < 2; ++n) bok[n] = 4 * kg + g < gm.G && n < live_n;
   };
   auto read_a = [&](bf16x8_t (&a)[MT], const char* stage, auto j) __attribute__((always_inline)) {
     const int fo = afrag ^ (int(j) << 4);
@@ -564,7 +568,7 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
   };
   auto cvt = [&](bf16x8_t (&b)[2], const u32x4 (&bq)[2], auto j) __attribute__((always_inline)) {
 #pragma unroll
-    for (int n = 0; n < 2; ++n) b[n] = fp4x8_to_bf16x8(bok ? bq[n][int(j)] : 0u, scale[n]);
+    for (int n = 0; n < 2; ++n) b[n] = fp4x8_to_bf16x8(bok[n] ? bq[n][int(j)] : 0u, scale[n]);
   };
   auto mfma_step = [&](const bf16x8_t (&a)[MT], const bf16x8_t (&b)[2]) __attribute__((always_inline)) {
 #pragma unroll
@@ -676,6 +680,7 @@ __device__ __forceinline__ void gemm_pass(const GemmCtx& c, char (&st0)[kGemmSta
     // the block's first operands (stage 0 stays valid until the first group's barrier); taken here
     // rather than carried through the previous block's epilogue, to keep that epilogue's register
     // pressure low: a spill would add vector-memory operations the stage waits do not count
+    live_n = max(0, min(2, gm.NT - ((c.nb0 + nb) * kGemmTiles + 2 * wave)));
     read_scales(st0, 0);
     read_a(a0, st0, std::integral_constant<int, 0>{});
     cvt(b0, w0, std::integral_constant<int, 0>{});

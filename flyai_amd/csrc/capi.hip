@@ -73,6 +73,7 @@ int attn_plan_tree(int, int, const int32_t*, int, int, int, flyai_attn_item*, in
                    int*, int*, int*);
 int launch_pack(const int32_t*, const int32_t*, const int64_t*, const int32_t*, int, int, int, int32_t*,
                 int32_t*, int32_t*, int32_t*, int64_t*, int32_t*, const int32_t*, int32_t*, hipStream_t);
+int launch_blob_fetch(const char*, char*, size_t, hipStream_t);
 
 }  // namespace flyai
 
@@ -99,7 +100,7 @@ struct flyai_stage {
   flyai_layer_desc* layers = nullptr;
   const uint16_t* cos_tab = nullptr;
   const uint16_t* sin_tab = nullptr;
-  // device workspace offsets; o_blob holds the per-step batch blob copied from the host
+  // device workspace offsets; o_blob holds the per-step batch blob moved from the host staging
   size_t o_blob, blob_max, o_cu, o_pos, o_sid, o_kvlen, o_slot, o_status, o_kvpos;
   size_t o_xn, o_gemm, o_qrot, o_attn, o_parts;
   size_t o_ids, o_w, o_logits, o_hist, o_off, o_perm, o_inv, o_hmoe, o_y;
@@ -113,6 +114,9 @@ struct flyai_stage {
   std::vector<flyai_attn_item> plan_pitems[2];
   char* dev = nullptr;
   char* host = nullptr;
+  // the staging's address in the device's address space (mapped pinned memory): the blob is then
+  // fetched by a kernel; null: the staging is not mapped, and an H2D copy moves it
+  const char* host_dev = nullptr;
   hipEvent_t staged[2] = {nullptr, nullptr};
   int half = 0;
   bool events_ready = false;
@@ -307,6 +311,13 @@ extern "C" int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t d
   drop_graphs(st);
   st->dev = static_cast<char*>(dev_ws);
   st->host = static_cast<char*>(host_pinned);
+  void* mapped = nullptr;
+  if (hipHostGetDevicePointer(&mapped, host_pinned, 0) == hipSuccess && mapped) {
+    st->host_dev = static_cast<const char*>(mapped);
+  } else {
+    st->host_dev = nullptr;
+    (void)hipGetLastError();  // not mapped: the H2D copy path, and no error left behind
+  }
   if (!st->events_ready) {
     for (int i = 0; i < 2; ++i) {
       const hipError_t e = hipEventCreateWithFlags(&st->staged[i], hipEventDisableTiming);
@@ -517,7 +528,8 @@ static int plan_needs_merge(const flyai_attn_group* groups, int n) {
 }
 
 // One compact blob per step: live counts | q_lens | starts | kv_cap | kv_base | items x2 | groups x2
-// [| tree], staged through the double-buffered pinned halves and copied with one H2D copy.
+// [| tree], staged through the double-buffered pinned halves and moved to the device by one
+// launch (blob_fetch_kernel; an H2D copy if the staging is not mapped).
 static int stage_blob(flyai_stage* st, StepPlan& sp, const int32_t* q_lens, const int32_t* starts,
                       const int64_t* kv_base, const int32_t* kv_cap, const int* n_items,
                       const int* n_groups, const std::vector<char>* tree, hipStream_t s) {
@@ -555,7 +567,10 @@ static int stage_blob(flyai_stage* st, StepPlan& sp, const int32_t* q_lens, cons
     memcpy(hb + sp.off_pitems[p], st->plan_pitems[p].data(), sp.n_pitems[p] * sizeof(flyai_attn_item));
   }
   if (tree) memcpy(hb + sp.off_tree, tree->data(), tree->size());
-  RUN(copy_h2d(st->dev + st->o_blob, hb, b.off, s));
+  if (st->host_dev)
+    RUN(launch_blob_fetch(st->host_dev + h * st->host_half, st->dev + st->o_blob, b.off, s));
+  else
+    RUN(copy_h2d(st->dev + st->o_blob, hb, b.off, s));
   const hipError_t er = hipEventRecord(st->staged[h], s);
   if (er != hipSuccess) return hip_fail("hipEventRecord", er);
   return FLYAI_OK;

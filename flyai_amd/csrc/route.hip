@@ -14,15 +14,26 @@ namespace flyai {
 // weight row and one 16-byte LDS read of x per chunk -- then a xor butterfly (as a reduce-scatter
 // over the wave's EPW x TT sums, wave_sum_scatter).  All JMAX weight
 // chunks of the wave's experts are loaded before the first FMA (one memory round trip).
-template <int TT, int EPW, int JMAX, bool ROUND_BF16>
+// XCD_GROUPED (a 1-D grid): the expert groups of one token group run one after another on one XCD
+// (workgroups are dealt to the 8 XCDs round-robin by index), so that XCD's L2 serves their x rows
+// after the first; with the 2-D grid they landed on different XCDs and each read x from HBM.
+template <int TT, int EPW, int JMAX, bool ROUND_BF16, bool XCD_GROUPED = false>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, const uint16_t* __restrict__ b,
     int T, int H, int E, float* __restrict__ logits) {
   extern __shared__ uint16_t xs[];  // [TT][H]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int t0 = blockIdx.x * TT;
+  int tg = blockIdx.x, eg = blockIdx.y;
+  if (XCD_GROUPED) {
+    const int neg = (E + 4 * EPW - 1) / (4 * EPW);
+    const int r = (int)blockIdx.x / 8;
+    eg = r % neg;
+    tg = (r / neg) * 8 + (int)blockIdx.x % 8;
+    if (tg * TT >= T) return;  // uniform over the workgroup
+  }
+  const int t0 = tg * TT;
   const int nt = min(TT, T - t0);
-  const int e0 = blockIdx.y * 4 * EPW + wave * EPW;
+  const int e0 = eg * 4 * EPW + wave * EPW;
   uint4 wv[EPW][JMAX];
 #pragma unroll
   for (int c = 0; c < EPW; ++c)
@@ -147,8 +158,9 @@ __global__ __launch_bounds__(256) void router_topk4_kernel(const float* __restri
 int launch_router_logits(const uint16_t* x, const uint16_t* w, const uint16_t* b, int T, int H,
                          int E, float* logits, hipStream_t s) {
   if (H <= 3072 && T >= 256) {  // prefill-sized: 16 experts per workgroup halve the x re-reads
-    hipLaunchKernelGGL((router_logits_kernel<8, 4, 6, true>), dim3(ceil_div(T, 8), ceil_div(E, 16)),
-                       dim3(256), 8 * H * sizeof(uint16_t), s, x, w, b, T, H, E, logits);
+    const int ntg8 = ceil_div(ceil_div(T, 8), 8) * 8;  // token groups, rounded to the 8 XCDs
+    hipLaunchKernelGGL((router_logits_kernel<8, 4, 6, true, true>), dim3(ntg8 * ceil_div(E, 16)), dim3(256),
+                       8 * H * sizeof(uint16_t), s, x, w, b, T, H, E, logits);
   } else if (H <= 3072) {  // 8 staged rows stay under 48 KiB of LDS; 6 chunks of 512
     hipLaunchKernelGGL((router_logits_kernel<8, 2, 6, true>), dim3(ceil_div(T, 8), ceil_div(E, 8)),
                        dim3(256), 8 * H * sizeof(uint16_t), s, x, w, b, T, H, E, logits);

@@ -403,7 +403,10 @@ int flyai_stage_set_layer(flyai_stage* st, int32_t layer, const flyai_layer_desc
 int flyai_stage_set_rope(flyai_stage* st, const uint16_t* cos_tab, const uint16_t* sin_tab);
 size_t flyai_stage_workspace_bytes(const flyai_stage* st);
 size_t flyai_stage_host_staging_bytes(const flyai_stage* st);
-/* device workspace (>= workspace_bytes) and pinned host staging (>= host_staging_bytes) */
+/* device workspace (>= workspace_bytes) and pinned host staging (>= host_staging_bytes).  Each step's
+ * batch blob goes through one half of the staging; when the staging is mapped into the device's
+ * address space (hipHostMalloc / pinned torch memory) a kernel reads it there, otherwise an H2D copy
+ * moves it. */
 int flyai_stage_set_workspace(flyai_stage* st, void* dev_ws, size_t dev_bytes, void* host_pinned,
                               size_t host_bytes);
 /* One step.  Batch description on the host (validated here; ContextOverflow -> FLYAI_ERANGE before

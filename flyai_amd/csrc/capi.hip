@@ -72,7 +72,8 @@ int launch_attn_step(const uint16_t*, const uint16_t*, const uint16_t*, const in
 int attn_plan_tree(int, int, const int32_t*, int, int, int, flyai_attn_item*, int, flyai_attn_group*, int,
                    int*, int*, int*);
 int launch_pack(const int32_t*, const int32_t*, const int64_t*, const int32_t*, int, int, int, int32_t*,
-                int32_t*, int32_t*, int32_t*, int64_t*, int32_t*, const int32_t*, int32_t*, hipStream_t);
+                int32_t*, int32_t*, int32_t*, int64_t*, int32_t*, const int32_t*, int32_t*, hipStream_t, int,
+                const uint16_t*, const float*, int, float, uint16_t*);
 int launch_blob_fetch(const char*, char*, size_t, hipStream_t);
 
 }  // namespace flyai
@@ -380,16 +381,16 @@ static int record_step(flyai_stage* st, const StepPlan& sp, const int32_t* count
   const flyai_attn_tree* tree_d = sp.tree ? reinterpret_cast<const flyai_attn_tree*>(blob + sp.off_tree) : nullptr;
   const int32_t* kv_pos = sp.tree ? I32(st->o_kvpos) : nullptr;
 
+  const int Tn = sp.Tn;
+  const int H = c.hidden, E = c.n_experts, k = c.top_k, I = c.intermediate;
+  const bool fused_route = Tn <= 256 && Tn * k <= 4096;
+  // the batch packing and the first layer's input RMSNorm in one launch (independent of each other)
   RUN(launch_pack(reinterpret_cast<const int32_t*>(blob + sp.off_q),
                   reinterpret_cast<const int32_t*>(blob + sp.off_st), base_d, cap_d, sp.S, c.head_dim,
                   c.max_tokens, I32(st->o_cu), I32(st->o_pos), I32(st->o_sid), I32(st->o_kvlen),
                   reinterpret_cast<int64_t*>(d + st->o_slot), I32(st->o_status),
                   sp.tree ? reinterpret_cast<const int32_t*>(blob + sp.off_tree_depth) : nullptr,
-                  I32(st->o_kvpos), s));
-  const int Tn = sp.Tn;
-  const int H = c.hidden, E = c.n_experts, k = c.top_k, I = c.intermediate;
-  const bool fused_route = Tn <= 256 && Tn * k <= 4096;
-  RUN(launch_rmsnorm(hidden, st->layers[0].ln1, Tn, H, c.rms_eps, B16(st->o_xn), s));
+                  I32(st->o_kvpos), s, Tn, hidden, st->layers[0].ln1, H, c.rms_eps, B16(st->o_xn)));
   for (int l = 0; l < c.n_layers; ++l) {
     const flyai_layer_desc& L = st->layers[l];
     const int p = L.sliding ? 1 : 0;

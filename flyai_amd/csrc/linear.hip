@@ -7,36 +7,11 @@
 namespace flyai {
 
 // ---- RMSNorm: y = bf16(w * (x * rsqrt(mean(x^2) + eps))), fp32 weight --------------------------
-constexpr int kRowThreads = 1024;  // one workgroup per token row: ~3 elements per thread at H = 2880
-
-__device__ __forceinline__ float block_sum_1024(float v, float* red) {
-  v = warp_sum(v);
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int w = 0; w < kRowThreads / 64; ++w) s += red[w];
-  return s;
-}
-
+// (kRowThreads, block_sum_1024 and rmsnorm_row: common.h)
 __global__ __launch_bounds__(kRowThreads) void rmsnorm_kernel(const uint16_t* __restrict__ x,
                                                               const float* __restrict__ w, int H,
                                                               float eps, uint16_t* __restrict__ y) {
-  __shared__ float red[kRowThreads / 64];
-  const int t = blockIdx.x, tid = threadIdx.x;
-  const uint16_t* xr = x + (size_t)t * H;
-  float ss = 0.f;
-  for (int i = tid; i < H; i += kRowThreads) {
-    const float v = bf2f(xr[i]);
-    ss = fmaf(v, v, ss);
-  }
-  const float total = block_sum_1024(ss, red);
-  const float r = rsqrtf(total / (float)H + eps);
-  uint16_t* yr = y + (size_t)t * H;
-  for (int i = tid; i < H; i += kRowThreads) {
-    const float hs = bf2f(xr[i]) * r;
-    yr[i] = f2bf(w[i] * hs);
-  }
+  rmsnorm_row(x, w, H, eps, y, blockIdx.x);
 }
 
 int launch_rmsnorm(const uint16_t* x, const float* w, int T, int H, float eps, uint16_t* y,

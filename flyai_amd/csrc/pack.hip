@@ -11,7 +11,7 @@ constexpr int kPackMaxSeqs = 8192;
 // Tree verify (tree_depth != NULL, one sequence): token i is rotated at position
 // starts[0] + tree_depth[i] but its K/V goes to slot starts[0] + i; kv_pos receives the slot
 // positions (it is only written in that mode).
-__global__ __launch_bounds__(kPackThreads) void pack_ragged_kernel(
+__device__ __forceinline__ void pack_ragged_body(
     const int32_t* __restrict__ q_lens, const int32_t* __restrict__ starts,
     const int64_t* __restrict__ kv_base, const int32_t* __restrict__ kv_cap, int S, int head_dim,
     int max_tokens, int32_t* __restrict__ cu_out, int32_t* __restrict__ positions,
@@ -79,6 +79,35 @@ __global__ __launch_bounds__(kPackThreads) void pack_ragged_kernel(
   }
 }
 
+__global__ __launch_bounds__(kPackThreads) void pack_ragged_kernel(
+    const int32_t* __restrict__ q_lens, const int32_t* __restrict__ starts,
+    const int64_t* __restrict__ kv_base, const int32_t* __restrict__ kv_cap, int S, int head_dim,
+    int max_tokens, int32_t* __restrict__ cu_out, int32_t* __restrict__ positions,
+    int32_t* __restrict__ seq_id, int32_t* __restrict__ kv_len, int64_t* __restrict__ kv_slot,
+    int32_t* __restrict__ status, const int32_t* __restrict__ tree_depth,
+    int32_t* __restrict__ kv_pos) {
+  pack_ragged_body(q_lens, starts, kv_base, kv_cap, S, head_dim, max_tokens, cu_out, positions, seq_id, kv_len,
+                   kv_slot, status, tree_depth, kv_pos);
+}
+
+// The step's first two launches as one: workgroup 0 packs the batch, workgroups 1..T RMS-normalise
+// the T hidden rows for the first layer (which does not depend on the packing).
+static_assert(kPackThreads == kRowThreads, "one block size for both bodies");
+__global__ __launch_bounds__(kPackThreads) void pack_norm_kernel(
+    const int32_t* __restrict__ q_lens, const int32_t* __restrict__ starts,
+    const int64_t* __restrict__ kv_base, const int32_t* __restrict__ kv_cap, int S, int head_dim,
+    int max_tokens, int32_t* __restrict__ cu_out, int32_t* __restrict__ positions,
+    int32_t* __restrict__ seq_id, int32_t* __restrict__ kv_len, int64_t* __restrict__ kv_slot,
+    int32_t* __restrict__ status, const int32_t* __restrict__ tree_depth,
+    int32_t* __restrict__ kv_pos, const uint16_t* __restrict__ x, const float* __restrict__ w, int H, float eps,
+    uint16_t* __restrict__ y) {
+  if (blockIdx.x == 0)
+    pack_ragged_body(q_lens, starts, kv_base, kv_cap, S, head_dim, max_tokens, cu_out, positions, seq_id, kv_len,
+                     kv_slot, status, tree_depth, kv_pos);
+  else
+    rmsnorm_row(x, w, H, eps, y, blockIdx.x - 1);
+}
+
 }  // namespace flyai
 
 using namespace flyai;
@@ -127,10 +156,19 @@ int launch_blob_fetch(const char* src_dev, char* dst, size_t bytes, hipStream_t 
   return check_launch("blob_fetch");
 }
 
+// The packing, and with norm_rows > 0 the first layer's RMSNorm of norm_rows rows of x in the same
+// launch (pack_norm_kernel).
 int launch_pack(const int32_t* q_lens, const int32_t* starts, const int64_t* kv_base,
                 const int32_t* kv_cap, int S, int head_dim, int max_tokens, int32_t* cu,
                 int32_t* positions, int32_t* seq_id, int32_t* kv_len, int64_t* kv_slot,
-                int32_t* status, const int32_t* tree_depth, int32_t* kv_pos, hipStream_t s) {
+                int32_t* status, const int32_t* tree_depth, int32_t* kv_pos, hipStream_t s,
+                int norm_rows, const uint16_t* x, const float* w, int H, float eps, uint16_t* y) {
+  if (norm_rows > 0) {
+    hipLaunchKernelGGL(pack_norm_kernel, dim3(1 + norm_rows), dim3(kPackThreads), 0, s, q_lens, starts, kv_base,
+                       kv_cap, S, head_dim, max_tokens, cu, positions, seq_id, kv_len, kv_slot, status,
+                       tree_depth, kv_pos, x, w, H, eps, y);
+    return check_launch("pack_norm");
+  }
   hipLaunchKernelGGL(pack_ragged_kernel, dim3(1), dim3(kPackThreads), 0, s, q_lens, starts, kv_base,
                      kv_cap, S, head_dim, max_tokens, cu, positions, seq_id, kv_len, kv_slot, status,
                      tree_depth, kv_pos);

@@ -251,7 +251,7 @@ def committed_traffic(profile, kernels):
 
 def cpu_threads():
     """Intra-op threads for the CPU oracle: every CPU this process may run on (its affinity mask,
-    which is the box's CPU share), unless OMP_NUM_THREADS narrows it."""
+    which is the host's CPU share), unless OMP_NUM_THREADS narrows it."""
     n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
     env = os.environ.get("OMP_NUM_THREADS", "").strip()
     return max(1, min(n, int(env))) if env.isdigit() else n

@@ -197,9 +197,9 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
     lds_barrier();  // the previous pass is done with the LDS rows
     // staging loads go out in batches of kStageBatch per thread (one round trip per batch, not per
     // vector); indices past the end are clamped for the load and not stored.  Batches of 5
-    // measured 4% slower on the C1 step than 4.  The pass's first weight groups are requested right
-    // after the first batch, so the weight stream does not wait for the activation round trip; the
-    // LDS-only barrier below leaves them in flight.
+    // measured 4% slower than 4 on the 9-layer decode step (32 sequences, 56 tokens).  The pass's
+    // first weight groups are requested right after the first batch, so the weight stream does not
+    // wait for the activation round trip; the LDS-only barrier below leaves them in flight.
     constexpr int kStageBatch = 4;
     const int total = rows * row_vecs;
     // (row, vector) of the thread's element b0 + j * 256 + tid, stepped by 256 without an integer
@@ -304,8 +304,8 @@ __global__ __launch_bounds__(256, 3) void moe_mxfp4_kernel(
 // Weight tiles per wave and weight-ring depth (128-K groups) of the decode-sized kernels.  Two tiles
 // and an 8-deep ring keep 14 KiB in flight per wave at 3 waves per SIMD (166 registers), against
 // 9 KiB for 3 tiles and a 4-deep ring (162 registers); the workgroups are also a third smaller, so
-// the end of the launch, where the last workgroups run alone, is shorter.  Measured on the C1 step
-// (9 layers, A/B on one box): 3 tiles x 4 deep 3.13 ms; 2 x 8 3.04 ms; 1 x 8, 2 x 4 and 2 x 12 for
+// the end of the launch, where the last workgroups run alone, is shorter.  Measured on the 9-layer
+// decode step of 32 sequences, 56 tokens (A/B on one box): 3 tiles x 4 deep 3.13 ms; 2 x 8 3.04 ms; 1 x 8, 2 x 4 and 2 x 12 for
 // gate_up and 1 x 8, 1 x 16 and 2 x 12 for down all slower.
 constexpr int kNTWGateUp = 2;
 constexpr int kNTWDown = 2;

@@ -132,8 +132,8 @@ extern "C" int flyai_pack_ragged(const int32_t* q_lens, const int32_t* starts,
 namespace flyai {
 
 // The step's batch blob from the pinned host staging (mapped into the device's address space) into
-// device memory, read by the GPU itself rather than by an H2D copy: on the C1 decode step (87
-// launches) the copy engine's transfer and its hand-over to the compute queue left the GPU idle about
+// device memory, read by the GPU itself rather than by an H2D copy: on a 9-layer decode step of 32
+// sequences (56 tokens, 87 launches) the copy engine's transfer and its hand-over to the compute queue left the GPU idle about
 // 20 us before every step (2.835 -> 2.789 ms per step).  The loads are system-coherent (sc0 sc1), so
 // they fetch what the host wrote for this step, never a cached line of an earlier one; offsets past
 // the blob read zero and are not stored.

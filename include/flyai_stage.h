@@ -289,8 +289,8 @@ int flyai_attn_ragged(const uint16_t* q, const uint16_t* k_pool, const uint16_t*
                       const flyai_attn_group* groups_dev, int32_t n_groups, float* partials,
                       uint16_t* out, flyai_stream_t stream);
 
-/* Chunked-prefill rows (SURVEY next item: chunked-prefill attention on device, replacing the flex
- * prefill of phase0/fastverify.py:138-155).  flyai_attn_plan_prefill is flyai_attn_plan with every
+/* Chunked-prefill rows (chunked-prefill attention on device, replacing the flex prefill of
+ * phase0/fastverify.py:138-155).  flyai_attn_plan_prefill is flyai_attn_plan with every
  * sequence of q_len >= prefill_min (0: none) moved to prefill items instead: 16 consecutive query tokens
  * x one kv head per item (ntok <= 16, key range [key_lo, key_hi) = the tiles' window start .. last
  * position + 1, group -1), the chunk's last tiles first.  flyai_attn_prefill runs them: a workgroup of

@@ -1,6 +1,6 @@
 """CPU oracle for one GPT-OSS-120B-shaped (and DeepSeek-V3-shaped) MoE pipeline-stage step.
 
-TEST INFRASTRUCTURE ONLY.  This package is the checker, never the product:
+TEST INFRASTRUCTURE ONLY.  This package is the test oracle, never the product:
 only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
 import it.  Nothing under ``flyai_amd/`` imports it, and the product path has no CPU fallback.
 

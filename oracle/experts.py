@@ -15,7 +15,7 @@ left to a kernel is fp32 accumulation order.  Parity: fp64 brute force on tiny s
 SwiGLU at the clamp boundaries (+-7, 0); transformers fixture (eager GptOssExperts on the
 dequantised weights) in tests/golden.
 
-DeepSeek FP8 (config C3), following the vendored V4 model (``vendor/deepseek_v4_ref/inference/
+DeepSeek FP8 (the 4-layer, 155-token DeepSeek-V3-shaped stage), following the vendored V4 model (``vendor/deepseek_v4_ref/inference/
 model.py:592-611`` Expert, ``:634-650`` MoE) and its GEMM semantics (``vendor/deepseek_v4_ref/
 inference/kernel.py:204-254`` fp8_gemm; CPU transcription ``engines/deepseek_v4/v4_kernels_cpu.py:
 67-104`` act_quant with power-of-two scale, ``:158-164`` fp8_gemm):

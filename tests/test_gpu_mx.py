@@ -5,7 +5,7 @@
   scale layout, padding bytes 127.
 * gate_up / down with the fp8 activation operand: against oracle.experts_mxfp4_fp8act, which carries
   the same two-term operands through an fp32 product (the bar: fp32 accumulation order and bf16
-  rounding of h only), and against the bf16 model math (experts_mxfp4) at the north_star bar
+  rounding of h only), and against the bf16 model math (experts_mxfp4) at the path's accuracy bar
   (max-abs-rel 2e-2, cosine 0.999; the two terms hold the bf16 operand to 2^-6 of each block's largest
   value, so the measured agreement is far inside it).  Groups of 8 rows or fewer keep the bf16 row-pass
   kernel, so a decode-sized batch gives the bf16 path's exact bits."""
@@ -116,7 +116,7 @@ def test_moe_experts_fp8act_vs_oracle(T, E, hot):
     assert mar <= 1e-2 and cos >= 0.99999, f"gate_up vs the fp8-activation oracle: {mar:.3g} {cos:.7f}"
     mar, cos = _metrics(yd, ry.numpy()[dense])
     assert mar <= 1e-2 and cos >= 0.99999, f"down vs the fp8-activation oracle: {mar:.3g} {cos:.7f}"
-    # against the bf16 model math: the north_star bar on the expert outputs themselves
+    # against the bf16 model math: the accuracy bar on the expert outputs themselves
     mar, cos = _metrics(hd, rh16.numpy()[dense])
     print(f"T={T} E={E}: gate_up vs bf16 math max-abs-rel {mar:.3g} cos {cos:.7f}")
     assert mar <= 2e-2 and cos >= 0.999, f"gate_up vs the bf16 model math: {mar:.3g} {cos:.6f}"

@@ -1,5 +1,5 @@
 """Host logic of the continuous-batch backend (no GPU): the contract passes the reference's own
-admission rules (shard/continuous_batch.py:18-48, restated here as the checker), and advance_batch
+admission rules (shard/continuous_batch.py:18-48, restated here as the expected answers), and advance_batch
 keeps the per-job semantics RingPool.execute_batch_step / ContinuousRingWorker rely on
 (shard/ring_pool.py:627-700, shard/continuous_batch.py:98-156).  The model is a deterministic fake
 with the GptOssModel.step signature."""
